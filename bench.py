@@ -1,0 +1,340 @@
+"""Benchmark of the MI355X picograd backward path (one GPU).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only c2,c3,c1,c5]
+
+Headline (the JSON `value`): config 2 of BASELINE.json -- the fused
+broadcasting elementwise backward of y = gelu(x + bias) * sigmoid(g),
+x, g f32 [16384, 4096], bias [4096], loss = sum_all(y).  One step is one
+pg_backward() over the resident graph: the fused kernel reads x, g and bias
+and writes dx, dg and dbias (the column sum over 16384 rows) in one pass.
+value = algorithmic bytes (16 B/element + 32 KiB) / measured step time.
+
+Also reported in `extra`: config 3 (bf16 dgrad + wgrad, TFLOP/s), config 1
+(the [64, 64] chain, µs per iteration of leaves + forward + backward) and
+config 5 when the MLP step is available.
+
+Timing: HIP events on the library stream around K steps (after W warmup
+steps, with stream synchronisation on both sides); per-kernel durations
+come from the library's kernel timer (HIP events around each launch of
+the dominant kernel on the same stream).  The CPU baseline is the
+reference's own CPU path (oracle/_ref, built from the reference sources)
+timed on this host over a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+sys.path.insert(0, str(ROOT / "tests"))
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0  # dense MFMA, MI355X
+T_JIT_MAIN, T_JIT_FIN, T_GEMM16, T_SGD, T_STAGE = 0, 1, 2, 3, 4
+
+
+class HipEvents:
+    """hipEvent timing on an explicit stream (the library stream)."""
+
+    def __init__(self, stream: int):
+        self.hip = C.CDLL("libamdhip64.so")
+        self.stream = C.c_void_p(stream)
+        for fn, args in (("hipEventCreate", [C.POINTER(C.c_void_p)]),
+                         ("hipEventRecord", [C.c_void_p, C.c_void_p]),
+                         ("hipEventSynchronize", [C.c_void_p]),
+                         ("hipEventElapsedTime", [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]),
+                         ("hipEventDestroy", [C.c_void_p])):
+            getattr(self.hip, fn).argtypes = args
+            getattr(self.hip, fn).restype = C.c_int
+
+    def time(self, fn, steps: int) -> float:
+        a, b = C.c_void_p(), C.c_void_p()
+        self.hip.hipEventCreate(C.byref(a))
+        self.hip.hipEventCreate(C.byref(b))
+        self.hip.hipEventRecord(a, self.stream)
+        for _ in range(steps):
+            fn()
+        self.hip.hipEventRecord(b, self.stream)
+        self.hip.hipEventSynchronize(b)
+        ms = C.c_float()
+        self.hip.hipEventElapsedTime(C.byref(ms), a, b)
+        self.hip.hipEventDestroy(a)
+        self.hip.hipEventDestroy(b)
+        return ms.value
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def timer_ms(lib, kind):
+    cnt = C.c_size_t()
+    total = lib.pg_amd_timer_read(kind, C.byref(cnt))
+    return total, cnt.value
+
+
+# ---------------------------------------------------------------- config 2
+
+def c2_inputs(R, Cc, seed=43):
+    from oracle_lib import Oracle
+    o = Oracle()
+    o.orc_seed(seed)
+    x = o.normal(R * Cc, 0.0, 1.0).reshape(R, Cc)
+    bias = o.normal(Cc, 0.0, 0.1)
+    g = o.normal(R * Cc, 0.0, 1.0).reshape(R, Cc)
+    return x, bias, g
+
+
+def c2_graph(L, x, bias, g):
+    nx, nb, ng = L.var(x), L.var(bias), L.var(g)
+    t0 = L.op("add", nx, nb)
+    t1 = L.op("gelu", t0)
+    t2 = L.op("sigmoid", ng)
+    y = L.op("mul", t1, t2)
+    loss = L.op("sum_all", y)
+    return loss, [loss, y, t2, t1, t0, nx, nb, ng]
+
+
+def bench_c2(L, ev, steps, warmup, R=16384, Cc=4096):
+    log(f"[c2] inputs {R}x{Cc}")
+    x, bias, g = c2_inputs(R, Cc)
+    loss, nodes = c2_graph(L, x, bias, g)
+    del x, g
+    L.sync()
+    step = lambda: L.pg_backward(loss)
+    for _ in range(warmup):
+        step()
+    L.sync()
+    assert L.pg_autograd_last_was_jit(), L.pg_autograd_last_error().decode()
+    L.pg_amd_timer_reset()
+    L.pg_amd_timer_enable(1)
+    ms = ev.time(step, steps)
+    L.pg_amd_timer_enable(0)
+    main_ms, main_n = timer_ms(L, T_JIT_MAIN)
+    fin_ms, fin_n = timer_ms(L, T_JIT_FIN)
+    L.pg_amd_timer_reset()
+    # untimed re-run without the timer events for the step time
+    ms = ev.time(step, steps)
+    nbytes = 16 * R * Cc + 8 * Cc  # read x, g; write dx, dg (+ bias in, dbias out)
+    step_ms = ms / steps
+    kern_ms = main_ms / max(main_n, 1)
+    for n in nodes:
+        L.pg_node_free(n)
+    L.sync()
+    return {
+        "step_ms": step_ms,
+        "gbs": nbytes / (step_ms * 1e-3) / 1e9,
+        "kernel_ms": kern_ms,
+        "kernel_gbs": nbytes / (kern_ms * 1e-3) / 1e9,
+        "fin_ms": fin_ms / max(fin_n, 1),
+        "bytes": nbytes,
+        "launches": main_n,
+    }
+
+
+def cpu_c2(rows=2048, Cc=4096, budget_s=20.0):
+    """The reference CPU path (oracle/_ref) on a row sample of config 2."""
+    from oracle_lib import REF_SO
+    from picograd_amd.capi import PgLib
+    if not REF_SO.exists():
+        return None
+    R = PgLib(REF_SO, device=False)
+    x, bias, g = c2_inputs(rows, Cc)
+    loss, nodes = c2_graph(R, x, bias, g)
+    t0 = time.perf_counter()
+    R.pg_backward(loss)  # warmup: absorbs the reference JIT's compile
+    times = []
+    while len(times) < 5 and time.perf_counter() - t0 < budget_s:
+        s = time.perf_counter()
+        R.pg_backward(loss)
+        times.append(time.perf_counter() - s)
+    for n in nodes:
+        R.pg_node_free(n)
+    t = float(np.median(times))
+    nbytes = 16 * rows * Cc + 8 * Cc
+    threads = int(os.environ.get("PICOGRAD_THREADS", min(os.cpu_count() or 1, 64)))
+    return {"value": nbytes / t / 1e9, "unit": "GB/s", "cores": threads, "kind": "reference",
+            "sample": f"config 2 at [{rows},{Cc}] (of [16384,{Cc}]), reference pg_backward "
+                      f"(hybrid JIT + eager, the pool capped at 64 threads; the JIT loop, "
+                      f"GELU' and dbias loops are single-threaded), median of {len(times)}",
+            "ms_per_step": t * 1e3}
+
+
+# ---------------------------------------------------------------- config 3
+
+def bench_c3(L, ev, steps, warmup, M=8192, K=4096, N=4096):
+    from oracle_lib import Oracle
+    from picograd_amd.capi import BF16
+    log(f"[c3] A {M}x{K}, W {K}x{N}")
+    o = Oracle()
+    o.orc_seed(44)
+    a16 = o.cast16(BF16, o.normal(M * K, 0.0, 1.0).reshape(M, K))
+    w16 = o.cast16(BF16, o.normal(K * N, 0.0, 0.02).reshape(K, N))
+    dc = o.normal(M * N, 0.0, 1.0).reshape(M, N)
+    na, nw = L.var(a16, dtype=BF16), L.var(w16, dtype=BF16)
+    c = L.op("matmul", na, nw)
+    seed = L.tensor(dc)
+    del a16, w16, dc
+    L.sync()
+    step = lambda: L.pg_amd_backward_from(c, seed)
+    for _ in range(warmup):
+        step()
+    L.sync()
+    L.pg_amd_timer_reset()
+    L.pg_amd_timer_enable(1)
+    ev.time(step, steps)
+    L.pg_amd_timer_enable(0)
+    g_ms, g_n = timer_ms(L, T_GEMM16)
+    L.pg_amd_timer_reset()
+    ms = ev.time(step, steps)
+    flops = 2 * 2 * M * N * K
+    step_ms = ms / steps
+    kern_ms = g_ms / max(g_n, 1)
+    L.pg_tensor_free(seed)
+    for n in (c, na, nw):
+        L.pg_node_free(n)
+    L.sync()
+    return {"step_ms": step_ms, "tflops": flops / (step_ms * 1e-3) / 1e12,
+            "gemm_ms": kern_ms, "gemm_tflops": (flops / 2) / (kern_ms * 1e-3) / 1e12,
+            "flops": flops, "gemm_launches": g_n}
+
+
+def cpu_c3(M=1024, K=4096, N=4096, budget_s=20.0):
+    """Reference bwd_matmul (bf16 upcast + transpose + f32 sgemm) on a row
+    sample of config 3."""
+    from oracle_lib import REF_SO, Oracle
+    from picograd_amd.capi import BF16, PgLib
+    if not REF_SO.exists():
+        return None
+    R = PgLib(REF_SO, device=False)
+    o = Oracle()
+    o.orc_seed(44)
+    a16 = o.cast16(BF16, o.normal(M * K, 0.0, 1.0).reshape(M, K))
+    w16 = o.cast16(BF16, o.normal(K * N, 0.0, 0.02).reshape(K, N))
+    w = o.normal(M * N, 0.0, 1.0).reshape(M, N)
+    na, nw = R.var(a16, dtype=BF16), R.var(w16, dtype=BF16)
+    c = R.op("matmul", na, nw)
+    gw = R.var(w, requires_grad=False)
+    prod = R.op("mul", c, gw)
+    loss = R.op("sum_all", prod)
+    R.pg_autograd_set_jit(False)
+    t0 = time.perf_counter()
+    times = []
+    while len(times) < 3 and time.perf_counter() - t0 < budget_s:
+        s = time.perf_counter()
+        R.pg_backward(loss)
+        times.append(time.perf_counter() - s)
+    R.pg_autograd_set_jit(True)
+    for n in (loss, prod, gw, c, na, nw):
+        R.pg_node_free(n)
+    t = float(np.median(times))
+    flops = 2 * 2 * M * N * K
+    return {"value": flops / t / 1e12, "unit": "TFLOP/s", "sample": f"M={M} of 8192", "ms": t * 1e3}
+
+
+# ---------------------------------------------------------------- config 1
+
+def bench_c1(L, iters=2000):
+    from oracle_lib import Oracle
+    o = Oracle()
+    o.orc_seed(42)
+    a, b, c = (o.uniform(4096, -1.0, 1.0).reshape(64, 64) for _ in range(3))
+    shp = (C.c_size_t * 2)(64, 64)
+
+    def one():
+        na = L.pg_var_from_data(2, shp, a.ctypes.data, True)
+        nb = L.pg_var_from_data(2, shp, b.ctypes.data, True)
+        nc = L.pg_var_from_data(2, shp, c.ctypes.data, True)
+        t0 = L.pg_ag_add(na, nb)
+        t1 = L.pg_ag_mul(t0, nc)
+        t2 = L.pg_ag_relu(t1)
+        t3 = L.pg_ag_tanh(t2)
+        loss = L.pg_ag_sum_all(t3)
+        L.pg_backward(loss)
+        for n in (loss, t3, t2, t1, t0, na, nb, nc):
+            L.pg_node_free(n)
+
+    for _ in range(20):
+        one()
+    L.sync()
+    s = time.perf_counter()
+    for _ in range(iters):
+        one()
+    L.sync()
+    return {"us_per_iter": (time.perf_counter() - s) / iters * 1e6, "iters": iters,
+            "reference_cpu_us_per_iter": 114.0}
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", default="c2,c3,c1")
+    a = ap.parse_args(argv)
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU only (every box here has one); --gpus {a.gpus} is not supported",
+              file=sys.stderr)
+        return 2
+    import picograd_amd
+    L = picograd_amd.load()
+    if L.pg_amd_init() != 0:
+        raise SystemExit(f"no device: {L.pg_amd_last_error().decode()}")
+    ev = HipEvents(L.pg_amd_stream())
+    only = set(a.only.split(","))
+    extra = {}
+    c2 = bench_c2(L, ev, a.steps, a.warmup)
+    log(f"[c2] {c2}")
+    if "c3" in only:
+        extra["c3_bf16_dgrad_wgrad"] = bench_c3(L, ev, max(3, a.steps // 2), a.warmup)
+        log(f"[c3] {extra['c3_bf16_dgrad_wgrad']}")
+    if "c1" in only:
+        extra["c1_chain_64x64"] = bench_c1(L)
+        log(f"[c1] {extra['c1_chain_64x64']}")
+    cpu = None
+    if not a.no_cpu:
+        log("[cpu] reference CPU path, config 2 sample")
+        cpu = cpu_c2()
+        if "c3" in only and cpu is not None:
+            log("[cpu] reference CPU path, config 3 sample")
+            c3cpu = cpu_c3()
+            if c3cpu:
+                extra.setdefault("c3_bf16_dgrad_wgrad", {})["cpu_reference"] = c3cpu
+    out = {
+        "metric": "fused-bwd HBM GB/s",
+        "value": round(c2["gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(c2["step_ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (splitmix64 seed 43, the reference's RNG)",
+        "config": {"workload": "config 2: fused broadcasting elementwise backward, "
+                               "y = gelu(x + bias) * sigmoid(g), x, g f32 [16384, 4096], bias [4096]",
+                   "rows": 16384, "cols": 4096},
+        "roofline": {"bound": "hbm", "achieved": round(c2["kernel_gbs"], 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(c2["kernel_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "pgjit_main (fused backward)", "kernel_ms": round(c2["kernel_ms"], 5),
+                     "finisher_ms": round(c2["fin_ms"], 5)},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

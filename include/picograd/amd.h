@@ -1,0 +1,58 @@
+/*
+ * MI355X-specific entry points of picograd-amd.  None has a counterpart in
+ * the reference; they expose what a device-resident backend adds: the
+ * stream all work is queued on, explicit synchronisation, allocator state
+ * and backward seeded with an explicit upstream gradient.
+ */
+#ifndef PICOGRAD_AMD_H
+#define PICOGRAD_AMD_H
+
+#include <stdbool.h>
+#include <stddef.h>
+
+#include "autograd.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Selects the device and creates the library stream.  Idempotent; every
+ * other entry point calls it.  Returns 0 on success. */
+int pg_amd_init(void);
+/* The hipStream_t (as void*) every kernel of the library is launched on. */
+void *pg_amd_stream(void);
+/* Waits for all queued work.  Returns 0 on success. */
+int pg_amd_sync(void);
+/* Last device-layer error message ("" if none). */
+const char *pg_amd_last_error(void);
+/* Bytes held by live tensors / kept in the allocator's free lists. */
+size_t pg_amd_bytes_in_use(void);
+size_t pg_amd_bytes_cached(void);
+/* Returns cached device blocks to the driver (waits for the stream). */
+void pg_amd_release_cached(void);
+
+/* pg_backward() with the root's upstream gradient given explicitly instead
+ * of 1 (like torch's backward(gradient)).  seed must have the root value's
+ * shape, f32; it is read, not kept, and must stay valid until the stream has
+ * run the backward.  The fused loss-suffix JIT does not apply here. */
+void pg_amd_backward_from(pg_node *root, const pg_tensor *seed);
+
+/* JIT compile statistics: programs compiled by hiprtc, and cache lookups
+ * that found a loaded kernel. */
+size_t pg_amd_jit_compiles(void);
+size_t pg_amd_jit_cache_hits(void);
+
+/* Kernel timer: while enabled, the fused backward kernel (kind 0), its
+ * reduction finisher (1), the MFMA GEMMs (2), the SGD kernel (3) and the
+ * GEMM operand staging (4) are bracketed by HIP events on the library
+ * stream.  pg_amd_timer_read waits for the stream and returns the summed
+ * milliseconds of one kind (and the number of launches). */
+void pg_amd_timer_enable(int on);
+double pg_amd_timer_read(int kind, size_t *count);
+void pg_amd_timer_reset(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,34 @@
+/*
+ * GEMM entry points of the reference's backend/backend.h:118-136, with
+ * device pointers.  Contract kept: row-major, leading dimensions in
+ * elements, C overwritten (beta = 0), A and B as uint16_t for F16/BF16, C
+ * f32 accumulated in f32.  a, b and c are device addresses (for example
+ * pg_tensor.dev); the call is enqueued on the library stream.
+ * pg_gemm (f32 x f32) is also device-side.
+ */
+#ifndef PICOGRAD_BACKEND_H
+#define PICOGRAD_BACKEND_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "dtype.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+void pg_gemm(size_t m, size_t n, size_t k, const float *a, size_t lda, const float *b, size_t ldb,
+             float *c, size_t ldc);
+void pg_gemm_ex(pg_dtype dtype, size_t m, size_t n, size_t k, const void *a, size_t lda,
+                const void *b, size_t ldb, float *c, size_t ldc);
+void pg_hgemm(size_t m, size_t n, size_t k, const uint16_t *a, size_t lda, const uint16_t *b,
+              size_t ldb, float *c, size_t ldc);
+void pg_bgemm(size_t m, size_t n, size_t k, const uint16_t *a, size_t lda, const uint16_t *b,
+              size_t ldb, float *c, size_t ldc);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

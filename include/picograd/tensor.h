@@ -1,0 +1,109 @@
+/*
+ * pg_tensor: the reference's tensor ABI (core/tensor.h:15-96) with the
+ * storage moved to MI355X HBM.
+ *
+ * The leading fields keep the reference layout so existing callers compile
+ * unchanged.  What differs:
+ *   - the elements live in device memory at `dev`; `data` is a host mirror
+ *     that is NULL until pg_tensor_sync_host() fills it, and is stale after
+ *     any later device write until the next pg_tensor_sync_host();
+ *   - a caller that edits the host mirror pushes it back with
+ *     pg_tensor_sync_device();
+ *   - every constructor and op enqueues its device work on the library
+ *     stream (pg_amd_stream()) and returns without waiting for it.
+ */
+#ifndef PICOGRAD_TENSOR_H
+#define PICOGRAD_TENSOR_H
+
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdio.h>
+
+#include "dtype.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PG_MAX_NDIM 8
+
+typedef struct pg_data_ref {
+    void *ptr;     /* device allocation */
+    size_t nbytes;
+    int refs;
+} pg_data_ref;
+
+typedef struct pg_tensor {
+    size_t ndim;
+    size_t shape[PG_MAX_NDIM];
+    size_t stride[PG_MAX_NDIM];
+    size_t numel;
+    union {
+        float *data;        /* host mirror, f32 view */
+        void *data_raw;
+        uint16_t *data_u16; /* host mirror, f16/bf16 view */
+    };
+    pg_data_ref *data_ref;
+    bool is_view;
+    struct pg_tensor *view_parent;
+    pg_dtype dtype;
+    size_t elem_size;
+    /* ---- appended: device residency ---- */
+    void *dev;          /* device address of element 0 */
+    unsigned pg_flags;  /* PG_TENSOR_* bits, library-internal */
+} pg_tensor;
+
+/* constructors: tensor.h:38-58 of the reference */
+pg_tensor *pg_tensor_new_dtype(pg_dtype dtype, size_t ndim, const size_t *shape);
+pg_tensor *pg_tensor_empty_dtype(pg_dtype dtype, size_t ndim, const size_t *shape);
+pg_tensor *pg_tensor_from_data_dtype(pg_dtype dtype, size_t ndim, const size_t *shape, const void *data);
+pg_tensor *pg_tensor_zeros_dtype(pg_dtype dtype, size_t ndim, const size_t *shape);
+pg_tensor *pg_tensor_ones_dtype(pg_dtype dtype, size_t ndim, const size_t *shape);
+pg_tensor *pg_tensor_full_dtype(pg_dtype dtype, size_t ndim, const size_t *shape, float value);
+
+pg_tensor *pg_tensor_new(size_t ndim, const size_t *shape);
+pg_tensor *pg_tensor_empty(size_t ndim, const size_t *shape);
+pg_tensor *pg_tensor_zeros(size_t ndim, const size_t *shape);
+pg_tensor *pg_tensor_ones(size_t ndim, const size_t *shape);
+pg_tensor *pg_tensor_full(size_t ndim, const size_t *shape, float value);
+pg_tensor *pg_tensor_from_data(size_t ndim, const size_t *shape, const float *data);
+pg_tensor *pg_tensor_uniform(size_t ndim, const size_t *shape, float low, float high);
+pg_tensor *pg_tensor_normal(size_t ndim, const size_t *shape, float mean, float stddev);
+
+pg_tensor *pg_tensor_clone(const pg_tensor *t);
+void pg_tensor_free(pg_tensor *t);
+
+static inline float *pg_tensor_f32(const pg_tensor *t) { return (float *)t->data_raw; }
+static inline uint16_t *pg_tensor_f16(const pg_tensor *t) { return (uint16_t *)t->data_raw; }
+static inline uint16_t *pg_tensor_bf16(const pg_tensor *t) { return (uint16_t *)t->data_raw; }
+static inline size_t pg_tensor_nbytes(const pg_tensor *t) { return t->numel * t->elem_size; }
+
+/* splitmix64 stream shared by pg_tensor_uniform/normal (tensor.c:289-339) */
+void pg_seed(unsigned long long seed);
+
+void pg_tensor_fill(pg_tensor *t, float value);
+void pg_tensor_copy_from(pg_tensor *dst, const pg_tensor *src);
+bool pg_tensor_reshape(pg_tensor *t, size_t ndim, const size_t *shape);
+
+size_t pg_shape_numel(size_t ndim, const size_t *shape);
+bool pg_shape_equal(size_t ndim_a, const size_t *shape_a, size_t ndim_b, const size_t *shape_b);
+
+pg_tensor *pg_tensor_view(const pg_tensor *src);
+pg_tensor *pg_tensor_reshape_view(const pg_tensor *src, size_t ndim, const size_t *shape);
+
+/* ---- appended: host/device synchronisation ---- */
+/* Waits for queued device work, then copies the elements into the host
+ * mirror t->data (allocated on first use).  Returns false on failure. */
+bool pg_tensor_sync_host(pg_tensor *t);
+/* Copies the host mirror back to device memory (after a caller edited it). */
+bool pg_tensor_sync_device(pg_tensor *t);
+/* Copies numel*elem_size bytes of device data into dst (waits first). */
+bool pg_tensor_copy_to_host(const pg_tensor *t, void *dst);
+/* Copies numel*elem_size bytes from src into device data (enqueued). */
+bool pg_tensor_copy_from_host(pg_tensor *t, const void *src);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

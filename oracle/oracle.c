@@ -1,0 +1,375 @@
+/*
+ * CPU oracle for the picograd backward path -- TEST INFRASTRUCTURE ONLY.
+ * Loaded only by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+ * leg, as the checker.  The product library never uses it.
+ * Each function restates the reference algorithm at the cited file:line.
+ */
+#define _POSIX_C_SOURCE 200809L
+#include "oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ---------------- RNG (tensor.c:289-339) ---------------- */
+
+static unsigned long long g_state = 0x9E3779B97F4A7C15ULL;
+
+void orc_seed(unsigned long long seed)
+{
+    /* tensor.c:292-297: a zero seed selects the default state */
+    g_state = seed != 0 ? seed : 0x9E3779B97F4A7C15ULL;
+}
+
+static unsigned long long orc_next(void)
+{
+    /* splitmix64 finaliser, tensor.c:299-309 */
+    g_state += 0x9E3779B97F4A7C15ULL;
+    unsigned long long z = g_state;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+    return z ^ (z >> 31);
+}
+
+static float orc_u01(void)
+{
+    /* top 24 bits scaled to [0,1), tensor.c:311-314 */
+    return (float)(orc_next() >> 40) * (1.0f / 16777216.0f);
+}
+
+void orc_uniform(float *out, size_t n, float low, float high)
+{
+    /* tensor.c:316-323 */
+    for (size_t i = 0; i < n; i++) {
+        out[i] = low + orc_u01() * (high - low);
+    }
+}
+
+void orc_normal(float *out, size_t n, float mean, float stddev)
+{
+    /* Box-Muller, cosine branch only, one pair of draws per element
+     * (tensor.c:325-339) */
+    for (size_t i = 0; i < n; i++) {
+        float u1 = orc_u01();
+        float u2 = orc_u01();
+        if (u1 < 1e-12f)
+            u1 = 1e-12f;
+        float mag = stddev * sqrtf(-2.0f * logf(u1));
+        out[i] = mean + mag * cosf(2.0f * 3.14159265358979f * u2);
+    }
+}
+
+/* ---------------- conversions (convert.h:15-104) ---------------- */
+
+uint16_t orc_f32_to_f16(float f)
+{
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t ex = (x >> 23) & 0xFFu;
+    uint32_t man = x & 0x7FFFFFu;
+    if (ex == 255) {
+        /* Inf stays Inf; NaN keeps the top payload bits and is quieted
+         * (convert.h:22-28) */
+        if (man == 0)
+            return (uint16_t)(sign | 0x7C00u);
+        uint16_t q = (uint16_t)(sign | 0x7C00u | (man >> 13));
+        if ((q & 0x3FFu) == 0)
+            q |= 1u;
+        return (uint16_t)(q | 0x200u);
+    }
+    int32_t e = (int32_t)ex - 112; /* rebias 127 -> 15 */
+    if (e >= 31)
+        return (uint16_t)(sign | 0x7C00u);
+    if (e <= 0) {
+        /* subnormal result; below 2^-25 it flushes to signed zero
+         * (convert.h:31-43) */
+        if (e < -10)
+            return (uint16_t)sign;
+        man |= 0x800000u;
+        uint32_t sh = (uint32_t)(1 - e) + 13u;
+        uint32_t keep = man >> sh;
+        uint32_t rem = man & ((1u << sh) - 1u);
+        uint32_t half = 1u << (sh - 1u);
+        if (rem > half || (rem == half && (keep & 1u)))
+            keep++;
+        return (uint16_t)(sign | keep);
+    }
+    /* normal: round the 13 dropped bits to nearest even; a carry out of the
+     * mantissa bumps the exponent (convert.h:45-51) */
+    uint32_t r = man + 0xFFFu + ((man >> 13) & 1u);
+    if (r & 0x800000u) {
+        r = 0;
+        e++;
+    }
+    if (e >= 31)
+        return (uint16_t)(sign | 0x7C00u);
+    return (uint16_t)(sign | ((uint32_t)e << 10) | (r >> 13));
+}
+
+float orc_f16_to_f32(uint16_t h)
+{
+    uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+    uint32_t ex = ((uint32_t)h >> 10) & 0x1Fu;
+    uint32_t man = (uint32_t)h & 0x3FFu;
+    uint32_t bits;
+    if (ex == 0) {
+        if (man == 0) {
+            bits = sign;
+        } else {
+            /* renormalise a subnormal (convert.h:60-69) */
+            int32_t e = 1;
+            while ((man & 0x400u) == 0) {
+                man <<= 1;
+                e--;
+            }
+            man &= 0x3FFu;
+            bits = sign | ((uint32_t)(e + 112) << 23) | (man << 13);
+        }
+    } else if (ex == 31) {
+        bits = sign | 0x7F800000u | (man << 13);
+    } else {
+        bits = sign | ((ex + 112u) << 23) | (man << 13);
+    }
+    float out;
+    memcpy(&out, &bits, 4);
+    return out;
+}
+
+uint16_t orc_f32_to_bf16(float f)
+{
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    /* a NaN becomes a positive quiet NaN keeping only bit 16 of the input
+     * (the sign is dropped: convert.h:89-92) */
+    if ((x & 0x7F800000u) == 0x7F800000u && (x & 0x7FFFFFu) != 0)
+        return (uint16_t)(0x7FC0u | ((x >> 16) & 1u));
+    return (uint16_t)((x + 0x7FFFu + ((x >> 16) & 1u)) >> 16);
+}
+
+float orc_bf16_to_f32(uint16_t h)
+{
+    uint32_t bits = (uint32_t)h << 16;
+    float out;
+    memcpy(&out, &bits, 4);
+    return out;
+}
+
+void orc_cast_f32(int dtype, const float *src, uint16_t *dst, size_t n)
+{
+    for (size_t i = 0; i < n; i++)
+        dst[i] = dtype == ORC_F16 ? orc_f32_to_f16(src[i]) : orc_f32_to_bf16(src[i]);
+}
+
+void orc_round_f32(int dtype, float *x, size_t n)
+{
+    if (dtype == ORC_F32)
+        return;
+    for (size_t i = 0; i < n; i++)
+        x[i] = dtype == ORC_F16 ? orc_f16_to_f32(orc_f32_to_f16(x[i]))
+                                : orc_bf16_to_f32(orc_f32_to_bf16(x[i]));
+}
+
+/* ---------------- SGD (sgd.c:111-162) ---------------- */
+
+void orc_sgd_step(float *p, const float *g, float *buf, size_t n, float lr,
+                  float momentum, float dampening, float weight_decay,
+                  bool nesterov)
+{
+    for (size_t j = 0; j < n; j++) {
+        float gj = g[j];
+        if (weight_decay != 0.0f)
+            gj += weight_decay * p[j]; /* decay joins the grad first */
+        float u = gj;
+        if (momentum != 0.0f) {
+            /* buffer starts at zero, so step 1 gives (1-d)*g (sgd.c:134-156) */
+            buf[j] = buf[j] * momentum + gj * (1.0f - dampening);
+            u = nesterov ? gj + momentum * buf[j] : buf[j];
+        }
+        p[j] -= lr * u;
+    }
+}
+
+/* ---------------- GEMM with f32 accumulation ---------------- */
+
+typedef struct {
+    int dtype, ta, tb, beta, f64;
+    size_t m, n, k, lda, ldb, ldc;
+    const void *a, *b;
+    void *c;
+    size_t r0, r1;
+} gemm_job;
+
+static inline float ld_elem(int dtype, const void *p, size_t idx)
+{
+    if (dtype == ORC_F32)
+        return ((const float *)p)[idx];
+    uint16_t h = ((const uint16_t *)p)[idx];
+    return dtype == ORC_F16 ? orc_f16_to_f32(h) : orc_bf16_to_f32(h);
+}
+
+static void *gemm_worker(void *arg)
+{
+    gemm_job *j = arg;
+    float *arow = malloc(j->k * sizeof(float));
+    float *bcol = malloc(j->k * sizeof(float) * 16);
+    for (size_t jb = 0; jb < j->n; jb += 16) {
+        size_t nj = j->n - jb < 16 ? j->n - jb : 16;
+        /* gather 16 columns of B, upcast once */
+        for (size_t q = 0; q < nj; q++)
+            for (size_t p = 0; p < j->k; p++) {
+                size_t idx = j->tb ? (jb + q) * j->ldb + p : p * j->ldb + jb + q;
+                bcol[q * j->k + p] = ld_elem(j->dtype, j->b, idx);
+            }
+        for (size_t i = j->r0; i < j->r1; i++) {
+            for (size_t p = 0; p < j->k; p++) {
+                size_t idx = j->ta ? p * j->lda + i : i * j->lda + p;
+                arow[p] = ld_elem(j->dtype, j->a, idx);
+            }
+            for (size_t q = 0; q < nj; q++) {
+                const float *bc = bcol + q * j->k;
+                if (j->f64) {
+                    double acc = 0.0;
+                    for (size_t p = 0; p < j->k; p++)
+                        acc += (double)arow[p] * (double)bc[p];
+                    ((double *)j->c)[i * j->ldc + jb + q] = acc;
+                } else {
+                    float acc = 0.0f;
+                    for (size_t p = 0; p < j->k; p++)
+                        acc += arow[p] * bc[p];
+                    float *cp = (float *)j->c + i * j->ldc + jb + q;
+                    *cp = j->beta ? *cp + acc : acc;
+                }
+            }
+        }
+    }
+    free(arow);
+    free(bcol);
+    return NULL;
+}
+
+static void gemm_run(int dtype, int ta, int tb, size_t m, size_t n, size_t k,
+                     const void *a, size_t lda, const void *b, size_t ldb,
+                     void *c, size_t ldc, int beta, int f64, int nthreads)
+{
+    if (nthreads < 1)
+        nthreads = 1;
+    if ((size_t)nthreads > m)
+        nthreads = m ? (int)m : 1;
+    gemm_job *jobs = calloc((size_t)nthreads, sizeof(gemm_job));
+    pthread_t *th = calloc((size_t)nthreads, sizeof(pthread_t));
+    size_t per = (m + (size_t)nthreads - 1) / (size_t)nthreads;
+    for (int t = 0; t < nthreads; t++) {
+        gemm_job *j = &jobs[t];
+        j->dtype = dtype; j->ta = ta; j->tb = tb; j->beta = beta; j->f64 = f64;
+        j->m = m; j->n = n; j->k = k; j->lda = lda; j->ldb = ldb; j->ldc = ldc;
+        j->a = a; j->b = b; j->c = c;
+        j->r0 = (size_t)t * per < m ? (size_t)t * per : m;
+        j->r1 = j->r0 + per < m ? j->r0 + per : m;
+    }
+    for (int t = 1; t < nthreads; t++)
+        pthread_create(&th[t], NULL, gemm_worker, &jobs[t]);
+    gemm_worker(&jobs[0]);
+    for (int t = 1; t < nthreads; t++)
+        pthread_join(th[t], NULL);
+    free(jobs);
+    free(th);
+}
+
+void orc_gemm_acc32(int dtype, int ta, int tb, size_t m, size_t n, size_t k,
+                    const void *a, size_t lda, const void *b, size_t ldb,
+                    float *c, size_t ldc, int beta, int nthreads)
+{
+    gemm_run(dtype, ta, tb, m, n, k, a, lda, b, ldb, c, ldc, beta, 0, nthreads);
+}
+
+void orc_gemm_acc64(int dtype, int ta, int tb, size_t m, size_t n, size_t k,
+                    const void *a, size_t lda, const void *b, size_t ldb,
+                    double *c, size_t ldc, int nthreads)
+{
+    gemm_run(dtype, ta, tb, m, n, k, a, lda, b, ldb, c, ldc, 0, 1, nthreads);
+}
+
+/* ---------------- elementwise chains ---------------- */
+
+float orc_sigmoid(float x)
+{
+    /* activations.c:149-160 / jit.c:334 */
+    return 1.0f / (1.0f + expf(-x));
+}
+
+float orc_gelu(float x)
+{
+    /* exact erf form, activations.c:166-173 */
+    return 0.5f * x * (1.0f + erff(x * 0.70710678118f));
+}
+
+static float gelu_grad(float x)
+{
+    /* grad_gelu, autograd.c:794-801 */
+    const float sqrt_2pi = 2.50662827463f;
+    const float inv_sqrt2 = 0.70710678118f;
+    float erf_term = erff(x * inv_sqrt2);
+    float phi = expf(-0.5f * x * x) / sqrt_2pi;
+    return 0.5f * (1.0f + erf_term) + x * phi;
+}
+
+void orc_chain1_backward(const float *a, const float *b, const float *c,
+                         size_t n, float *da, float *db, float *dc)
+{
+    /* forward: t0 = a+b, t1 = t0*c, t2 = relu(t1), t3 = tanh(t2);
+     * upstream of t3 is the sum_all scale 1.  Local grads as the JIT suffix
+     * emits them: tanh' = 1 - tanh(x)^2 recomputed from the input
+     * (autograd.c:2260-2267), relu' = step(x) (:2244-2249), mul' = other
+     * operand (:2189-2194), add' = 1 (:2176). */
+    for (size_t i = 0; i < n; i++) {
+        float t0 = a[i] + b[i];
+        float t1 = t0 * c[i];
+        float t2 = t1 > 0.0f ? t1 : 0.0f;
+        float th = tanhf(t2);
+        float g2 = 1.0f * (1.0f - th * th);
+        float g1 = g2 * (t1 > 0.0f ? 1.0f : 0.0f);
+        float g0 = g1 * c[i];
+        dc[i] = g1 * t0;
+        da[i] = g0;
+        db[i] = g0;
+    }
+}
+
+void orc_chain2_backward(const float *x, const float *bias, const float *g,
+                         size_t R, size_t C, float *dx, float *dg,
+                         float *dbias, double *dbias64)
+{
+    /* forward: t0 = x+bias, t1 = gelu(t0), t2 = sigmoid(g), y = t1*t2.
+     * dL/dt1 = t2, dL/dt2 = t1, dg = dt2 * s(1-s), dt0 = dt1 * gelu'(t0),
+     * dx = dt0, dbias[c] = sum over rows of dt0 (row order, f32). */
+    for (size_t c = 0; c < C; c++) {
+        dbias[c] = 0.0f;
+        if (dbias64)
+            dbias64[c] = 0.0;
+    }
+    for (size_t r = 0; r < R; r++) {
+        for (size_t c = 0; c < C; c++) {
+            size_t i = r * C + c;
+            float t0 = x[i] + bias[c];
+            float t1 = orc_gelu(t0);
+            float s = orc_sigmoid(g[i]);
+            float dt1 = 1.0f * s;
+            float dt2 = 1.0f * t1;
+            dg[i] = dt2 * (s * (1.0f - s));
+            float dt0 = dt1 * gelu_grad(t0);
+            dx[i] = dt0;
+            dbias[c] += dt0;
+            if (dbias64)
+                dbias64[c] += (double)dt0;
+        }
+    }
+}
+
+float orc_mse_grad_scale(size_t ndim, const size_t *shape, bool mean)
+{
+    if (!mean || ndim == 0)
+        return 2.0f;
+    return 2.0f * (1.0f / (float)shape[ndim - 1]);
+}

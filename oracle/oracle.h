@@ -1,0 +1,107 @@
+/*
+ * CPU oracle for the picograd backward path -- TEST INFRASTRUCTURE ONLY.
+ *
+ * A plain-C11 restatement of the reference CPU algorithms this build
+ * replaces on the GPU.  Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load it, and only as the checker: the product library
+ * (picograd_amd/) never links, calls or falls back to anything here.
+ *
+ * Every function cites the reference file:line it restates (paths relative
+ * to the reference checkout).  How each one is pinned:
+ *   orc_seed/orc_uniform/orc_normal   golden RNG streams from the compiled
+ *                                     reference (tests/golden) -- bit-exact
+ *   orc_f32_to_bf16 ... orc_f16_to_f32 exhaustive 2^16 decode + special
+ *                                     values + random sample vs the
+ *                                     reference's convert.h built as a shim
+ *   orc_sgd_step                      test_opt.c:48-138 known answers and
+ *                                     golden multi-step trajectories
+ *   orc_gemm_acc32                    f64 brute force, ragged shapes, and the
+ *                                     reference pg_gemm_ex (bgemm/hgemm)
+ *   orc_chain1_backward               golden C1 grads (JIT on and off)
+ *   orc_chain2_backward               golden C2 grads at a reduced shape
+ *   orc_mse_grad_scale                golden mse/mean_all graphs
+ * No function here is "parity unpinned".
+ */
+#ifndef PG_ORACLE_H
+#define PG_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <stdbool.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { ORC_F32 = 0, ORC_F16 = 1, ORC_BF16 = 2 };
+
+/* RNG: splitmix64 stream (tensor.c:289-339). */
+void orc_seed(unsigned long long seed);
+void orc_uniform(float *out, size_t n, float low, float high);
+void orc_normal(float *out, size_t n, float mean, float stddev);
+
+/* RNE conversions (convert.h:15-104). */
+uint16_t orc_f32_to_bf16(float f);
+float orc_bf16_to_f32(uint16_t h);
+uint16_t orc_f32_to_f16(float f);
+float orc_f16_to_f32(uint16_t h);
+void orc_cast_f32(int dtype, const float *src, uint16_t *dst, size_t n);
+void orc_round_f32(int dtype, float *x, size_t n); /* x = f32(dtype(x)) */
+
+/* SGD (sgd.c:111-162): one step over one parameter tensor. */
+void orc_sgd_step(float *p, const float *g, float *buf, size_t n, float lr,
+                  float momentum, float dampening, float weight_decay,
+                  bool nesterov);
+
+/*
+ * C[i,j] (+)= sum_p A(i,p) * B(p,j), every product formed from f32 values
+ * (16-bit operands upcast first) and accumulated in f32 in p order.
+ * A(i,p) = ta ? a[p*lda+i] : a[i*lda+p];  B(p,j) = tb ? b[j*ldb+p] : b[p*ldb+j].
+ * dtype selects how a and b are read (ORC_F32: float*, else uint16_t*).
+ * beta 0 overwrites C, 1 adds into it.  Threads over rows of C.
+ * Restates the f32-accumulate contract of pg_cpu_gemm_ex (gemm.c:575-629)
+ * and the dgrad/wgrad products of bwd_matmul (autograd.c:655-692).
+ */
+void orc_gemm_acc32(int dtype, int ta, int tb, size_t m, size_t n, size_t k,
+                    const void *a, size_t lda, const void *b, size_t ldb,
+                    float *c, size_t ldc, int beta, int nthreads);
+/* Same product accumulated in f64 (the error yardstick). */
+void orc_gemm_acc64(int dtype, int ta, int tb, size_t m, size_t n, size_t k,
+                    const void *a, size_t lda, const void *b, size_t ldb,
+                    double *c, size_t ldc, int nthreads);
+
+/*
+ * Config-1 chain: loss = sum_all(tanh(relu((a+b)*c))), flat n elements.
+ * Writes dL/da, dL/db, dL/dc (autograd.c:2166-2297 chain rule as the JIT
+ * suffix applies it; autograd.c:519-559 for the eager local grads).
+ */
+void orc_chain1_backward(const float *a, const float *b, const float *c,
+                         size_t n, float *da, float *db, float *dc);
+
+/*
+ * Config-2 chain: loss = sum_all(gelu(x + bias) * sigmoid(g)), x,g [R,C],
+ * bias [C].  dx, dg [R,C]; dbias [C] summed over rows in row order in f32
+ * (autograd.c:364-387), dbias64 (optional) the same sum in f64.
+ * GELU' follows grad_gelu (autograd.c:794-801), sigmoid' the JIT form
+ * s*(1-s) (autograd.c:2251-2258).
+ */
+void orc_chain2_backward(const float *x, const float *bias, const float *g,
+                         size_t R, size_t C, float *dx, float *dg,
+                         float *dbias, double *dbias64);
+
+/* Forward values used by the chains (activations.c:113-173). */
+float orc_gelu(float x);
+float orc_sigmoid(float x);
+
+/*
+ * Upstream-grad scale that pg_ag_mse(pred, tgt, mean) hands to d = pred-tgt:
+ * 2 * (mean ? 1/shape[ndim-1] : 1)   (autograd.c:1018-1043, :1758-1771;
+ * reduce_all only divides by the last remaining axis).
+ */
+float orc_mse_grad_scale(size_t ndim, const size_t *shape, bool mean);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

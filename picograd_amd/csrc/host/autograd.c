@@ -1,0 +1,624 @@
+/*
+ * Autograd nodes, forward ops and the eager (non-fused) device backward of
+ * each op.  Node ownership and graph construction follow the reference's
+ * autograd/autograd.c:64-260 (attach retains parents, requires_grad
+ * propagates, no-grad mode builds detached nodes); every value and grad is
+ * a device tensor and every op enqueues kernels on the library stream.
+ */
+#define _POSIX_C_SOURCE 200809L
+#include "internal.h"
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ---------------------------------------------------------------- state */
+
+static char g_err[512];
+static bool g_grad_enabled = true;
+static int g_no_grad_depth;
+
+void pga_set_err(const char *fmt, ...)
+{
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+}
+
+const char *pg_autograd_last_error(void) { return g_err; }
+bool pg_autograd_is_grad_enabled(void) { return g_grad_enabled && g_no_grad_depth == 0; }
+void pg_autograd_set_grad_enabled(bool enabled) { g_grad_enabled = enabled; }
+void pg_no_grad_push(void) { g_no_grad_depth++; }
+void pg_no_grad_pop(void)
+{
+    if (g_no_grad_depth > 0)
+        g_no_grad_depth--;
+}
+
+/* ---------------------------------------------------------------- nodes */
+
+static pg_node *node_wrap(pg_tensor *t, bool requires_grad)
+{
+    if (!t)
+        return NULL;
+    pg_node *n = calloc(1, sizeof *n);
+    if (!n) {
+        pg_tensor_free(t);
+        return NULL;
+    }
+    n->value = t;
+    n->requires_grad = requires_grad;
+    n->refs = 1;
+    return n;
+}
+
+static pg_node *attach(pg_tensor *value, size_t np, pg_node **parents, void (*bwd)(pg_node *), void *ctx,
+                       pg_ag_op_t op)
+{
+    if (!value) {
+        free(ctx);
+        return NULL;
+    }
+    if (!pg_autograd_is_grad_enabled()) {
+        free(ctx);
+        return node_wrap(value, false);
+    }
+    pg_node *n = calloc(1, sizeof *n);
+    if (!n) {
+        pg_tensor_free(value);
+        free(ctx);
+        return NULL;
+    }
+    n->value = value;
+    n->backward = bwd;
+    n->ctx = ctx;
+    n->ag_op = op;
+    n->refs = 1;
+    if (np) {
+        n->parents = malloc(np * sizeof *n->parents);
+        if (!n->parents) {
+            free(n);
+            pg_tensor_free(value);
+            free(ctx);
+            return NULL;
+        }
+        for (size_t i = 0; i < np; i++) {
+            n->parents[i] = pg_node_retain(parents[i]);
+            n->requires_grad |= parents[i]->requires_grad;
+        }
+        n->nparents = np;
+        if (!n->requires_grad) {
+            n->backward = NULL;
+            free(ctx);
+            n->ctx = NULL;
+        }
+    }
+    return n;
+}
+
+pg_node *pg_var_from_data(size_t ndim, const size_t *shape, const float *data, bool rg)
+{
+    return node_wrap(pg_tensor_from_data(ndim, shape, data), rg);
+}
+
+pg_node *pg_var_from_tensor(const pg_tensor *t, bool rg)
+{
+    if (!t)
+        return NULL;
+    pg_tensor *c = pgt_alloc(t->dtype, t->ndim, t->shape);
+    if (!c)
+        return NULL;
+    if (t->pg_flags & PG_TENSOR_ZERO_PENDING)
+        pg_tensor_fill(c, 0.0f);
+    else
+        pgd_d2d(c->dev, t->dev, t->numel * t->elem_size);
+    return node_wrap(c, rg);
+}
+
+pg_node *pg_var_zeros(size_t ndim, const size_t *shape, bool rg) { return node_wrap(pg_tensor_zeros(ndim, shape), rg); }
+pg_node *pg_var_ones(size_t ndim, const size_t *shape, bool rg) { return node_wrap(pg_tensor_ones(ndim, shape), rg); }
+pg_node *pg_var_full(size_t ndim, const size_t *shape, float v, bool rg)
+{
+    return node_wrap(pg_tensor_full(ndim, shape, v), rg);
+}
+pg_node *pg_var_uniform(size_t ndim, const size_t *shape, float lo, float hi, bool rg)
+{
+    return node_wrap(pg_tensor_uniform(ndim, shape, lo, hi), rg);
+}
+pg_node *pg_var_normal(size_t ndim, const size_t *shape, float mean, float sd, bool rg)
+{
+    return node_wrap(pg_tensor_normal(ndim, shape, mean, sd), rg);
+}
+pg_node *pg_var_scalar(float v, bool rg) { return pg_var_full(1, (size_t[]){1}, v, rg); }
+
+pg_node *pg_node_retain(pg_node *n)
+{
+    if (n)
+        n->refs++;
+    return n;
+}
+
+void pg_node_free(pg_node *n)
+{
+    if (!n)
+        return;
+    size_t cap = 16, sp = 0;
+    pg_node **stk = malloc(cap * sizeof *stk);
+    if (!stk)
+        return;
+    stk[sp++] = n;
+    while (sp) {
+        pg_node *t = stk[--sp];
+        if (--t->refs)
+            continue;
+        pg_tensor_free(t->value);
+        pg_tensor_free(t->grad);
+        free(t->ctx);
+        if (sp + t->nparents > cap) {
+            while (sp + t->nparents > cap)
+                cap *= 2;
+            pg_node **ns = realloc(stk, cap * sizeof *ns);
+            if (!ns)
+                break;
+            stk = ns;
+        }
+        for (size_t i = 0; i < t->nparents; i++)
+            stk[sp++] = t->parents[i];
+        free(t->parents);
+        free(t);
+    }
+    free(stk);
+}
+
+pg_node *pg_node_detach(pg_node *n)
+{
+    if (!n || !n->value)
+        return NULL;
+    return node_wrap(pg_tensor_clone(n->value), false);
+}
+
+/* ---------------------------------------------------------------- grads */
+
+pg_tensor *pga_grad_for_write(pg_node *n, int *beta)
+{
+    if (!n->grad) {
+        n->grad = pgt_alloc(PG_DTYPE_F32, n->value->ndim, n->value->shape);
+        *beta = 0;
+        return n->grad;
+    }
+    if (n->grad->pg_flags & PG_TENSOR_ZERO_PENDING) {
+        n->grad->pg_flags &= ~PG_TENSOR_ZERO_PENDING;
+        *beta = 0;
+    } else {
+        *beta = 1;
+    }
+    return n->grad;
+}
+
+/* dst grad (+)= scale * (g summed onto dst's shape) */
+static void accum(pg_node *dst, const pg_tensor *g, float scale)
+{
+    if (!dst->requires_grad || !g)
+        return;
+    int beta;
+    pg_tensor *dg = pga_grad_for_write(dst, &beta);
+    if (!dg)
+        return;
+    pgk_bcast bc;
+    memset(&bc, 0, sizeof bc);
+    bc.ndim = (int)g->ndim;
+    size_t off = g->ndim - dg->ndim;
+    for (size_t d = 0; d < g->ndim; d++) {
+        bc.shape[d] = (int64_t)g->shape[d];
+        if (d < off)
+            bc.sa[d] = 0;
+        else
+            bc.sa[d] = dg->shape[d - off] == 1 ? 0 : (int64_t)dg->stride[d - off];
+    }
+    pgd_check(pgk_reduce_into_f32((float *)dg->dev, dg->numel, (const float *)g->dev, &bc, scale, beta, pgd_stream()),
+              "accum");
+}
+
+/* ---------------------------------------------------------------- elementwise forward */
+
+static bool need_f32(const pg_tensor *t, const char *what)
+{
+    if (!t || !t->dev) {
+        pga_set_err("%s: null tensor", what);
+        return false;
+    }
+    if (t->dtype != PG_DTYPE_F32 || !pgt_is_contiguous(t)) {
+        pga_set_err("%s: needs a contiguous f32 tensor", what);
+        return false;
+    }
+    pgt_materialize((pg_tensor *)t);
+    return true;
+}
+
+/* broadcast (common.h:6-54 rules); strides of a and b over the out shape */
+static bool bcast_desc(const pg_tensor *a, const pg_tensor *b, size_t *ond, size_t *oshape, pgk_bcast *bc)
+{
+    size_t nd = a->ndim > b->ndim ? a->ndim : b->ndim;
+    for (size_t d = 0; d < nd; d++) {
+        size_t da = d < nd - a->ndim ? 1 : a->shape[d - (nd - a->ndim)];
+        size_t db = d < nd - b->ndim ? 1 : b->shape[d - (nd - b->ndim)];
+        if (da != db && da != 1 && db != 1)
+            return false;
+        oshape[d] = da > db ? da : db;
+    }
+    *ond = nd;
+    memset(bc, 0, sizeof *bc);
+    bc->ndim = (int)nd;
+    for (size_t d = 0; d < nd; d++) {
+        bc->shape[d] = (int64_t)oshape[d];
+        size_t ia = d - (nd - a->ndim), ib = d - (nd - b->ndim);
+        bc->sa[d] = (d < nd - a->ndim || a->shape[ia] == 1) ? 0 : (int64_t)a->stride[ia];
+        bc->sb[d] = (d < nd - b->ndim || b->shape[ib] == 1) ? 0 : (int64_t)b->stride[ib];
+    }
+    return true;
+}
+
+static pg_tensor *binary_fwd(int op, const pg_tensor *a, const pg_tensor *b)
+{
+    if (!need_f32(a, "binary op") || !need_f32(b, "binary op"))
+        return NULL;
+    size_t nd, shp[PG_MAX_NDIM];
+    pgk_bcast bc;
+    if (!bcast_desc(a, b, &nd, shp, &bc)) {
+        pga_set_err("binary op: incompatible broadcast shapes");
+        return NULL;
+    }
+    pg_tensor *y = pgt_alloc(PG_DTYPE_F32, nd, shp);
+    if (!y)
+        return NULL;
+    if (!pgd_check(pgk_binary_f32(op, (const float *)a->dev, (const float *)b->dev, (float *)y->dev, &bc,
+                                  pgd_stream()),
+                   "binary")) {
+        pg_tensor_free(y);
+        return NULL;
+    }
+    return y;
+}
+
+static pg_tensor *unary_fwd(int op, const pg_tensor *a, float p0, float p1)
+{
+    if (!need_f32(a, "unary op"))
+        return NULL;
+    pg_tensor *y = pgt_alloc(PG_DTYPE_F32, a->ndim, a->shape);
+    if (!y)
+        return NULL;
+    if (!pgd_check(pgk_unary_f32(op, (const float *)a->dev, (float *)y->dev, a->numel, p0, p1, pgd_stream()),
+                   "unary")) {
+        pg_tensor_free(y);
+        return NULL;
+    }
+    return y;
+}
+
+/* ---------------------------------------------------------------- eager backward */
+
+/* dst (+)= scale * reduce_to_dst( g OP other ) via a temp of g's shape */
+static void accum_binary(pg_node *dst, const pg_tensor *g, int op, const pg_tensor *other, float scale)
+{
+    if (!dst->requires_grad)
+        return;
+    size_t nd, shp[PG_MAX_NDIM];
+    pgk_bcast bc;
+    if (!bcast_desc(g, other, &nd, shp, &bc))
+        return;
+    pg_tensor *t = pgt_alloc(PG_DTYPE_F32, nd, shp);
+    if (!t)
+        return;
+    pgk_binary_f32(op, (const float *)g->dev, (const float *)other->dev, (float *)t->dev, &bc, pgd_stream());
+    accum(dst, t, scale);
+    pg_tensor_free(t);
+}
+
+static void bwd_add(pg_node *n)
+{
+    accum(n->parents[0], n->grad, 1.0f);
+    accum(n->parents[1], n->grad, 1.0f);
+}
+
+static void bwd_sub(pg_node *n)
+{
+    accum(n->parents[0], n->grad, 1.0f);
+    accum(n->parents[1], n->grad, -1.0f);
+}
+
+static void bwd_mul(pg_node *n)
+{
+    accum_binary(n->parents[0], n->grad, PGK_MUL, n->parents[1]->value, 1.0f);
+    accum_binary(n->parents[1], n->grad, PGK_MUL, n->parents[0]->value, 1.0f);
+}
+
+static void bwd_div(pg_node *n)
+{
+    pg_node *pa = n->parents[0], *pb = n->parents[1];
+    const pg_tensor *g = n->grad;
+    accum_binary(pa, g, PGK_DIV, pb->value, 1.0f);
+    if (pb->requires_grad) {
+        /* -(g * a) / (b * b)  (autograd.c:497-509) */
+        pg_tensor *d = binary_fwd(PGK_MUL, pb->value, pb->value);
+        pg_tensor *num = d ? binary_fwd(PGK_MUL, g, pa->value) : NULL;
+        pg_tensor *t = num ? binary_fwd(PGK_DIV, num, d) : NULL;
+        if (t)
+            accum(pb, t, -1.0f);
+        pg_tensor_free(d);
+        pg_tensor_free(num);
+        pg_tensor_free(t);
+    }
+}
+
+static void bwd_neg(pg_node *n) { accum(n->parents[0], n->grad, -1.0f); }
+
+static int unary_code(pg_ag_op_t op)
+{
+    switch (op) {
+    case PG_AG_OP_EXP: return PGK_EXP;
+    case PG_AG_OP_LOG: return PGK_LOG;
+    case PG_AG_OP_SQRT: return PGK_SQRT;
+    case PG_AG_OP_SIN: return PGK_SIN;
+    case PG_AG_OP_COS: return PGK_COS;
+    case PG_AG_OP_RELU: return PGK_RELU;
+    case PG_AG_OP_SIGMOID: return PGK_SIGMOID;
+    case PG_AG_OP_TANH: return PGK_TANH;
+    case PG_AG_OP_GELU: return PGK_GELU;
+    case PG_AG_OP_ERF: return PGK_ERF;
+    case PG_AG_OP_ABS: return PGK_ABS;
+    case PG_AG_OP_LEAKY_RELU: return PGK_LEAKY;
+    case PG_AG_OP_CLAMP: return PGK_CLAMP;
+    default: return -1;
+    }
+}
+
+static void bwd_unary(pg_node *n)
+{
+    pg_node *p = n->parents[0];
+    if (!p->requires_grad)
+        return;
+    int beta;
+    pg_tensor *dg = pga_grad_for_write(p, &beta);
+    if (!dg)
+        return;
+    float p0 = 0, p1 = 0;
+    if (n->ctx) {
+        p0 = ((pga_param_ctx *)n->ctx)->p0;
+        p1 = ((pga_param_ctx *)n->ctx)->p1;
+    }
+    pgd_check(pgk_unary_bwd_f32(unary_code(n->ag_op), (const float *)n->grad->dev, (const float *)p->value->dev,
+                                (float *)dg->dev, dg->numel, p0, p1, 1.0f, beta, pgd_stream()),
+              "unary backward");
+}
+
+static void bwd_reduce(pg_node *n)
+{
+    pg_node *p = n->parents[0];
+    if (!p->requires_grad)
+        return;
+    pga_red_ctx *cx = n->ctx;
+    const pg_tensor *like = p->value, *g = n->grad;
+    float scale = n->ag_op == PG_AG_OP_MEAN ? 1.0f / (float)like->shape[cx->axis] : 1.0f;
+    pgk_bcast bc;
+    memset(&bc, 0, sizeof bc);
+    bc.ndim = (int)like->ndim;
+    for (size_t d = 0; d < like->ndim; d++) {
+        bc.shape[d] = (int64_t)like->shape[d];
+        if (d == cx->axis) {
+            bc.sa[d] = 0;
+            continue;
+        }
+        size_t gd = cx->keepdim ? d : (d < cx->axis ? d : d - 1);
+        bc.sa[d] = (int64_t)g->stride[gd];
+    }
+    int beta;
+    pg_tensor *dg = pga_grad_for_write(p, &beta);
+    if (!dg)
+        return;
+    pgd_check(pgk_expand_into_f32((float *)dg->dev, (const float *)g->dev, &bc, scale, beta, pgd_stream()),
+              "reduce backward");
+}
+
+void pga_backward_node(pg_node *n)
+{
+    if (n->backward && n->grad)
+        n->backward(n);
+}
+
+/* ---------------------------------------------------------------- op wrappers */
+
+#define BINARY_AG(name, code, bwd, agop)                                                                          \
+    pg_node *name(pg_node *a, pg_node *b)                                                                         \
+    {                                                                                                             \
+        if (!a || !b || !a->value || !b->value) {                                                                 \
+            pga_set_err(#name ": null operand");                                                                  \
+            return NULL;                                                                                          \
+        }                                                                                                         \
+        pg_tensor *v = binary_fwd(code, a->value, b->value);                                                      \
+        return v ? attach(v, 2, (pg_node *[]){a, b}, bwd, NULL, agop) : NULL;                                     \
+    }
+
+BINARY_AG(pg_ag_add, PGK_ADD, bwd_add, PG_AG_OP_ADD)
+BINARY_AG(pg_ag_sub, PGK_SUB, bwd_sub, PG_AG_OP_SUB)
+BINARY_AG(pg_ag_mul, PGK_MUL, bwd_mul, PG_AG_OP_MUL)
+BINARY_AG(pg_ag_div, PGK_DIV, bwd_div, PG_AG_OP_DIV)
+
+static pg_node *unary_ag(pg_node *a, int code, pg_ag_op_t op, void (*bwd)(pg_node *), float p0, float p1,
+                         bool with_ctx)
+{
+    if (!a || !a->value) {
+        pga_set_err("unary op: null operand");
+        return NULL;
+    }
+    pg_tensor *v = unary_fwd(code, a->value, p0, p1);
+    if (!v)
+        return NULL;
+    pga_param_ctx *cx = NULL;
+    if (with_ctx) {
+        cx = malloc(sizeof *cx);
+        if (!cx) {
+            pg_tensor_free(v);
+            return NULL;
+        }
+        cx->p0 = p0;
+        cx->p1 = p1;
+    }
+    return attach(v, 1, &a, bwd, cx, op);
+}
+
+pg_node *pg_ag_neg(pg_node *a) { return unary_ag(a, PGK_NEG, PG_AG_OP_NEG, bwd_neg, 0, 0, false); }
+pg_node *pg_ag_exp(pg_node *a) { return unary_ag(a, PGK_EXP, PG_AG_OP_EXP, bwd_unary, 0, 0, false); }
+pg_node *pg_ag_log(pg_node *a) { return unary_ag(a, PGK_LOG, PG_AG_OP_LOG, bwd_unary, 0, 0, false); }
+pg_node *pg_ag_sqrt(pg_node *a) { return unary_ag(a, PGK_SQRT, PG_AG_OP_SQRT, bwd_unary, 0, 0, false); }
+pg_node *pg_ag_sin(pg_node *a) { return unary_ag(a, PGK_SIN, PG_AG_OP_SIN, bwd_unary, 0, 0, false); }
+pg_node *pg_ag_cos(pg_node *a) { return unary_ag(a, PGK_COS, PG_AG_OP_COS, bwd_unary, 0, 0, false); }
+pg_node *pg_ag_relu(pg_node *a) { return unary_ag(a, PGK_RELU, PG_AG_OP_RELU, bwd_unary, 0, 0, false); }
+pg_node *pg_ag_sigmoid(pg_node *a) { return unary_ag(a, PGK_SIGMOID, PG_AG_OP_SIGMOID, bwd_unary, 0, 0, false); }
+pg_node *pg_ag_tanh(pg_node *a) { return unary_ag(a, PGK_TANH, PG_AG_OP_TANH, bwd_unary, 0, 0, false); }
+pg_node *pg_ag_gelu(pg_node *a) { return unary_ag(a, PGK_GELU, PG_AG_OP_GELU, bwd_unary, 0, 0, false); }
+pg_node *pg_ag_erf(pg_node *a) { return unary_ag(a, PGK_ERF, PG_AG_OP_ERF, bwd_unary, 0, 0, false); }
+pg_node *pg_ag_abs(pg_node *a) { return unary_ag(a, PGK_ABS, PG_AG_OP_ABS, bwd_unary, 0, 0, false); }
+pg_node *pg_ag_leaky_relu(pg_node *a, float alpha)
+{
+    return unary_ag(a, PGK_LEAKY, PG_AG_OP_LEAKY_RELU, bwd_unary, alpha, 0, true);
+}
+pg_node *pg_ag_clamp(pg_node *a, float lo, float hi)
+{
+    if (lo > hi) {
+        pga_set_err("clamp: lo > hi");
+        return NULL;
+    }
+    return unary_ag(a, PGK_CLAMP, PG_AG_OP_CLAMP, bwd_unary, lo, hi, true);
+}
+
+pg_node *pg_ag_matmul(pg_node *a, pg_node *b)
+{
+    if (!a || !b || !a->value || !b->value) {
+        pga_set_err("matmul: null operand");
+        return NULL;
+    }
+    pg_tensor *v = pgm_matmul_forward(a->value, b->value);
+    return v ? attach(v, 2, (pg_node *[]){a, b}, pgm_matmul_backward, NULL, PG_AG_OP_MATMUL) : NULL;
+}
+
+/* reduce.c:90-110 output shape: axis kept as 1 or removed; never 0-d */
+static pg_node *ag_reduce(pg_node *a, size_t axis, bool keepdim, bool mean)
+{
+    if (!a || !a->value || a->value->ndim < 1 || axis >= a->value->ndim) {
+        pga_set_err("reduce: bad axis");
+        return NULL;
+    }
+    const pg_tensor *t = a->value;
+    if (!need_f32(t, "reduce"))
+        return NULL;
+    size_t shp[PG_MAX_NDIM], nd = 0;
+    for (size_t d = 0; d < t->ndim; d++) {
+        if (d == axis) {
+            if (keepdim)
+                shp[nd++] = 1;
+        } else {
+            shp[nd++] = t->shape[d];
+        }
+    }
+    if (nd == 0)
+        shp[nd++] = 1;
+    size_t outer = 1, inner = 1, len = t->shape[axis];
+    for (size_t d = 0; d < axis; d++)
+        outer *= t->shape[d];
+    for (size_t d = axis + 1; d < t->ndim; d++)
+        inner *= t->shape[d];
+    pg_tensor *v = pgt_alloc(PG_DTYPE_F32, nd, shp);
+    if (!v)
+        return NULL;
+    float scale = mean ? 1.0f / (float)len : 1.0f;
+    if (!pgd_check(pgk_sum_axis_f32((const float *)t->dev, (float *)v->dev, outer, len, inner, scale, pgd_stream()),
+                   "reduce")) {
+        pg_tensor_free(v);
+        return NULL;
+    }
+    pga_red_ctx *cx = malloc(sizeof *cx);
+    if (!cx) {
+        pg_tensor_free(v);
+        return NULL;
+    }
+    cx->axis = axis;
+    cx->keepdim = keepdim;
+    return attach(v, 1, &a, bwd_reduce, cx, mean ? PG_AG_OP_MEAN : PG_AG_OP_SUM);
+}
+
+pg_node *pg_ag_sum(pg_node *a, size_t axis, bool keepdim) { return ag_reduce(a, axis, keepdim, false); }
+pg_node *pg_ag_mean(pg_node *a, size_t axis, bool keepdim) { return ag_reduce(a, axis, keepdim, true); }
+
+/* reduce_all (autograd.c:1018-1043): sum axis 0 until one axis is left, then
+ * sum or mean over it -- so mean_all divides by the last axis only */
+static pg_node *reduce_all(pg_node *a, bool mean)
+{
+    if (!a || !a->value || a->value->ndim < 1) {
+        pga_set_err("reduce_all: bad operand");
+        return NULL;
+    }
+    pg_node *cur = pg_node_retain(a);
+    for (size_t d = a->value->ndim; d > 1; d--) {
+        pg_node *nx = pg_ag_sum(cur, 0, false);
+        pg_node_free(cur);
+        if (!nx)
+            return NULL;
+        cur = nx;
+    }
+    pg_node *out = mean ? pg_ag_mean(cur, 0, false) : pg_ag_sum(cur, 0, false);
+    pg_node_free(cur);
+    return out;
+}
+
+pg_node *pg_ag_sum_all(pg_node *a) { return reduce_all(a, false); }
+pg_node *pg_ag_mean_all(pg_node *a) { return reduce_all(a, true); }
+
+/* autograd.c:1758-1771 */
+pg_node *pg_ag_mse(pg_node *pred, pg_node *target, bool mean)
+{
+    if (!pred || !target) {
+        pga_set_err("mse: null operand");
+        return NULL;
+    }
+    pg_node *d = pg_ag_sub(pred, target);
+    if (!d)
+        return NULL;
+    pg_node *sq = pg_ag_mul(d, d);
+    pg_node_free(d);
+    if (!sq)
+        return NULL;
+    pg_node *loss = mean ? pg_ag_mean_all(sq) : pg_ag_sum_all(sq);
+    pg_node_free(sq);
+    return loss;
+}
+
+/* ---------------------------------------------------------------- not in this build */
+
+static pg_node *unsupported(const char *what)
+{
+    pga_set_err("%s is not part of the MI355X build", what);
+    return NULL;
+}
+
+pg_node *pg_ag_pow(pg_node *a, pg_node *b) { (void)a; (void)b; return unsupported("pg_ag_pow"); }
+pg_node *pg_ag_softmax(pg_node *a, size_t axis) { (void)a; (void)axis; return unsupported("pg_ag_softmax"); }
+pg_node *pg_ag_transpose(pg_node *a, size_t x, size_t y) { (void)a; (void)x; (void)y; return unsupported("pg_ag_transpose"); }
+pg_node *pg_ag_layernorm(pg_node *x, pg_node *w, pg_node *b, float e) { (void)x; (void)w; (void)b; (void)e; return unsupported("pg_ag_layernorm"); }
+pg_node *pg_ag_rmsnorm(pg_node *x, pg_node *w, float e) { (void)x; (void)w; (void)e; return unsupported("pg_ag_rmsnorm"); }
+pg_node *pg_ag_batchnorm(pg_node *x, pg_node *w, pg_node *b, float e) { (void)x; (void)w; (void)b; (void)e; return unsupported("pg_ag_batchnorm"); }
+pg_node *pg_ag_batchnorm2d(pg_node *x, pg_node *w, pg_node *b, pg_tensor *rm, pg_tensor *rv, float e, float m, bool t)
+{
+    (void)x; (void)w; (void)b; (void)rm; (void)rv; (void)e; (void)m; (void)t;
+    return unsupported("pg_ag_batchnorm2d");
+}
+pg_node *pg_ag_conv2d(pg_node *x, pg_node *w, pg_node *b, size_t kh, size_t kw, int s, int p)
+{
+    (void)x; (void)w; (void)b; (void)kh; (void)kw; (void)s; (void)p;
+    return unsupported("pg_ag_conv2d");
+}
+pg_node *pg_ag_embedding(pg_node *w, const pg_tensor *i) { (void)w; (void)i; return unsupported("pg_ag_embedding"); }
+pg_node *pg_ag_dropout(pg_node *x, float p, bool t) { (void)x; (void)p; (void)t; return unsupported("pg_ag_dropout"); }
+pg_node *pg_ag_cross_entropy(pg_node *l, const size_t *t, size_t n, bool m) { (void)l; (void)t; (void)n; (void)m; return unsupported("pg_ag_cross_entropy"); }
+pg_node *pg_ag_bce_with_logits(pg_node *l, const float *t, size_t n, bool m) { (void)l; (void)t; (void)n; (void)m; return unsupported("pg_ag_bce_with_logits"); }

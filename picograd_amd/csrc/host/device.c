@@ -1,0 +1,312 @@
+/*
+ * Device layer: one HIP device, one stream, a caching allocator.
+ *
+ * Every kernel and copy of the library is queued on a single non-blocking
+ * stream, so a block freed on the host may be handed to the next
+ * allocation at once: any later use is queued behind every earlier use.
+ * Blocks are cached in size classes (powers of two up to 1 MiB, 2 MiB
+ * granules above) and returned to the driver only on pg_amd_release_cached()
+ * or when an allocation fails.
+ */
+#define _POSIX_C_SOURCE 200809L
+#include "internal.h"
+
+#include <hip/hip_runtime_api.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+static hipStream_t g_stream;
+static int g_init_state; /* 0 = not tried, 1 = ok, -1 = failed */
+static char g_err[512];
+
+void pgd_set_err(const char *fmt, ...)
+{
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+}
+
+const char *pg_amd_last_error(void) { return g_err; }
+
+static bool hip_ok(hipError_t e, const char *what)
+{
+    if (e == hipSuccess)
+        return true;
+    pgd_set_err("%s: %s", what, hipGetErrorString(e));
+    return false;
+}
+
+bool pgd_check(int status, const char *what)
+{
+    if (status == 0)
+        return true;
+    pgd_set_err("%s: %s", what, hipGetErrorString((hipError_t)status));
+    return false;
+}
+
+int pg_amd_init(void)
+{
+    if (g_init_state)
+        return g_init_state > 0 ? 0 : -1;
+    int n = 0;
+    if (!hip_ok(hipGetDeviceCount(&n), "hipGetDeviceCount") || n < 1) {
+        if (!g_err[0])
+            pgd_set_err("no HIP device");
+        g_init_state = -1;
+        return -1;
+    }
+    if (!hip_ok(hipSetDevice(0), "hipSetDevice") ||
+        !hip_ok(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking), "hipStreamCreate")) {
+        g_init_state = -1;
+        return -1;
+    }
+    g_init_state = 1;
+    return 0;
+}
+
+bool pgd_ok(void) { return pg_amd_init() == 0; }
+
+pgk_stream pgd_stream(void)
+{
+    pg_amd_init();
+    return (pgk_stream)g_stream;
+}
+
+void *pg_amd_stream(void) { return pgd_stream(); }
+
+bool pgd_sync(void)
+{
+    if (!pgd_ok())
+        return false;
+    return hip_ok(hipStreamSynchronize(g_stream), "hipStreamSynchronize");
+}
+
+int pg_amd_sync(void) { return pgd_sync() ? 0 : -1; }
+
+/* ---------------- caching allocator ---------------- */
+
+typedef struct blk {
+    void *p;
+    size_t cls;
+    struct blk *next;
+} blk;
+
+#define NBINS 1024
+static blk *g_bins[NBINS];
+static size_t g_in_use, g_cached;
+
+static size_t size_class(size_t n)
+{
+    if (n <= 256)
+        return 256;
+    if (n <= ((size_t)1 << 20)) {
+        size_t c = 512;
+        while (c < n)
+            c <<= 1;
+        return c;
+    }
+    size_t g = (size_t)2 << 20;
+    return (n + g - 1) / g * g;
+}
+
+static size_t bin_of(size_t cls) { return (cls / 256 * 2654435761u) % NBINS; }
+
+static void release_all(void)
+{
+    if (g_init_state > 0)
+        hipStreamSynchronize(g_stream);
+    for (size_t i = 0; i < NBINS; i++) {
+        blk *b = g_bins[i];
+        while (b) {
+            blk *nx = b->next;
+            hipFree(b->p);
+            g_cached -= b->cls;
+            free(b);
+            b = nx;
+        }
+        g_bins[i] = NULL;
+    }
+}
+
+void pg_amd_release_cached(void) { release_all(); }
+size_t pg_amd_bytes_in_use(void) { return g_in_use; }
+size_t pg_amd_bytes_cached(void) { return g_cached; }
+
+void *pgd_malloc(size_t nbytes)
+{
+    if (!pgd_ok())
+        return NULL;
+    size_t cls = size_class(nbytes ? nbytes : 1);
+    blk **pp = &g_bins[bin_of(cls)];
+    for (blk *b = *pp; b; pp = &b->next, b = b->next) {
+        if (b->cls == cls) {
+            void *p = b->p;
+            *pp = b->next;
+            free(b);
+            g_cached -= cls;
+            g_in_use += cls;
+            return p;
+        }
+    }
+    void *p = NULL;
+    hipError_t e = hipMalloc(&p, cls);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        release_all();
+        e = hipMalloc(&p, cls);
+    }
+    if (!hip_ok(e, "hipMalloc"))
+        return NULL;
+    g_in_use += cls;
+    return p;
+}
+
+void pgd_free(void *p, size_t nbytes)
+{
+    if (!p)
+        return;
+    size_t cls = size_class(nbytes ? nbytes : 1);
+    blk *b = malloc(sizeof *b);
+    g_in_use -= cls;
+    if (!b) {
+        hipStreamSynchronize(g_stream);
+        hipFree(p);
+        return;
+    }
+    b->p = p;
+    b->cls = cls;
+    b->next = g_bins[bin_of(cls)];
+    g_bins[bin_of(cls)] = b;
+    g_cached += cls;
+}
+
+static void *g_scratch[PGD_SCRATCH_SLOTS];
+static size_t g_scratch_n[PGD_SCRATCH_SLOTS];
+
+void *pgd_scratch(int slot, size_t nbytes)
+{
+    if (slot < 0 || slot >= PGD_SCRATCH_SLOTS)
+        return NULL;
+    if (g_scratch_n[slot] >= nbytes && g_scratch[slot])
+        return g_scratch[slot];
+    if (g_scratch[slot])
+        pgd_free(g_scratch[slot], g_scratch_n[slot]);
+    g_scratch[slot] = pgd_malloc(nbytes);
+    g_scratch_n[slot] = g_scratch[slot] ? nbytes : 0;
+    return g_scratch[slot];
+}
+
+bool pgd_h2d(void *dst, const void *src, size_t nbytes)
+{
+    if (!nbytes)
+        return true;
+    if (!pgd_ok())
+        return false;
+    /* pageable source: the copy is staged before the call returns */
+    return hip_ok(hipMemcpyAsync(dst, src, nbytes, hipMemcpyHostToDevice, g_stream),
+                  "hipMemcpyAsync H2D") &&
+           hip_ok(hipStreamSynchronize(g_stream), "hipStreamSynchronize");
+}
+
+bool pgd_d2h(void *dst, const void *src, size_t nbytes)
+{
+    if (!pgd_ok())
+        return false;
+    if (!nbytes)
+        return pgd_sync();
+    return hip_ok(hipMemcpyAsync(dst, src, nbytes, hipMemcpyDeviceToHost, g_stream),
+                  "hipMemcpyAsync D2H") &&
+           hip_ok(hipStreamSynchronize(g_stream), "hipStreamSynchronize");
+}
+
+bool pgd_d2d(void *dst, const void *src, size_t nbytes)
+{
+    if (!nbytes)
+        return true;
+    if (!pgd_ok())
+        return false;
+    return hip_ok(hipMemcpyAsync(dst, src, nbytes, hipMemcpyDeviceToDevice, g_stream),
+                  "hipMemcpyAsync D2D");
+}
+
+/* ---------------- kernel timer ----------------
+ * When enabled, hot launch sites bracket their kernels with HIP events on
+ * the library stream; pg_amd_timer_read() sums the elapsed times per kind. */
+
+typedef struct {
+    hipEvent_t a, b;
+    int kind;
+} tev;
+
+static tev *g_tev;
+static size_t g_ntev, g_captev;
+static int g_timer_on;
+
+void pg_amd_timer_enable(int on)
+{
+    g_timer_on = on;
+}
+
+int pgd_tbegin(int kind)
+{
+    if (!g_timer_on || !pgd_ok())
+        return -1;
+    if (g_ntev == g_captev) {
+        size_t nc = g_captev ? g_captev * 2 : 256;
+        tev *p = realloc(g_tev, nc * sizeof *p);
+        if (!p)
+            return -1;
+        g_tev = p;
+        g_captev = nc;
+    }
+    tev *t = &g_tev[g_ntev];
+    if (hipEventCreate(&t->a) != hipSuccess)
+        return -1;
+    if (hipEventCreate(&t->b) != hipSuccess) {
+        hipEventDestroy(t->a);
+        return -1;
+    }
+    t->kind = kind;
+    hipEventRecord(t->a, g_stream);
+    return (int)g_ntev++;
+}
+
+void pgd_tend(int slot)
+{
+    if (slot >= 0 && (size_t)slot < g_ntev)
+        hipEventRecord(g_tev[slot].b, g_stream);
+}
+
+double pg_amd_timer_read(int kind, size_t *count)
+{
+    double total = 0.0;
+    size_t n = 0;
+    if (pgd_ok())
+        hipStreamSynchronize(g_stream);
+    for (size_t i = 0; i < g_ntev; i++) {
+        if (g_tev[i].kind != kind)
+            continue;
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, g_tev[i].a, g_tev[i].b) == hipSuccess) {
+            total += ms;
+            n++;
+        }
+    }
+    if (count)
+        *count = n;
+    return total;
+}
+
+void pg_amd_timer_reset(void)
+{
+    if (pgd_ok())
+        hipStreamSynchronize(g_stream);
+    for (size_t i = 0; i < g_ntev; i++) {
+        hipEventDestroy(g_tev[i].a);
+        hipEventDestroy(g_tev[i].b);
+    }
+    g_ntev = 0;
+}

@@ -1,0 +1,86 @@
+/*
+ * Internal interfaces of the picograd-amd host library (C11).
+ */
+#ifndef PG_INTERNAL_H
+#define PG_INTERNAL_H
+
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "picograd/amd.h"
+#include "picograd/autograd.h"
+#include "picograd/backend.h"
+#include "picograd/jit.h"
+#include "picograd/sgd.h"
+#include "picograd/tensor.h"
+#include "../kernels/launch.h"
+
+/* pg_tensor.pg_flags */
+#define PG_TENSOR_ZERO_PENDING 1u /* logically zero; device bytes not written */
+
+/* ---- device layer (device.c) ---- */
+bool pgd_ok(void);                 /* init on first use; false if no device */
+pgk_stream pgd_stream(void);
+void *pgd_malloc(size_t nbytes);   /* cached, stream-ordered reuse */
+void pgd_free(void *p, size_t nbytes);
+bool pgd_h2d(void *dst, const void *src, size_t nbytes);  /* enqueued */
+bool pgd_d2h(void *dst, const void *src, size_t nbytes);  /* waits */
+bool pgd_d2d(void *dst, const void *src, size_t nbytes);  /* enqueued */
+bool pgd_sync(void);
+void pgd_set_err(const char *fmt, ...);
+/* records a launcher status; false (and last error set) when non-zero */
+bool pgd_check(int status, const char *what);
+/* a scratch device buffer of at least nbytes, reused across calls on the
+ * stream (grows, never shrinks) */
+void *pgd_scratch(int slot, size_t nbytes);
+#define PGD_SCRATCH_SLOTS 4
+/* kernel timer (pg_amd_timer_*): kinds and bracket calls */
+enum { PGD_T_JIT_MAIN = 0, PGD_T_JIT_FIN = 1, PGD_T_GEMM16 = 2, PGD_T_SGD = 3, PGD_T_STAGE = 4 };
+int pgd_tbegin(int kind);
+void pgd_tend(int slot);
+
+/* ---- tensors (tensor.c) ---- */
+pg_tensor *pgt_alloc(pg_dtype dtype, size_t ndim, const size_t *shape);
+void pgt_set_contig_strides(pg_tensor *t);
+bool pgt_is_contiguous(const pg_tensor *t);
+/* materialise a pending zero (grad tensors) */
+void pgt_materialize(pg_tensor *t);
+
+/* ---- RNG (tensor.c) ---- */
+void pg_rng_uniform_host(float *out, size_t n, float low, float high);
+void pg_rng_normal_host(float *out, size_t n, float mean, float stddev);
+
+/* ---- autograd shared (autograd.c / walker.c) ---- */
+void pga_set_err(const char *fmt, ...);
+bool pga_op_fusible(pg_ag_op_t op);
+/* grad storage: returns the grad tensor ready for a write; *beta is 0 if
+ * the writer must overwrite (grad fresh or logically zero), 1 to add */
+pg_tensor *pga_grad_for_write(pg_node *n, int *beta);
+void pga_backward_node(pg_node *n); /* eager device backward of one node */
+
+typedef struct { size_t axis; bool keepdim; } pga_red_ctx;
+typedef struct { float p0, p1; } pga_param_ctx;
+
+/* ---- matmul helpers (gemm.c) ---- */
+pg_tensor *pgm_matmul_forward(const pg_tensor *a, const pg_tensor *b);
+void pgm_matmul_backward(pg_node *n);
+
+/* ---- JIT internals used by the walker (jit.c) ---- */
+typedef struct pgj_region pgj_region;
+
+/* Extended graph features for fused backward regions. */
+int pgj_add_input_ex(pg_jit_graph *g, size_t ndim, const size_t *shape);
+/* marks node `id` as an output reduced (summed) onto `ndim/shape`, a shape
+ * broadcast-compatible with the loop shape, combining with beta */
+void pgj_mark_output_ex(pg_jit_graph *g, int id, size_t ndim, const size_t *shape, int beta);
+int pgj_op_internal(pg_jit_graph *g, int op, int a, int b);
+enum { PGJ_OP_GELU_GRAD = 100, PGJ_OP_SIGN = 101, PGJ_OP_ERF_GRAD = 102 };
+/* compile (cached) and launch with device pointers; loop shape given
+ * explicitly.  Returns false and sets the JIT error on failure. */
+bool pgj_launch(pg_jit_graph *g, size_t loop_ndim, const size_t *loop_shape,
+                const void *const *inputs, size_t ninputs, void *const *outputs,
+                size_t noutputs);
+extern size_t pgj_stat_compiles, pgj_stat_hits;
+
+#endif

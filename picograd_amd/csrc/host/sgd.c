@@ -1,0 +1,133 @@
+/*
+ * SGD over device-resident parameters (reference opt/sgd.c).
+ *
+ * Same registration, defaults, config checks, lazily zeroed momentum
+ * buffer and zero_grad-frees-grads behaviour as sgd.c:18-109; the update of
+ * sgd.c:147-160 runs for all parameters in one multi-tensor kernel launch
+ * (up to 32 tensors per launch, blockIdx.y picks the tensor).
+ */
+#define _POSIX_C_SOURCE 200809L
+#include "internal.h"
+
+#include <assert.h>
+#include <stdlib.h>
+
+typedef struct {
+    pg_node *param;
+    pg_tensor *buf;
+} sgd_state;
+
+struct pg_sgd {
+    pg_sgd_cfg cfg;
+    sgd_state *st;
+    size_t n, cap;
+};
+
+pg_sgd_cfg pg_sgd_cfg_default(void)
+{
+    pg_sgd_cfg c = {.lr = 0.01f, .momentum = 0.0f, .dampening = 0.0f, .weight_decay = 0.0f, .nesterov = false};
+    return c;
+}
+
+pg_sgd *pg_sgd_new(const pg_sgd_cfg *cfg)
+{
+    pg_sgd_cfg def = pg_sgd_cfg_default();
+    if (!cfg)
+        cfg = &def;
+    /* sgd.c:43-47 */
+    assert(cfg->lr >= 0.0f);
+    assert(cfg->momentum >= 0.0f);
+    assert(cfg->dampening >= 0.0f);
+    assert(cfg->weight_decay >= 0.0f);
+    assert(!cfg->nesterov || (cfg->momentum > 0.0f && cfg->dampening == 0.0f));
+    pg_sgd *o = calloc(1, sizeof *o);
+    if (!o)
+        return NULL;
+    o->cfg = *cfg;
+    return o;
+}
+
+void pg_sgd_free(pg_sgd *opt)
+{
+    if (!opt)
+        return;
+    for (size_t i = 0; i < opt->n; i++) {
+        pg_node_free(opt->st[i].param);
+        pg_tensor_free(opt->st[i].buf);
+    }
+    free(opt->st);
+    free(opt);
+}
+
+int pg_sgd_add_param(pg_sgd *opt, pg_node *param)
+{
+    assert(opt && param && param->requires_grad);
+    if (opt->n == opt->cap) {
+        size_t nc = opt->cap ? opt->cap * 2 : 8;
+        sgd_state *p = realloc(opt->st, nc * sizeof *p);
+        if (!p)
+            return -1;
+        opt->st = p;
+        opt->cap = nc;
+    }
+    opt->st[opt->n].param = pg_node_retain(param);
+    opt->st[opt->n].buf = NULL;
+    opt->n++;
+    return 0;
+}
+
+size_t pg_sgd_num_params(const pg_sgd *opt) { return opt ? opt->n : 0; }
+
+void pg_sgd_zero_grad(pg_sgd *opt)
+{
+    assert(opt);
+    for (size_t i = 0; i < opt->n; i++) {
+        pg_node *p = opt->st[i].param;
+        if (p->grad) {
+            pg_tensor_free(p->grad);
+            p->grad = NULL;
+        }
+    }
+}
+
+void pg_sgd_step(pg_sgd *opt)
+{
+    assert(opt);
+    if (!pgd_ok())
+        return;
+    const pg_sgd_cfg c = opt->cfg;
+    pgk_sgd_seg *segs = calloc(opt->n ? opt->n : 1, sizeof *segs);
+    if (!segs)
+        return;
+    int ns = 0;
+    for (size_t i = 0; i < opt->n; i++) {
+        pg_node *p = opt->st[i].param;
+        pg_tensor *g = p->grad;
+        if (!g)
+            continue;
+        assert(g->numel == p->value->numel);
+        if (p->value->dtype != PG_DTYPE_F32) {
+            pga_set_err("pg_sgd_step: parameter storage must be f32");
+            continue;
+        }
+        pgt_materialize(g);
+        if (c.momentum != 0.0f && !opt->st[i].buf) {
+            opt->st[i].buf = pg_tensor_zeros(p->value->ndim, p->value->shape);
+            if (!opt->st[i].buf)
+                continue;
+        }
+        segs[ns].p = p->value->dev;
+        segs[ns].g = g->dev;
+        segs[ns].buf = c.momentum != 0.0f ? opt->st[i].buf->dev : NULL;
+        segs[ns].shadow = NULL;
+        segs[ns].n = p->value->numel;
+        ns++;
+    }
+    int tk = ns ? pgd_tbegin(PGD_T_SGD) : -1;
+    if (ns)
+        pgd_check(pgk_sgd_multi(segs, ns, c.lr, c.momentum, c.dampening, c.weight_decay, c.nesterov ? 1 : 0,
+                                pgd_stream()),
+                  "pg_sgd_step");
+    pgd_tend(tk);
+    free(segs);
+}

@@ -1,0 +1,115 @@
+/*
+ * C-ABI launchers of the hand-written gfx950 kernels (kernels, .hip files).
+ * The C11 host code calls only these; each enqueues on the given stream and
+ * returns 0, or a hipError_t value when the launch was rejected.
+ */
+#ifndef PGK_LAUNCH_H
+#define PGK_LAUNCH_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void *pgk_stream; /* hipStream_t */
+
+#define PGK_MAX_NDIM 8
+
+/* unary forward / backward op codes (shared with the JIT codegen) */
+enum {
+    PGK_NEG = 0, PGK_EXP, PGK_LOG, PGK_SQRT, PGK_SIN, PGK_COS, PGK_RELU,
+    PGK_SIGMOID, PGK_TANH, PGK_GELU, PGK_ERF, PGK_ABS, PGK_LEAKY, PGK_CLAMP,
+    PGK_UNARY_COUNT
+};
+/* binary op codes */
+enum { PGK_ADD = 0, PGK_SUB, PGK_MUL, PGK_DIV, PGK_BINARY_COUNT };
+
+/* An output of `ndim` dims and two (broadcast) operand stride sets, in
+ * elements; a zero stride repeats the operand along that dim. */
+typedef struct {
+    int ndim;
+    int64_t shape[PGK_MAX_NDIM];
+    int64_t sa[PGK_MAX_NDIM];
+    int64_t sb[PGK_MAX_NDIM];
+} pgk_bcast;
+
+int pgk_fill_f32(float *dst, size_t n, float v, pgk_stream s);
+int pgk_fill_u16(uint16_t *dst, size_t n, uint16_t v, pgk_stream s);
+
+/* y = op(x) */
+int pgk_unary_f32(int op, const float *x, float *y, size_t n, float p0, float p1, pgk_stream s);
+/* dx = (beta ? dx : 0) + scale * g * op'(x) */
+int pgk_unary_bwd_f32(int op, const float *g, const float *x, float *dx, size_t n, float p0,
+                      float p1, float scale, int beta, pgk_stream s);
+/* y[i] = a[off_a(i)] op b[off_b(i)] over bc->shape */
+int pgk_binary_f32(int op, const float *a, const float *b, float *y, const pgk_bcast *bc,
+                   pgk_stream s);
+
+/*
+ * dst (dst_numel elements) (beta ? += : =) scale * sum of src over the
+ * source elements that map onto each dst element.  src is contiguous with
+ * shape bc->shape; bc->sa holds dst strides per src dim (0 on reduced dims).
+ * Deterministic: each dst element sums its sources in row-major order.
+ */
+int pgk_reduce_into_f32(float *dst, size_t dst_numel, const float *src, const pgk_bcast *bc,
+                        float scale, int beta, pgk_stream s);
+/* dst[i] (beta ? += : =) scale * src[off(i)], broadcasting src over bc->shape
+ * with strides bc->sa (dst contiguous). */
+int pgk_expand_into_f32(float *dst, const float *src, const pgk_bcast *bc, float scale, int beta,
+                        pgk_stream s);
+
+/* forward reductions: y[o, i] = scale * sum_l x[o, l, i] */
+int pgk_sum_axis_f32(const float *x, float *y, size_t outer, size_t len, size_t inner,
+                     float scale, pgk_stream s);
+
+/* dtype casts with the reference's RNE bit rules; dtype 1 = f16, 2 = bf16 */
+int pgk_cast_to16(int dtype, const float *src, uint16_t *dst, size_t n, pgk_stream s);
+int pgk_cast_from16(int dtype, const uint16_t *src, float *dst, size_t n, pgk_stream s);
+/*
+ * Staging for the MFMA GEMMs: dst[c * ldd + r] = cvt(src[r * lds + c]) for a
+ * rows x cols source (transposed copy), dst padded with zeros for
+ * r in [rows, ldd) when pad != 0.  src_dtype 0 = f32 (rounded to dtype),
+ * else 16-bit of the same dtype.  batch copies use the given strides.
+ */
+int pgk_transpose_to16(int dtype, int src_dtype, const void *src, size_t rows, size_t cols,
+                       size_t lds, uint16_t *dst, size_t ldd, size_t batch, size_t sstride,
+                       size_t dstride, pgk_stream s);
+/* dst[r * ldd + c] = cvt(src[r * lds + c]), zero pad for c in [cols, ldd) */
+int pgk_copy_to16(int dtype, int src_dtype, const void *src, size_t rows, size_t cols, size_t lds,
+                  uint16_t *dst, size_t ldd, size_t batch, size_t sstride, size_t dstride,
+                  pgk_stream s);
+
+/*
+ * C[b][i, j] (beta ? += : =) sum_p A[b][i, p] * B[b][j, p]
+ * f16/bf16 operands, both with the reduction dim contiguous ("NT"), f32
+ * accumulate and output.  lda/ldb multiples of 8, bases 16-byte aligned,
+ * k padded with zeros up to a multiple of 8 (the staging kernels ensure it).
+ */
+int pgk_gemm16_nt(int dtype, size_t m, size_t n, size_t k, const uint16_t *a, size_t lda,
+                  size_t stride_a, const uint16_t *b, size_t ldb, size_t stride_b, float *c,
+                  size_t ldc, size_t stride_c, size_t batch, int beta, pgk_stream s);
+
+/* f32 GEMM, C (beta ? += : =) op(A) op(B); ta/tb select A^T / B^T
+ * (A(i,p) = ta ? a[p*lda+i] : a[i*lda+p], same for B(p,j)). */
+int pgk_gemm_f32(int ta, int tb, size_t m, size_t n, size_t k, const float *a, size_t lda,
+                 size_t stride_a, const float *b, size_t ldb, size_t stride_b, float *c,
+                 size_t ldc, size_t stride_c, size_t batch, int beta, pgk_stream s);
+
+/* multi-tensor SGD */
+typedef struct {
+    float *p;
+    const float *g;
+    float *buf;       /* NULL when momentum == 0 */
+    uint16_t *shadow; /* optional bf16 copy of p written after the update */
+    size_t n;
+} pgk_sgd_seg;
+int pgk_sgd_multi(const pgk_sgd_seg *segs, int nseg, float lr, float momentum, float dampening,
+                  float weight_decay, int nesterov, pgk_stream s);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,125 @@
+"""ctypes handle on the CPU oracle (oracle/liboracle.so) -- the checker.
+
+Test infrastructure only: tests, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg use it; the product library never does.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent.parent
+ORACLE_SO = ROOT / "oracle" / "liboracle.so"
+REF_SO = ROOT / "oracle" / "_ref" / "libpicograd_ref.so"
+REF_CONVERT_SO = ROOT / "oracle" / "_ref" / "libref_convert.so"
+
+_vp, _sz, _fl, _ip = C.c_void_p, C.c_size_t, C.c_float, C.c_int
+
+
+class Oracle:
+    def __init__(self, path: Path = ORACLE_SO):
+        if not path.exists():
+            raise FileNotFoundError(f"{path} missing: run `make -C oracle`")
+        L = C.CDLL(str(path))
+        protos = {
+            "orc_seed": (None, [C.c_ulonglong]),
+            "orc_uniform": (None, [_vp, _sz, _fl, _fl]),
+            "orc_normal": (None, [_vp, _sz, _fl, _fl]),
+            "orc_f32_to_bf16": (C.c_uint16, [_fl]),
+            "orc_bf16_to_f32": (_fl, [C.c_uint16]),
+            "orc_f32_to_f16": (C.c_uint16, [_fl]),
+            "orc_f16_to_f32": (_fl, [C.c_uint16]),
+            "orc_cast_f32": (None, [_ip, _vp, _vp, _sz]),
+            "orc_round_f32": (None, [_ip, _vp, _sz]),
+            "orc_sgd_step": (None, [_vp, _vp, _vp, _sz, _fl, _fl, _fl, _fl, C.c_bool]),
+            "orc_gemm_acc32": (None, [_ip, _ip, _ip, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _ip, _ip]),
+            "orc_gemm_acc64": (None, [_ip, _ip, _ip, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _ip]),
+            "orc_chain1_backward": (None, [_vp, _vp, _vp, _sz, _vp, _vp, _vp]),
+            "orc_chain2_backward": (None, [_vp, _vp, _vp, _sz, _sz, _vp, _vp, _vp, _vp]),
+            "orc_gelu": (_fl, [_fl]),
+            "orc_sigmoid": (_fl, [_fl]),
+            "orc_mse_grad_scale": (_fl, [_sz, C.POINTER(_sz), C.c_bool]),
+        }
+        for name, (res, args) in protos.items():
+            fn = getattr(L, name)
+            fn.restype, fn.argtypes = res, args
+            setattr(self, name, fn)
+        self.lib = L
+
+    # ---- numpy conveniences
+    def uniform(self, n: int, lo: float, hi: float) -> np.ndarray:
+        out = np.empty(n, np.float32)
+        self.orc_uniform(out.ctypes.data, n, lo, hi)
+        return out
+
+    def normal(self, n: int, mean: float, sd: float) -> np.ndarray:
+        out = np.empty(n, np.float32)
+        self.orc_normal(out.ctypes.data, n, mean, sd)
+        return out
+
+    def cast16(self, dtype: int, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.empty(x.shape, np.uint16)
+        self.orc_cast_f32(dtype, x.ctypes.data, out.ctypes.data, x.size)
+        return out
+
+    def gemm(self, dtype: int, a: np.ndarray, b: np.ndarray, ta=False, tb=False, f64=False,
+             threads: int = 8) -> np.ndarray:
+        """C = op(A) . op(B) with f32 (or f64) accumulation of upcast operands."""
+        a = np.ascontiguousarray(a)
+        b = np.ascontiguousarray(b)
+        m = a.shape[1] if ta else a.shape[0]
+        k = a.shape[0] if ta else a.shape[1]
+        n = b.shape[0] if tb else b.shape[1]
+        c = np.zeros((m, n), np.float64 if f64 else np.float32)
+        if f64:
+            self.orc_gemm_acc64(dtype, int(ta), int(tb), m, n, k, a.ctypes.data, a.shape[1],
+                                b.ctypes.data, b.shape[1], c.ctypes.data, n, threads)
+        else:
+            self.orc_gemm_acc32(dtype, int(ta), int(tb), m, n, k, a.ctypes.data, a.shape[1],
+                                b.ctypes.data, b.shape[1], c.ctypes.data, n, 0, threads)
+        return c
+
+    def sgd_step(self, p, g, buf, lr, mu, damp, wd, nesterov) -> None:
+        self.orc_sgd_step(p.ctypes.data, g.ctypes.data, buf.ctypes.data if buf is not None else None,
+                          p.size, lr, mu, damp, wd, nesterov)
+
+    def chain1(self, a, b, c):
+        da, db, dc = (np.empty_like(a) for _ in range(3))
+        self.orc_chain1_backward(a.ctypes.data, b.ctypes.data, c.ctypes.data, a.size,
+                                 da.ctypes.data, db.ctypes.data, dc.ctypes.data)
+        return da, db, dc
+
+    def chain2(self, x, bias, g):
+        R, Cc = x.shape
+        dx, dg = np.empty_like(x), np.empty_like(g)
+        db = np.empty(Cc, np.float32)
+        db64 = np.empty(Cc, np.float64)
+        self.orc_chain2_backward(x.ctypes.data, bias.ctypes.data, g.ctypes.data, R, Cc,
+                                 dx.ctypes.data, dg.ctypes.data, db.ctypes.data, db64.ctypes.data)
+        return dx, dg, db, db64
+
+
+def bf16_to_f32(h: np.ndarray) -> np.ndarray:
+    return (h.astype(np.uint32) << 16).view(np.float32)
+
+
+def f16_to_f32(h: np.ndarray) -> np.ndarray:
+    return h.view(np.float16).astype(np.float32)
+
+
+def rel_fro(x: np.ndarray, ref: np.ndarray) -> float:
+    x = x.astype(np.float64)
+    ref = ref.astype(np.float64)
+    return float(np.linalg.norm(x - ref) / max(np.linalg.norm(ref), 1e-300))
+
+
+def max_rel(x: np.ndarray, ref: np.ndarray, floor_frac: float = 1e-5) -> float:
+    """max |x - ref| / (|ref| + floor), floor = floor_frac * max|ref|: the
+    elementwise relative error with a floor where grads pass through zero."""
+    x = x.astype(np.float64)
+    ref = ref.astype(np.float64)
+    floor = floor_frac * max(float(np.abs(ref).max()), 1e-30)
+    return float((np.abs(x - ref) / (np.abs(ref) + floor)).max())
