@@ -55,8 +55,12 @@ void orc_normal(float *out, size_t n, float mean, float stddev)
         float u2 = orc_u01();
         if (u1 < 1e-12f)
             u1 = 1e-12f;
-        float mag = stddev * sqrtf(-2.0f * logf(u1));
-        out[i] = mean + mag * cosf(2.0f * 3.14159265358979f * u2);
+        /* stddev * radius * cos, formed as (stddev * cos) * radius: the
+         * order the reference's -ffast-math build (clang) evaluates it in,
+         * which the golden streams pin bit for bit for stddev != 1 */
+        float radius = sqrtf(-2.0f * logf(u1));
+        float c = cosf(2.0f * 3.14159265358979f * u2);
+        out[i] = mean + (stddev * c) * radius;
     }
 }
 

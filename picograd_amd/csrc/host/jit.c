@@ -724,7 +724,14 @@ static void emit_body(sbuf *b, const pg_jit_graph *g, const plan_t *P, const boo
             continue;
         for (int e = 0; e < vec; e++) {
             if (n->kind == JN_CONST) {
-                sb_add(b, "    const float v%zu_%d = %.9gf;\n", id, e, (double)n->cval);
+                /* exact hex-float literal of the f32 constant */
+                float cv = n->cval;
+                if (cv != cv)
+                    sb_add(b, "    const float v%zu_%d = __builtin_nanf(\"\");\n", id, e);
+                else if (cv > 3.4028235e38f || cv < -3.4028235e38f)
+                    sb_add(b, "    const float v%zu_%d = %s__builtin_inff();\n", id, e, cv < 0 ? "-" : "");
+                else
+                    sb_add(b, "    const float v%zu_%d = (float)%a;\n", id, e, (double)cv);
                 continue;
             }
             char sa[32], sc[32];

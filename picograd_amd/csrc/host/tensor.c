@@ -212,8 +212,13 @@ void pg_rng_normal_host(float *out, size_t n, float mean, float stddev)
         float u1 = rng_u01(), u2 = rng_u01();
         if (u1 < 1e-12f)
             u1 = 1e-12f;
-        float mag = stddev * sqrtf(-2.0f * logf(u1));
-        out[i] = mean + mag * cosf(2.0f * 3.14159265358979f * u2);
+        /* Box-Muller, cosine branch (tensor.c:325-339).  The product is
+         * formed as (stddev * cos) * radius: the order the reference's
+         * -ffast-math build evaluates it in, so seeded draws agree bit for
+         * bit with the reference for any stddev. */
+        float radius = sqrtf(-2.0f * logf(u1));
+        float c = cosf(2.0f * 3.14159265358979f * u2);
+        out[i] = mean + (stddev * c) * radius;
     }
 }
 

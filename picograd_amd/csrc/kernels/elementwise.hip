@@ -419,6 +419,9 @@ struct sgd_table {
 __device__ __forceinline__ void sgd_elem(float &p, float g, float &b, bool has_buf, float lr, float mu,
                                          float damp, float wd, int nesterov)
 {
+    // The reference's x86 build (-mavx2, no -mfma) rounds every product and
+    // sum separately; keeping them unfused here gives the same bits.
+#pragma clang fp contract(off)
     float gj = g;
     if (wd != 0.0f)
         gj = gj + wd * p;

@@ -1,0 +1,320 @@
+"""Writes the golden vectors under tests/golden/ from the reference's own
+CPU path.
+
+The reference is C11: oracle/ref.mk compiles its CPU sources, where they lie
+in the reference checkout, into oracle/_ref/libpicograd_ref.so (and its
+header-only converters into oracle/_ref/libref_convert.so).  This script
+calls that build through the reference's public C ABI and stores inputs and
+outputs as small .npz files (no pickles).  The committed fixtures are data
+only; the tests compare the oracle (oracle/liboracle.so) and, on the GPU,
+the MI355X library against them.
+
+    python tests/golden/make_golden.py      # needs oracle/_ref built
+
+Every case names the reference code it exercises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import sys
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+ROOT = HERE.parent.parent
+sys.path.insert(0, str(ROOT))
+sys.path.insert(0, str(ROOT / "tests"))
+
+from oracle_lib import REF_CONVERT_SO, REF_SO  # noqa: E402
+from picograd_amd.capi import BF16, F16, F32, PgLib, SgdCfg, shape_arg  # noqa: E402
+
+
+def ref_lib() -> PgLib:
+    if not REF_SO.exists():
+        raise SystemExit(f"{REF_SO} missing: build it with `make -C oracle ref`")
+    return PgLib(REF_SO, device=False)
+
+
+def rng_streams(R: PgLib) -> dict:
+    """pg_seed + pg_tensor_uniform/normal (core/tensor.c:289-339)."""
+    out = {}
+    for seed in (42, 43, 44, 45, 46, 0):
+        R.pg_seed(seed)
+        nd, sh = shape_arg((1000,))
+        t = R.pg_tensor_uniform(nd, sh, -1.0, 1.0)
+        out[f"uniform_{seed}"] = R.read(t)
+        R.pg_tensor_free(t)
+        t = R.pg_tensor_normal(nd, sh, 0.0, 1.0)
+        out[f"normal_{seed}"] = R.read(t)
+        R.pg_tensor_free(t)
+        t = R.pg_tensor_normal(nd, sh, 0.5, 0.02)
+        out[f"normal_sd002_{seed}"] = R.read(t)
+        R.pg_tensor_free(t)
+    return out
+
+
+def conversions() -> dict:
+    """convert.h:15-104 RNE converters: every 16-bit pattern decoded, and a
+    set of f32 inputs (specials, halfway cases, subnormals, random bits)
+    encoded."""
+    L = C.CDLL(str(REF_CONVERT_SO))
+    L.ref_f32_to_f16.restype = C.c_uint16
+    L.ref_f32_to_f16.argtypes = [C.c_float]
+    L.ref_f32_to_bf16.restype = C.c_uint16
+    L.ref_f32_to_bf16.argtypes = [C.c_float]
+    L.ref_f16_to_f32.restype = C.c_float
+    L.ref_f16_to_f32.argtypes = [C.c_uint16]
+    L.ref_bf16_to_f32.restype = C.c_float
+    L.ref_bf16_to_f32.argtypes = [C.c_uint16]
+    rng = np.random.default_rng(2024)
+    special = np.array([0x00000000, 0x80000000, 0x7F800000, 0xFF800000, 0x7FC00000, 0xFFC00001,
+                        0x7F800001, 0x7FBFFFFF, 0x00000001, 0x007FFFFF, 0x33000000, 0x33000001,
+                        0x387FC000, 0x38800000, 0x477FE000, 0x477FF000, 0x477FEFFF, 0x7F7FFFFF,
+                        0x3F808000, 0x3F818000, 0x3F808001, 0x3F7FFFFF, 0x3F800000, 0xBF808000,
+                        0x33800000, 0x337FFFFF, 0x387FE000, 0x387FF000, 0x38000000, 0x37800000],
+                       dtype=np.uint32)
+    rand_bits = rng.integers(0, 2**32, size=20000, dtype=np.uint64).astype(np.uint32)
+    # values around the f16 range and subnormal boundary, as floats
+    rand_vals = np.concatenate([rng.standard_normal(4000), rng.uniform(-70000, 70000, 2000),
+                                rng.uniform(-1e-4, 1e-4, 2000), rng.uniform(-7e-8, 7e-8, 1000)])
+    enc_in = np.concatenate([special, rand_bits, rand_vals.astype(np.float32).view(np.uint32)])
+    f = enc_in.view(np.float32)
+    to_f16 = np.array([L.ref_f32_to_f16(float(v)) for v in f], np.uint16)
+    to_bf16 = np.array([L.ref_f32_to_bf16(float(v)) for v in f], np.uint16)
+    allh = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    # ctypes returns Python floats: go through f32 bit patterns explicitly
+    f16_dec = np.array([L.ref_f16_to_f32(int(h)) for h in allh], np.float32).view(np.uint32)
+    bf16_dec = np.array([L.ref_bf16_to_f32(int(h)) for h in allh], np.float32).view(np.uint32)
+    return {"enc_in_bits": enc_in, "to_f16": to_f16, "to_bf16": to_bf16, "f16_dec_bits": f16_dec,
+            "bf16_dec_bits": bf16_dec}
+
+
+def _free(R, *nodes):
+    for n in nodes:
+        R.pg_node_free(n)
+
+
+def sgd_trajectories(R: PgLib) -> dict:
+    """pg_sgd_step (opt/sgd.c:111-162), three steps per configuration, the
+    grads set exactly through loss = sum_all(p * G)."""
+    cfgs = [(0.01, 0.9, 0.0, 1e-4, True), (0.1, 0.5, 0.3, 0.01, False), (0.05, 0.0, 0.0, 0.0, False),
+            (0.2, 0.7, 0.0, 0.05, True)]
+    rng = np.random.default_rng(11)
+    out = {"cfgs": np.array([c[:4] + (float(c[4]),) for c in cfgs], np.float32)}
+    for ci, (lr, mu, d, wd, nest) in enumerate(cfgs):
+        p0 = rng.standard_normal(257).astype(np.float32)
+        gs = rng.standard_normal((3, 257)).astype(np.float32)
+        p = R.var(p0)
+        opt = R.pg_sgd_new(C.byref(SgdCfg(lr, mu, d, wd, nest)))
+        R.pg_sgd_add_param(opt, p)
+        traj = []
+        for s in range(3):
+            R.pg_sgd_zero_grad(opt)
+            gn = R.var(gs[s], requires_grad=False)
+            prod = R.op("mul", p, gn)
+            loss = R.op("sum_all", prod)
+            R.pg_backward(loss)
+            _free(R, loss, prod, gn)
+            R.pg_sgd_step(opt)
+            traj.append(R.value(p))
+        R.pg_sgd_free(opt)
+        _free(R, p)
+        out[f"p0_{ci}"] = p0
+        out[f"g_{ci}"] = gs
+        out[f"traj_{ci}"] = np.stack(traj)
+    return out
+
+
+def chain1(R: PgLib) -> dict:
+    """Config 1 chain through the reference pg_backward, JIT on and off
+    (autograd.c:2483-2533; the fused loop of jit.c:399-583)."""
+    out = {}
+    R.pg_seed(42)
+    nd, sh = shape_arg((64, 64))
+    ts = [R.pg_tensor_uniform(nd, sh, -1.0, 1.0) for _ in range(3)]
+    a, b, c = (R.read(t) for t in ts)
+    for t in ts:
+        R.pg_tensor_free(t)
+    out.update(a=a, b=b, c=c)
+    for jit in (True, False):
+        R.pg_autograd_set_jit(jit)
+        na, nb, nc = R.var(a), R.var(b), R.var(c)
+        t0 = R.op("add", na, nb)
+        t1 = R.op("mul", t0, nc)
+        t2 = R.op("relu", t1)
+        t3 = R.op("tanh", t2)
+        loss = R.op("sum_all", t3)
+        R.pg_backward(loss)
+        tag = "jit" if jit else "eager"
+        # last_was_jit is only updated while the JIT is enabled (autograd.c:2499-2519)
+        assert not jit or R.pg_autograd_last_was_jit(), R.pg_autograd_last_error()
+        out[f"da_{tag}"], out[f"db_{tag}"], out[f"dc_{tag}"] = (R.grad(n) for n in (na, nb, nc))
+        out[f"loss_{tag}"] = R.value(loss)
+        _free(R, loss, t3, t2, t1, t0, na, nb, nc)
+    R.pg_autograd_set_jit(True)
+    return out
+
+
+def chain2(R: PgLib, rows=96, cols=160) -> dict:
+    """Config 2 chain at a reduced shape: hybrid JIT (mul, sigmoid) + eager
+    GELU' + serial broadcast reduction for dbias (autograd.c:364-387)."""
+    out = {}
+    R.pg_seed(43)
+    nd, sh = shape_arg((rows, cols))
+    tx = R.pg_tensor_normal(nd, sh, 0.0, 1.0)
+    x = R.read(tx)
+    ndb, shb = shape_arg((cols,))
+    tb = R.pg_tensor_normal(ndb, shb, 0.0, 0.1)
+    bias = R.read(tb)
+    tg = R.pg_tensor_normal(nd, sh, 0.0, 1.0)
+    g = R.read(tg)
+    for t in (tx, tb, tg):
+        R.pg_tensor_free(t)
+    out.update(x=x, bias=bias, g=g)
+    for jit in (True, False):
+        R.pg_autograd_set_jit(jit)
+        nx, nb, ng = R.var(x), R.var(bias), R.var(g)
+        t0 = R.op("add", nx, nb)
+        t1 = R.op("gelu", t0)
+        t2 = R.op("sigmoid", ng)
+        y = R.op("mul", t1, t2)
+        loss = R.op("sum_all", y)
+        R.pg_backward(loss)
+        tag = "jit" if jit else "eager"
+        out[f"dx_{tag}"], out[f"dg_{tag}"], out[f"dbias_{tag}"] = (R.grad(n) for n in (nx, ng, nb))
+        out[f"loss_{tag}"] = R.value(loss)
+        out[f"was_jit_{tag}"] = np.array(bool(R.pg_autograd_last_was_jit()))
+        _free(R, loss, y, t2, t1, t0, nx, nb, ng)
+    R.pg_autograd_set_jit(True)
+    return out
+
+
+GEMM_SHAPES = [(129, 96, 40), (17, 33, 9), (1, 1, 8), (64, 64, 64), (33, 70, 257)]
+
+
+def gemms(R: PgLib) -> dict:
+    """pg_gemm_ex / pg_hgemm / pg_bgemm (backend.c:150-192 -> gemm.c:575-629):
+    C = A.B from 16-bit operands with f32 accumulation, C overwritten."""
+    out = {}
+    rng = np.random.default_rng(5)
+    for dt, name in ((F16, "f16"), (BF16, "bf16")):
+        for (m, n, k) in GEMM_SHAPES:
+            a = rng.standard_normal((m, k)).astype(np.float32)
+            b = rng.standard_normal((k, n)).astype(np.float32)
+            if dt == F16:
+                a16 = a.astype(np.float16).view(np.uint16)
+                b16 = b.astype(np.float16).view(np.uint16)
+            else:  # RNE to bf16 on the bits (finite inputs)
+                a16 = _bf16(a)
+                b16 = _bf16(b)
+            c = np.full((m, n), np.nan, np.float32)
+            R.pg_gemm_ex(dt, m, n, k, a16.ctypes.data, k, b16.ctypes.data, n, c.ctypes.data, n)
+            key = f"{name}_{m}_{n}_{k}"
+            out[f"{key}_a"], out[f"{key}_b"], out[f"{key}_c"] = a16, b16, c
+    f = rng.standard_normal((7, 5)).astype(np.float32), rng.standard_normal((5, 3)).astype(np.float32)
+    c = np.zeros((7, 3), np.float32)
+    R.pg_gemm(7, 3, 5, f[0].ctypes.data, 5, f[1].ctypes.data, 3, c.ctypes.data, 3)
+    out.update(f32_a=f[0], f32_b=f[1], f32_c=c)
+    # which f16 micro the reference picked (gemm.c:277-284): AVX512-FP16
+    # hosts run hgemm_avx512fp16_micro, which drops the accumulator of the
+    # first 16 columns of each 32-column strip between KC=256 k-blocks
+    flags = Path("/proc/cpuinfo").read_text()
+    out["host_avx512fp16"] = np.array("avx512_fp16" in flags)
+    return out
+
+
+def _bf16(x: np.ndarray) -> np.ndarray:
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+MM_SHAPES = [(65, 40, 33), (8, 16, 24), (130, 72, 20)]
+
+
+def matmul_backward(R: PgLib) -> dict:
+    """bwd_matmul (autograd.c:561-706) with bf16 and f16 leaves: loss =
+    sum_all(matmul(A, W) * G) makes dC = G.  G is chosen exactly
+    representable in the operand dtype, so rounding dC to the operand dtype
+    is the identity and the grads are exact products accumulated in f32."""
+    out = {}
+    rng = np.random.default_rng(9)
+    for dt, name in ((F16, "f16"), (BF16, "bf16")):
+        for (M, K, N) in MM_SHAPES:
+            a = rng.standard_normal((M, K)).astype(np.float32)
+            w = (0.02 * rng.standard_normal((K, N))).astype(np.float32)
+            g = rng.standard_normal((M, N)).astype(np.float32)
+            if dt == F16:
+                a16, w16 = a.astype(np.float16).view(np.uint16), w.astype(np.float16).view(np.uint16)
+                g = g.astype(np.float16).astype(np.float32)
+            else:
+                a16, w16 = _bf16(a), _bf16(w)
+                g = (_bf16(g).astype(np.uint32) << 16).view(np.float32)
+            R.pg_autograd_set_jit(False)
+            na, nw = R.var(a16, dtype=dt), R.var(w16, dtype=dt)
+            c = R.op("matmul", na, nw)
+            ng = R.var(g, requires_grad=False)
+            prod = R.op("mul", c, ng)
+            loss = R.op("sum_all", prod)
+            R.pg_backward(loss)
+            key = f"{name}_{M}_{K}_{N}"
+            out[f"{key}_a"], out[f"{key}_w"], out[f"{key}_g"] = a16, w16, g
+            out[f"{key}_c"] = R.value(c)
+            out[f"{key}_da"], out[f"{key}_dw"] = R.grad(na), R.grad(nw)
+            _free(R, loss, prod, ng, c, na, nw)
+            R.pg_autograd_set_jit(True)
+    # batched f32: bmm-style [B, M, K] . [B, K, N]
+    a = rng.standard_normal((3, 9, 7)).astype(np.float32)
+    w = rng.standard_normal((3, 7, 5)).astype(np.float32)
+    g = rng.standard_normal((3, 9, 5)).astype(np.float32)
+    na, nw = R.var(a), R.var(w)
+    c = R.op("matmul", na, nw)
+    ng = R.var(g, requires_grad=False)
+    prod = R.op("mul", c, ng)
+    loss = R.op("sum_all", prod)
+    R.pg_backward(loss)
+    out.update(bmm_a=a, bmm_w=w, bmm_g=g, bmm_c=R.value(c), bmm_da=R.grad(na), bmm_dw=R.grad(nw))
+    _free(R, loss, prod, ng, c, na, nw)
+    return out
+
+
+def mse(R: PgLib) -> dict:
+    """pg_ag_mse(pred, target, mean) (autograd.c:1758-1771) over a [6, 10]
+    prediction: the mean divides by the last axis only (reduce_all,
+    autograd.c:1018-1043)."""
+    rng = np.random.default_rng(3)
+    pred = rng.standard_normal((6, 10)).astype(np.float32)
+    tgt = rng.standard_normal((6, 10)).astype(np.float32)
+    out = {"pred": pred, "tgt": tgt}
+    for mean in (True, False):
+        npd, nt = R.var(pred), R.var(tgt, requires_grad=False)
+        loss = R.pg_ag_mse(npd, nt, mean)
+        R.pg_backward(loss)
+        tag = "mean" if mean else "sum"
+        out[f"loss_{tag}"] = R.value(loss)
+        out[f"dpred_{tag}"] = R.grad(npd)
+        _free(R, loss, npd, nt)
+    return out
+
+
+def main() -> int:
+    R = ref_lib()
+    cases = {
+        "rng": rng_streams(R),
+        "convert": conversions(),
+        "sgd": sgd_trajectories(R),
+        "chain1": chain1(R),
+        "chain2": chain2(R),
+        "gemm": gemms(R),
+        "matmul_bwd": matmul_backward(R),
+        "mse": mse(R),
+    }
+    for name, arrays in cases.items():
+        path = HERE / f"{name}.npz"
+        np.savez_compressed(path, **arrays)
+        print(f"wrote {path.relative_to(ROOT)} ({path.stat().st_size} bytes)")
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

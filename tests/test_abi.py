@@ -1,0 +1,162 @@
+"""The C-ABI library on the CPU: it loads, exports every function the public
+headers declare, links nothing of the oracle, and its host-only logic
+(JIT graph building, hashing, codegen + hiprtc compile) works without a
+GPU.  No test here launches device work."""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+import picograd_amd
+from picograd_amd.capi import shape_arg
+
+ROOT = Path(__file__).resolve().parent.parent
+INCLUDE = ROOT / "include" / "picograd"
+LIB = ROOT / "picograd_amd" / "lib" / "libpicograd_amd.so"
+
+_DECL = re.compile(r"^(?!\s*(?:static|typedef|#|\*|/))[A-Za-z_][\w\s\*]*?\b(pg_\w+)\s*\(", re.M)
+
+
+def declared_functions() -> dict[str, list[str]]:
+    out = {}
+    for h in sorted(INCLUDE.glob("*.h")):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        text = re.sub(r"//[^\n]*", "", text)
+        names = sorted(set(_DECL.findall(text)))
+        out[h.name] = names
+    return out
+
+
+def test_headers_declare_the_reference_abi():
+    decl = declared_functions()
+    every = {n for v in decl.values() for n in v}
+    # the reference entry points the drop-in must keep (autograd.h, jit.h,
+    # sgd.h, backend.h, tensor.h of the reference)
+    for name in ("pg_backward", "pg_backward_jit", "pg_ag_add", "pg_ag_matmul", "pg_ag_mse", "pg_ag_gelu",
+                 "pg_jit_compile", "pg_jit_run", "pg_jit_run_single", "pg_jit_graph_hash",
+                 "pg_sgd_new", "pg_sgd_step", "pg_sgd_zero_grad", "pg_gemm", "pg_gemm_ex", "pg_hgemm",
+                 "pg_bgemm", "pg_seed", "pg_tensor_uniform", "pg_tensor_normal", "pg_var_from_data"):
+        assert name in every, name
+    assert len(every) > 100
+
+
+def test_library_exports_every_declared_function():
+    lib = C.CDLL(str(LIB))
+    missing = [(h, n) for h, names in declared_functions().items() for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_library_does_not_link_the_oracle():
+    syms = subprocess.run(["nm", "-D", "--defined-only", str(LIB)], capture_output=True, text=True,
+                          check=True).stdout
+    assert "orc_" not in syms
+    deps = subprocess.run(["ldd", str(LIB)], capture_output=True, text=True).stdout
+    assert "oracle" not in deps and "picograd_ref" not in deps
+    assert "libamdhip64" in deps and "libhiprtc" in deps
+
+
+def test_kernels_are_built_for_gfx950_only(tmp_path):
+    """The fat binary embedded in the library carries gfx950 code objects
+    and no other GPU target."""
+    fatbin = tmp_path / "fatbin"
+    r = subprocess.run(["objcopy", "-O", "binary", "--only-section=.hip_fatbin", str(LIB), str(fatbin)],
+                       capture_output=True, text=True)
+    if r.returncode != 0 or not fatbin.exists():
+        pytest.skip("objcopy unavailable")
+    data = fatbin.read_bytes()
+    targets = set(re.findall(rb"amdgcn-amd-amdhsa--(gfx\w+)", data))
+    assert targets == {b"gfx950"}, targets
+
+
+@pytest.fixture(scope="module")
+def host_lib(tmp_path_factory):
+    os.environ["PG_JIT_CACHE_DIR"] = str(tmp_path_factory.mktemp("jitcache"))
+    return picograd_amd.load()
+
+
+def _graph(L, build):
+    g = L.pg_jit_graph_new()
+    out = build(g)
+    if out is not None:
+        L.pg_jit_mark_output(g, out)
+    return g
+
+
+def test_jit_graph_building_and_errors(host_lib):
+    """test_jit.c:270-296: invalid ids fail with -1, a graph without
+    outputs does not compile, broadcasting follows numpy rules."""
+    L = host_lib
+    g = L.pg_jit_graph_new()
+    assert L.pg_jit_add(g, 999, 1000) == -1
+    assert L.pg_jit_compile(g) is None
+    a = L.pg_jit_add_input(g, *shape_arg((2, 4)))
+    b = L.pg_jit_add_input(g, *shape_arg((4,)))
+    c = L.pg_jit_add_input(g, *shape_arg((3,)))
+    assert L.pg_jit_add(g, a, b) >= 0
+    assert L.pg_jit_add(g, a, c) == -1  # 4 vs 3 does not broadcast
+    assert L.pg_jit_num_inputs(g) == 3 and L.pg_jit_num_nodes(g) == 4
+    ins = (C.c_int * 1)(a)
+    assert L.pg_jit_add_op(g, 0, ins, 1) == -1  # binary op with one input
+    L.pg_jit_graph_free(g)
+
+
+def test_jit_hash_is_structural(host_lib):
+    L = host_lib
+
+    def build(shape, op):
+        def f(g):
+            a = L.pg_jit_add_input(g, *shape_arg(shape))
+            b = L.pg_jit_add_input(g, *shape_arg(shape))
+            return op(g, a, b)
+        return f
+    g1 = _graph(L, build((4, 4), L.pg_jit_add))
+    g2 = _graph(L, build((4, 4), L.pg_jit_add))
+    g3 = _graph(L, build((4, 4), L.pg_jit_mul))
+    g4 = _graph(L, build((4, 5), L.pg_jit_add))
+    h = [L.pg_jit_graph_hash(g) for g in (g1, g2, g3, g4)]
+    assert h[0] == h[1] and len(set(h)) == 3
+    for g in (g1, g2, g3, g4):
+        L.pg_jit_graph_free(g)
+
+
+def test_jit_codegen_compiles_for_gfx950_without_a_gpu(host_lib):
+    """pg_jit_compile generates HIP source and compiles it with hiprtc for
+    gfx950 before it needs the device: on this CPU-only host it stops at
+    the module load, after writing the code object to the cache."""
+    L = host_lib
+    cache = Path(os.environ["PG_JIT_CACHE_DIR"])
+    before = set(cache.glob("*.hsaco"))
+
+    def chain(g):  # the config-1 chain plus a broadcast bias, every op kind
+        a = L.pg_jit_add_input(g, *shape_arg((64, 64)))
+        b = L.pg_jit_add_input(g, *shape_arg((64,)))
+        x = L.pg_jit_relu(g, L.pg_jit_mul(g, L.pg_jit_add(g, a, b), a))
+        for op in (L.pg_jit_tanh, L.pg_jit_gelu, L.pg_jit_sigmoid, L.pg_jit_erf, L.pg_jit_exp, L.pg_jit_abs,
+                   L.pg_jit_sin, L.pg_jit_cos, L.pg_jit_neg, L.pg_jit_step):
+            x = op(g, x)
+        x = L.pg_jit_div(g, L.pg_jit_sub(g, x, L.pg_jit_add_const(g, 0.5)), L.pg_jit_add_const(g, 3.0))
+        return L.pg_jit_sqrt(g, L.pg_jit_log(g, L.pg_jit_add(g, L.pg_jit_abs(g, x),
+                                                               L.pg_jit_add_const(g, 1.0))))
+    g = _graph(L, chain)
+    exe = L.pg_jit_compile(g)
+    if exe is None:
+        err = L.pg_jit_last_error().decode()
+        assert "no device" in err, err
+        assert set(cache.glob("*.hsaco")) - before, "no code object was written"
+    else:  # a GPU is present
+        L.pg_jit_exe_free(exe)
+    L.pg_jit_graph_free(g)
+    # a compile error surfaces as NULL plus the hiprtc log
+    os.environ["PG_JIT_FORCE_COMPILE_ERROR"] = "1"
+    try:
+        g = _graph(L, lambda g: L.pg_jit_neg(g, L.pg_jit_add_input(g, *shape_arg((5,)))))
+        assert L.pg_jit_compile(g) is None
+        assert "hiprtc compile failed" in L.pg_jit_last_error().decode()
+        L.pg_jit_graph_free(g)
+    finally:
+        del os.environ["PG_JIT_FORCE_COMPILE_ERROR"]

@@ -1,9 +1,10 @@
 """GPU parity of the MI355X path against the CPU oracle, through the C ABI.
 
 Tolerances: f32 elementwise grads max relative
-error <= 1e-5 (with a floor of 1e-5 * max|ref| where grads pass through
-zero); f16/bf16 GEMM grads relative Frobenius <= 1e-3 against the
-f32-accumulating oracle on the same 16-bit operands; SGD weights <= 1e-6.
+error <= 1e-5 (oracle_lib.max_rel: elements below 1% of max|ref| are held
+to 1e-7 * max|ref| absolute, where grads pass through zero); f16/bf16 GEMM
+grads relative Frobenius <= 1e-3 against the f32-accumulating oracle on the
+same 16-bit operands; SGD weights <= 1e-6 relative, and in fact bit-exact.
 """
 import ctypes as C
 
@@ -60,6 +61,8 @@ def test_sgd_multi_tensor_matches_oracle(lib, oracle, cfg):
             got = lib.value(n)
             err = np.abs(got - rp) / np.maximum(np.abs(rp), 1e-30)
             assert err.max() <= SGD_TOL, f"step {step}: max rel {err.max():.3e}"
+            # neither side fuses multiply-adds: the weights agree bit for bit
+            assert np.array_equal(got.view(np.uint32), rp.view(np.uint32)), f"step {step}"
     lib.pg_sgd_free(opt)
     for n in nodes:
         lib.pg_node_free(n)

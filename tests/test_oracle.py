@@ -1,0 +1,296 @@
+"""The CPU oracle pinned against the reference's own outputs (CPU only).
+
+tests/golden/*.npz were written by tests/golden/make_golden.py from the
+reference's CPU path compiled from its sources (oracle/_ref).  Each test
+below checks one oracle function against those vectors, against the
+reference's known answers, or against what the mathematics fixes, and
+some plant a plausible mistake in a copy of the oracle's arithmetic to show
+the check would catch it.
+"""
+from __future__ import annotations
+
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle_lib import bf16_to_f32, max_rel, rel_fro
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+F16, BF16 = 1, 2
+
+
+def golden(name: str) -> dict:
+    with np.load(GOLDEN / f"{name}.npz", allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+# ---------------------------------------------------------------- RNG
+
+@pytest.mark.parametrize("seed", [42, 43, 44, 45, 46, 0])
+def test_rng_streams_bit_exact(oracle, seed):
+    """splitmix64 + Box-Muller (tensor.c:289-339) reproduce the reference's
+    streams bit for bit, seeds of every config and the zero-seed default."""
+    g = golden("rng")
+    oracle.orc_seed(seed)
+    u = oracle.uniform(1000, -1.0, 1.0)
+    n = oracle.normal(1000, 0.0, 1.0)
+    n2 = oracle.normal(1000, 0.5, 0.02)
+    assert np.array_equal(u.view(np.uint32), g[f"uniform_{seed}"].view(np.uint32))
+    assert np.array_equal(n.view(np.uint32), g[f"normal_{seed}"].view(np.uint32))
+    assert np.array_equal(n2.view(np.uint32), g[f"normal_sd002_{seed}"].view(np.uint32))
+
+
+def test_rng_moments(oracle):
+    oracle.orc_seed(7)
+    u = oracle.uniform(200000, -1.0, 1.0)
+    n = oracle.normal(200000, 0.0, 1.0)
+    assert u.min() >= -1.0 and u.max() < 1.0
+    assert abs(u.mean()) < 0.01 and abs(n.mean()) < 0.01 and abs(n.std() - 1.0) < 0.01
+
+
+# ---------------------------------------------------------------- conversions
+
+def test_decode_every_16bit_pattern(oracle):
+    g = golden("convert")
+    lib = oracle.lib
+    h = np.arange(65536, dtype=np.uint32)
+    f16 = np.array([oracle.orc_f16_to_f32(int(x)) for x in h], np.float32).view(np.uint32)
+    bf = np.array([oracle.orc_bf16_to_f32(int(x)) for x in h], np.float32).view(np.uint32)
+    assert np.array_equal(f16, g["f16_dec_bits"])
+    assert np.array_equal(bf, g["bf16_dec_bits"])
+    # finite f16 decode agrees with numpy's IEEE half
+    fin = (h & 0x7C00) != 0x7C00
+    ref = h.astype(np.uint16).view(np.float16).astype(np.float32).view(np.uint32)
+    assert np.array_equal(f16[fin], ref[fin])
+    del lib
+
+
+def test_encode_matches_reference(oracle):
+    g = golden("convert")
+    f = g["enc_in_bits"].view(np.float32)
+    to16 = np.empty(f.size, np.uint16)
+    tob = np.empty(f.size, np.uint16)
+    oracle.orc_cast_f32(F16, f.ctypes.data, to16.ctypes.data, f.size)
+    oracle.orc_cast_f32(BF16, f.ctypes.data, tob.ctypes.data, f.size)
+    # bf16: bit-exact for every non-NaN input.  The reference source maps a
+    # NaN to the quiet NaN 0x7FC0 | bit 16 (convert.h:89-92) and the oracle
+    # does so too; the reference's own -ffast-math build folds that test
+    # away (finite-math) and rounds NaN bits like numbers instead.
+    nan = np.isnan(f)
+    assert np.array_equal(tob[~nan], g["to_bf16"][~nan])
+    assert np.all(tob[nan] == (0x7FC0 | ((g["enc_in_bits"][nan] >> 16) & 1)))
+    # f16: the reference's subnormal branch (convert.h:31-42) shifts the
+    # 24-bit significand by 1-e instead of 1-e+13, so its results for
+    # 2^-25 <= |x| < 2^-14 are not f16 values of x.  The oracle (and the
+    # device cast) round those IEEE-correctly; everywhere else they agree
+    # with the reference bit for bit.
+    ex = (g["enc_in_bits"] >> 23) & 0xFF
+    sub = (ex >= 127 - 25) & (ex <= 127 - 15)
+    keep = ~sub & ~nan  # NaN payloads: the same finite-math caveat as bf16
+    assert np.array_equal(to16[keep], g["to_f16"][keep])
+    assert sub.sum() > 100 and not np.array_equal(to16[sub], g["to_f16"][sub])
+    # finite values that stay finite: IEEE round-to-nearest-even (numpy) agrees
+    fin = np.isfinite(f) & (np.abs(f) < 65504.0)
+    assert np.array_equal(to16[fin], f[fin].astype(np.float16).view(np.uint16))
+
+
+def test_bf16_rounding_planted_mistake_is_caught():
+    """Truncation instead of RNE (a plausible slip) disagrees with the
+    reference on the fixture's halfway and random inputs."""
+    g = golden("convert")
+    bits = g["enc_in_bits"]
+    fin = (bits & 0x7F800000) != 0x7F800000
+    trunc = (bits >> 16).astype(np.uint16)
+    assert not np.array_equal(trunc[fin], g["to_bf16"][fin])
+
+
+# ---------------------------------------------------------------- SGD
+
+def test_sgd_trajectories_bit_exact(oracle):
+    """Three steps of pg_sgd_step (sgd.c:111-162) under four configurations
+    reproduce the reference's weights exactly."""
+    g = golden("sgd")
+    for ci, (lr, mu, d, wd, nest) in enumerate(g["cfgs"]):
+        p = g[f"p0_{ci}"].copy()
+        buf = np.zeros_like(p)
+        for s in range(3):
+            oracle.sgd_step(p, g[f"g_{ci}"][s].copy(), buf if mu else None, lr, mu, d, wd, bool(nest))
+            assert np.array_equal(p.view(np.uint32), g[f"traj_{ci}"][s].view(np.uint32)), (ci, s)
+
+
+def test_sgd_known_answers(oracle):
+    """test_opt.c:48-138: plain, momentum, weight decay and Nesterov runs."""
+    def run(lr, mu, d, wd, nest, steps, grad):
+        p = np.array([1.0], np.float32)
+        buf = np.zeros(1, np.float32)
+        out = []
+        for _ in range(steps):
+            oracle.sgd_step(p, np.array([grad(p[0])], np.float32), buf if mu else None, lr, mu, d, wd, nest)
+            out.append(float(p[0]))
+        return out
+    g2 = lambda x: 2.0 * (x - 2.0)
+    assert np.allclose(run(0.1, 0, 0, 0, False, 2, g2), [1.2, 1.36], atol=1e-5)
+    assert np.allclose(run(0.1, 0.9, 0, 0, False, 2, g2), [1.2, 1.54], atol=1e-5)
+    assert np.allclose(run(0.1, 0, 0, 0.5, False, 1, lambda x: 2.0 * x), [0.75], atol=1e-5)
+    assert np.allclose(run(0.1, 0.5, 0, 0, True, 2, g2), [1.3, 1.56], atol=1e-5)
+
+
+def test_sgd_planted_mistake_is_caught():
+    """Nesterov with buf alone (dropping the g' term) misses the fixture."""
+    g = golden("sgd")
+    lr, mu, d, wd, _ = g["cfgs"][0]
+    p = g["p0_0"].astype(np.float32)
+    gj = g["g_0"][0] + np.float32(wd) * p
+    buf = np.float32(1 - d) * gj
+    wrong = p - np.float32(lr) * (np.float32(mu) * buf)
+    assert np.abs(wrong - g["traj_0"][0]).max() > 1e-5
+
+
+# ---------------------------------------------------------------- elementwise chains
+
+def test_chain1_matches_reference(oracle):
+    g = golden("chain1")
+    da, db, dc = oracle.chain1(g["a"].ravel().copy(), g["b"].ravel().copy(), g["c"].ravel().copy())
+    for tag in ("jit", "eager"):
+        assert max_rel(da, g[f"da_{tag}"].ravel()) <= 1e-6
+        assert max_rel(db, g[f"db_{tag}"].ravel()) <= 1e-6
+        assert max_rel(dc, g[f"dc_{tag}"].ravel()) <= 1e-6
+
+
+def test_chain1_closed_form_and_planted_mistake(oracle):
+    """tanh' = 1 - tanh^2 against d/dx tanh = sech^2 in f64; a tanh' that
+    forgets the square fails the 1e-5 bar."""
+    g = golden("chain1")
+    a, b, c = (g[k].astype(np.float64).ravel() for k in "abc")
+    t0 = a + b
+    t1 = t0 * c
+    step = (t1 > 0).astype(np.float64)
+    sech2 = 1.0 / np.cosh(np.maximum(t1, 0)) ** 2
+    dc64 = sech2 * step * t0
+    da64 = sech2 * step * c
+    da, db, dc = oracle.chain1(g["a"].ravel().copy(), g["b"].ravel().copy(), g["c"].ravel().copy())
+    assert max_rel(da, da64) <= 1e-5 and max_rel(dc, dc64) <= 1e-5
+    wrong = (1.0 - np.tanh(np.maximum(t1, 0))) * step * c
+    assert max_rel(wrong, g["da_jit"].ravel()) > 1e-2
+
+
+def test_chain2_matches_reference(oracle):
+    g = golden("chain2")
+    x, bias, gg = g["x"], g["bias"], g["g"]
+    R, Cc = x.shape
+    dx, dg, db, db64 = oracle.chain2(x.copy(), bias.copy(), gg.copy())
+    for tag in ("jit", "eager"):
+        assert max_rel(dx, g[f"dx_{tag}"]) <= 1e-5
+        assert max_rel(dg, g[f"dg_{tag}"]) <= 1e-5
+        bound = 4 * R * np.finfo(np.float32).eps * np.abs(dx).sum(axis=0) + 1e-30
+        assert np.all(np.abs(g[f"dbias_{tag}"] - db64) <= bound)
+    assert np.all(np.abs(db - db64) <= 4 * R * np.finfo(np.float32).eps * np.abs(dx).sum(axis=0))
+
+
+def test_chain2_gelu_grad_closed_form_and_planted_mistake(oracle):
+    """GELU'(x) = Phi(x) + x phi(x) in f64; dropping the x phi(x) term (a
+    plausible slip) fails the bar."""
+    g = golden("chain2")
+    x, bias, gg = (g[k].astype(np.float64) for k in ("x", "bias", "g"))
+    t0 = x + bias
+    Phi = 0.5 * (1.0 + np.vectorize(math.erf)(t0 / math.sqrt(2.0)))
+    phi = np.exp(-0.5 * t0 * t0) / math.sqrt(2.0 * math.pi)
+    s = 1.0 / (1.0 + np.exp(-gg))
+    dx64 = s * (Phi + t0 * phi)
+    dg64 = t0 * Phi * s * (1.0 - s)
+    dx, dg, _, _ = oracle.chain2(g["x"].copy(), g["bias"].copy(), g["g"].copy())
+    assert max_rel(dx, dx64) <= 1e-5 and max_rel(dg, dg64) <= 1e-5
+    assert max_rel(s * Phi, g["dx_jit"]) > 1e-3
+
+
+# ---------------------------------------------------------------- GEMM
+
+def _gemm_keys(g):
+    return sorted({k.rsplit("_", 1)[0] for k in g if k[:3] in ("f16", "bf1")})
+
+
+def test_gemm_ex_matches_reference(oracle):
+    """pg_gemm_ex / hgemm / bgemm (gemm.c:575-629): the oracle's f32
+    accumulation of upcast operands agrees with the reference up to
+    summation order, and both sit within f32 bounds of an f64 sum."""
+    g = golden("gemm")
+    for key in _gemm_keys(g):
+        dt = F16 if key.startswith("f16") else BF16
+        a, b, c = g[f"{key}_a"], g[f"{key}_b"], g[f"{key}_c"]
+        mine = oracle.gemm(dt, a, b)
+        ref64 = oracle.gemm(dt, a, b, f64=True)
+        k = a.shape[1]
+        if dt == F16 and k > 256 and bool(g["host_avx512fp16"]):
+            # the reference's AVX512-FP16 micro (hgemm_avx512fp16.c:22-34)
+            # resets the accumulator of columns 0-15 of every 32-column
+            # strip at each KC=256 block, so those columns hold only the
+            # last block's products; the other columns are the full sum.
+            # Hosts without AVX512-FP16 run the scalar micro, which is right.
+            lo = (np.arange(c.shape[1]) % 32) < 16
+            kk = (k - 1) // 256 * 256
+            last = oracle.gemm(dt, np.ascontiguousarray(a[:, kk:]), np.ascontiguousarray(b[kk:, :]))
+            assert rel_fro(last[:, lo], c[:, lo]) <= 1e-6, key
+            assert rel_fro(mine[:, ~lo], c[:, ~lo]) <= 1e-6, key
+            continue
+        assert rel_fro(mine, c) <= 1e-6, key
+        assert rel_fro(c, ref64) <= 2 * k * 6e-8 + 1e-7, key
+        assert rel_fro(mine, ref64) <= 2 * k * 6e-8 + 1e-7, key
+    a, b = g["f32_a"], g["f32_b"]
+    assert np.allclose(oracle.gemm(0, a, b), g["f32_c"], rtol=1e-6, atol=1e-6)
+
+
+def test_gemm_brute_force_and_transpose_flags(oracle):
+    """op(A)op(B) with the transpose flags against numpy f64 on ragged
+    shapes; a transposed operand would fail."""
+    rng = np.random.default_rng(1)
+    for (m, n, k) in [(5, 7, 3), (1, 9, 17), (13, 1, 4)]:
+        a = rng.standard_normal((m, k)).astype(np.float32)
+        b = rng.standard_normal((k, n)).astype(np.float32)
+        a16, b16 = oracle.cast16(BF16, a), oracle.cast16(BF16, b)
+        af, bf = bf16_to_f32(a16).astype(np.float64), bf16_to_f32(b16).astype(np.float64)
+        want = af @ bf
+        assert rel_fro(oracle.gemm(BF16, a16, b16), want) <= 1e-6
+        assert rel_fro(oracle.gemm(BF16, np.ascontiguousarray(a16.T), b16, ta=True), want) <= 1e-6
+        assert rel_fro(oracle.gemm(BF16, a16, np.ascontiguousarray(b16.T), tb=True), want) <= 1e-6
+        if m == n == k:
+            assert rel_fro(oracle.gemm(BF16, a16, b16, ta=True), want) > 1e-2
+
+
+def test_matmul_backward_matches_reference(oracle):
+    """bwd_matmul (autograd.c:561-706) on 16-bit leaves with dC exactly
+    representable: dA = dC.W^T and dW = A^T.dC from the oracle agree with
+    the reference up to summation order."""
+    g = golden("matmul_bwd")
+    keys = sorted({k.rsplit("_", 1)[0] for k in g if k.startswith(("f16", "bf16"))})
+    for key in keys:
+        dt = F16 if key.startswith("f16") else BF16
+        a, w, gr = g[f"{key}_a"], g[f"{key}_w"], g[f"{key}_g"]
+        g16 = oracle.cast16(dt, gr)
+        da = oracle.gemm(dt, g16, w, tb=True)
+        dw = oracle.gemm(dt, a, g16, ta=True)
+        assert rel_fro(da, g[f"{key}_da"]) <= 1e-6, key
+        assert rel_fro(dw, g[f"{key}_dw"]) <= 1e-6, key
+        assert rel_fro(oracle.gemm(dt, a, w), g[f"{key}_c"]) <= 1e-6, key
+    a, w, gr = g["bmm_a"], g["bmm_w"], g["bmm_g"]
+    da = np.einsum("bmn,bkn->bmk", gr.astype(np.float64), w.astype(np.float64))
+    dw = np.einsum("bmk,bmn->bkn", a.astype(np.float64), gr.astype(np.float64))
+    assert rel_fro(g["bmm_da"], da) <= 1e-6 and rel_fro(g["bmm_dw"], dw) <= 1e-6
+
+
+# ---------------------------------------------------------------- losses
+
+def test_mse_scale_matches_reference(oracle):
+    """mean_all divides by the last axis only: mse grad = 2 (p - t) / 10
+    on [6, 10] (autograd.c:1018-1043, :1758-1771)."""
+    import ctypes as C
+    g = golden("mse")
+    d = g["pred"] - g["tgt"]
+    shape = (C.c_size_t * 2)(6, 10)
+    s_mean = oracle.orc_mse_grad_scale(2, shape, True)
+    s_sum = oracle.orc_mse_grad_scale(2, shape, False)
+    assert np.allclose(s_mean * d, g["dpred_mean"], rtol=1e-6, atol=0)
+    assert np.allclose(s_sum * d, g["dpred_sum"], rtol=1e-6, atol=0)
+    assert np.allclose(g["loss_mean"], (d.astype(np.float64) ** 2).sum() / 10, rtol=1e-5)
+    assert not np.allclose(2.0 / 60 * d, g["dpred_mean"], rtol=1e-3)
