@@ -81,6 +81,25 @@ def timer_ms(lib, kind):
     return total, cnt.value
 
 
+# ---------------------------------------------------------------- counter calibration
+
+CALIB_ROWS, CALIB_COLS = 16384, 4096
+
+
+def calibrate_copy(L, reps=3):
+    """pg_ag_neg over an f32 [16384, 4096] leaf: the k_unary kernel reads
+    256 MiB and writes 256 MiB, a copy of known size whose FETCH_SIZE and
+    WRITE_SIZE readings scale the fused kernel's."""
+    shp = (C.c_size_t * 2)(CALIB_ROWS, CALIB_COLS)
+    x = L.pg_var_full(2, shp, 1.5, False)
+    for _ in range(reps):
+        y = L.pg_ag_neg(x)
+        L.pg_node_free(y)
+    L.sync()
+    L.pg_node_free(x)
+    log(f"[calib] k_unary copy of {CALIB_ROWS * CALIB_COLS * 4} B read + write, {reps} launches")
+
+
 # ---------------------------------------------------------------- config 2
 
 def c2_inputs(R, Cc, seed=43):
@@ -280,6 +299,8 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="c2,c3,c1")
+    ap.add_argument("--calib", action="store_true",
+                    help="first run a plain copy kernel of known size (the HBM counter calibration)")
     a = ap.parse_args(argv)
     if a.gpus != 1:
         print(f"bench.py measures one GPU only (every box here has one); --gpus {a.gpus} is not supported",
@@ -292,6 +313,8 @@ def main(argv=None):
     ev = HipEvents(L.pg_amd_stream())
     only = set(a.only.split(","))
     extra = {}
+    if a.calib:
+        calibrate_copy(L)
     c2 = bench_c2(L, ev, a.steps, a.warmup)
     log(f"[c2] {c2}")
     if "c3" in only:

@@ -75,6 +75,7 @@ _PROTOS = {
     "pg_var_from_data": (vp, [sz, SZP, vp, bo]),
     "pg_var_from_tensor": (vp, [vp, bo]),
     "pg_var_zeros": (vp, [sz, SZP, bo]),
+    "pg_var_full": (vp, [sz, SZP, fl, bo]),
     "pg_var_uniform": (vp, [sz, SZP, fl, fl, bo]),
     "pg_var_normal": (vp, [sz, SZP, fl, fl, bo]),
     "pg_var_scalar": (vp, [fl, bo]),
