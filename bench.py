@@ -23,10 +23,14 @@ timed on this host over a bounded sample of the same workload.
 from __future__ import annotations
 
 import argparse
+import csv
 import ctypes as C
 import json
 import os
+import shutil
+import subprocess
 import sys
+import tempfile
 import time
 from pathlib import Path
 
@@ -98,6 +102,76 @@ def calibrate_copy(L, reps=3):
     L.sync()
     L.pg_node_free(x)
     log(f"[calib] k_unary copy of {CALIB_ROWS * CALIB_COLS * 4} B read + write, {reps} launches")
+
+
+# ---------------------------------------------------------------- HBM traffic (rocprofv3 --pmc)
+
+def _pmc_pass(counter: str, outdir: Path) -> dict[str, list[float]] | None:
+    """One rocprofv3 counter pass over `bench.py --pmc-child`; returns the
+    per-dispatch counter values (KiB) by kernel name."""
+    cmd = ["rocprofv3", "--pmc", counter, "-d", str(outdir), "-o", "run", "--output-format", "csv", "--",
+           sys.executable, str(Path(__file__).resolve()), "--pmc-child"]
+    env = dict(os.environ, TMPDIR="/tmp")
+    try:
+        subprocess.run(cmd, timeout=150, env=env, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL,
+                       check=False)
+    except subprocess.TimeoutExpired:
+        return None
+    files = list(outdir.rglob("run_counter_collection.csv"))
+    if not files:
+        return None
+    out: dict[str, list[float]] = {}
+    with open(files[0]) as f:
+        for r in csv.DictReader(f):
+            name = r["Kernel_Name"].replace("(anonymous namespace)::", "").split("(")[0]
+            out.setdefault(f"{name}@{r['Grid_Size']}", []).append(float(r["Counter_Value"]))
+    return out
+
+
+def measure_traffic() -> dict | None:
+    """HBM bytes per pgjit_main launch from FETCH_SIZE and WRITE_SIZE, each
+    scaled by what the same counter reads for the calibration copy
+    (k_unary reading and writing 256 MiB).  Runs before this process
+    touches the GPU, as two child processes under rocprofv3."""
+    if not shutil.which("rocprofv3"):
+        return None
+    calib_grid = "2097152"  # k_unary over 16384 x 4096 f32: 8192 blocks x 256
+    calib_kib = CALIB_ROWS * CALIB_COLS * 4 / 1024
+    res = {}
+    with tempfile.TemporaryDirectory(dir="/tmp") as td:
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            got = _pmc_pass(counter, Path(td) / counter)
+            if not got:
+                return None
+            cal = got.get(f"k_unary@{calib_grid}")
+            main = [v for k, v in got.items() if k.startswith("pgjit_main@")]
+            if not cal or not main:
+                return None
+            cal_kib = sum(cal) / len(cal)
+            main_kib = sum(main[0]) / len(main[0])
+            res[counter] = {"kib_per_dispatch": round(main_kib, 1), "calib_kib": round(cal_kib, 1),
+                            "factor": round(calib_kib / cal_kib, 4)}
+    total = sum(v["kib_per_dispatch"] * v["factor"] * 1024 for v in res.values())
+    return {"bytes": int(total), "counters": res}
+
+
+def pmc_child() -> int:
+    """The workload the counter passes profile: the calibration copy, then
+    three backward steps of config 2."""
+    import picograd_amd
+    L = picograd_amd.load()
+    if L.pg_amd_init() != 0:
+        return 1
+    calibrate_copy(L)
+    x, bias, g = c2_inputs(16384, 4096)
+    loss, nodes = c2_graph(L, x, bias, g)
+    for _ in range(3):
+        L.pg_backward(loss)
+    L.sync()
+    for n in nodes:
+        L.pg_node_free(n)
+    L.sync()
+    return 0
 
 
 # ---------------------------------------------------------------- config 2
@@ -301,11 +375,20 @@ def main(argv=None):
     ap.add_argument("--only", default="c2,c3,c1")
     ap.add_argument("--calib", action="store_true",
                     help="first run a plain copy kernel of known size (the HBM counter calibration)")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 counter passes")
+    ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
     a = ap.parse_args(argv)
+    if a.pmc_child:
+        return pmc_child()
     if a.gpus != 1:
         print(f"bench.py measures one GPU only (every box here has one); --gpus {a.gpus} is not supported",
               file=sys.stderr)
         return 2
+    traffic = None
+    if not a.no_traffic:
+        log("[traffic] rocprofv3 FETCH_SIZE / WRITE_SIZE passes (child processes)")
+        traffic = measure_traffic()
+        log(f"[traffic] {traffic}")
     import picograd_amd
     L = picograd_amd.load()
     if L.pg_amd_init() != 0:
@@ -349,7 +432,9 @@ def main(argv=None):
                                "y = gelu(x + bias) * sigmoid(g), x, g f32 [16384, 4096], bias [4096]",
                    "rows": 16384, "cols": 4096},
         "roofline": {"bound": "hbm", "achieved": round(c2["kernel_gbs"], 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(c2["kernel_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(c2["kernel_gbs"] / HBM_PEAK_GBS, 4),
+                     "traffic": traffic["bytes"] if traffic else None,
+                     "traffic_counters": traffic["counters"] if traffic else None,
                      "kernel": "pgjit_main (fused backward)", "kernel_ms": round(c2["kernel_ms"], 5),
                      "finisher_ms": round(c2["fin_ms"], 5)},
         "cpu_baseline": cpu,

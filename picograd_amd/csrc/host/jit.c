@@ -649,21 +649,21 @@ static void emit_expr(sbuf *b, const jnode *n, const char *a, const char *c)
     case PG_JIT_MUL: sb_add(b, "(%s * %s)", a, c); break;
     case PG_JIT_DIV: sb_add(b, "(%s / %s)", a, c); break;
     case PG_JIT_NEG: sb_add(b, "(-%s)", a); break;
-    case PG_JIT_EXP: sb_add(b, "expf(%s)", a); break;
+    case PG_JIT_EXP: sb_add(b, "pgm_exp(%s)", a); break;
     case PG_JIT_LOG: sb_add(b, "logf(%s)", a); break;
     case PG_JIT_SQRT: sb_add(b, "sqrtf(%s)", a); break;
     case PG_JIT_SIN: sb_add(b, "sinf(%s)", a); break;
     case PG_JIT_COS: sb_add(b, "cosf(%s)", a); break;
     case PG_JIT_ABS: sb_add(b, "fabsf(%s)", a); break;
     case PG_JIT_RELU: sb_add(b, "(%s > 0.0f ? %s : 0.0f)", a, a); break;
-    case PG_JIT_SIGMOID: sb_add(b, "(1.0f / (1.0f + expf(-%s)))", a); break;
+    case PG_JIT_SIGMOID: sb_add(b, "pgm_sigmoid(%s)", a); break;
     case PG_JIT_TANH: sb_add(b, "tanhf(%s)", a); break;
-    case PG_JIT_GELU: sb_add(b, "(0.5f * %s * (1.0f + erff(%s * 0.70710678118f)))", a, a); break;
+    case PG_JIT_GELU: sb_add(b, "pgm_gelu(%s)", a); break;
     case PG_JIT_ERF: sb_add(b, "erff(%s)", a); break;
     case PG_JIT_STEP: sb_add(b, "(%s > 0.0f ? 1.0f : 0.0f)", a); break;
-    case PGJ_OP_GELU_GRAD: sb_add(b, "pg_gelu_grad(%s)", a); break;
+    case PGJ_OP_GELU_GRAD: sb_add(b, "pgm_gelu_grad(%s)", a); break;
     case PGJ_OP_SIGN: sb_add(b, "(%s > 0.0f ? 1.0f : (%s < 0.0f ? -1.0f : 0.0f))", a, a); break;
-    case PGJ_OP_ERF_GRAD: sb_add(b, "(1.12837916709551f * expf(-%s * %s))", a, a); break;
+    case PGJ_OP_ERF_GRAD: sb_add(b, "(1.12837916709551f * pgm_exp(-%s * %s))", a, a); break;
     default: sb_add(b, "0.0f"); break;
     }
 }
@@ -686,36 +686,46 @@ static void emit_offset(sbuf *b, const plan_t *P, int i, const char *idx)
     sb_add(b, "_o; })");
 }
 
-static void emit_body(sbuf *b, const pg_jit_graph *g, const plan_t *P, const bool *reach, int vec,
-                      const char *idx)
+/* Values are named v<node>_<copy>_<lane>: `copy` is the unrolled position
+ * (several rows or strides per loop iteration), `lane` the element of a
+ * 4-wide vector. */
+
+/* loads of every used input for one copy at flat index `idx` */
+static void emit_loads(sbuf *b, const plan_t *P, int vec, const char *idx, int u)
 {
-    /* loads */
     for (int i = 0; i < P->nin; i++) {
         if (!P->in_used[i])
             continue;
         int nid = P->in_node[i];
-        if (vec == 4) {
-            bool bc_inner = P->istr[i][P->ndim - 1] == 0;
-            if (bc_inner) {
-                sb_add(b, "    float s%d = a.in[%d][", nid, i);
-                emit_offset(b, P, i, idx);
-                sb_add(b, "];\n");
-                for (int e = 0; e < 4; e++)
-                    sb_add(b, "    float v%d_%d = s%d;\n", nid, e, nid);
-            } else {
-                sb_add(b, "    float4 q%d = *(const float4 *)(a.in[%d] + ", nid, i);
-                emit_offset(b, P, i, idx);
-                sb_add(b, ");\n");
-                sb_add(b, "    float v%d_0 = q%d.x, v%d_1 = q%d.y, v%d_2 = q%d.z, v%d_3 = q%d.w;\n", nid, nid, nid,
-                       nid, nid, nid, nid, nid);
-            }
+        if (vec == 4 && P->istr[i][P->ndim - 1] != 0) {
+            /* an input of the full loop shape is read exactly once: stream it
+             * past the caches; broadcast inputs are re-read and stay cached */
+            if (P->in_direct[i])
+                sb_add(b, "    const pgf4 q%d_%d = __builtin_nontemporal_load((const pgf4 *)(in%d + ", nid, u, i);
+            else
+                sb_add(b, "    const pgf4 q%d_%d = *(const pgf4 *)(in%d + ", nid, u, i);
+            emit_offset(b, P, i, idx);
+            sb_add(b, P->in_direct[i] ? "));\n" : ");\n");
+            sb_add(b, "    float v%d_%d_0 = q%d_%d.x, v%d_%d_1 = q%d_%d.y, v%d_%d_2 = q%d_%d.z, v%d_%d_3 = q%d_%d.w;\n",
+                   nid, u, nid, u, nid, u, nid, u, nid, u, nid, u, nid, u, nid, u);
+        } else if (P->in_direct[i]) {
+            sb_add(b, "    const float s%d_%d = __builtin_nontemporal_load(in%d + ", nid, u, i);
+            emit_offset(b, P, i, idx);
+            sb_add(b, ");\n");
         } else {
-            sb_add(b, "    float v%d_0 = a.in[%d][", nid, i);
+            sb_add(b, "    const float s%d_%d = in%d[", nid, u, i);
             emit_offset(b, P, i, idx);
             sb_add(b, "];\n");
         }
+        if (!(vec == 4 && P->istr[i][P->ndim - 1] != 0))
+            for (int e = 0; e < vec; e++)
+                sb_add(b, "    float v%d_%d_%d = s%d_%d;\n", nid, u, e, nid, u);
     }
-    /* computation */
+}
+
+/* the straight-line forward recompute and chain rule of one copy */
+static void emit_compute(sbuf *b, const pg_jit_graph *g, const bool *reach, int vec, int u)
+{
     for (size_t id = 0; id < g->nn; id++) {
         if (!reach[id])
             continue;
@@ -727,21 +737,62 @@ static void emit_body(sbuf *b, const pg_jit_graph *g, const plan_t *P, const boo
                 /* exact hex-float literal of the f32 constant */
                 float cv = n->cval;
                 if (cv != cv)
-                    sb_add(b, "    const float v%zu_%d = __builtin_nanf(\"\");\n", id, e);
+                    sb_add(b, "    const float v%zu_%d_%d = __builtin_nanf(\"\");\n", id, u, e);
                 else if (cv > 3.4028235e38f || cv < -3.4028235e38f)
-                    sb_add(b, "    const float v%zu_%d = %s__builtin_inff();\n", id, e, cv < 0 ? "-" : "");
+                    sb_add(b, "    const float v%zu_%d_%d = %s__builtin_inff();\n", id, u, e, cv < 0 ? "-" : "");
                 else
-                    sb_add(b, "    const float v%zu_%d = (float)%a;\n", id, e, (double)cv);
+                    sb_add(b, "    const float v%zu_%d_%d = (float)%a;\n", id, u, e, (double)cv);
                 continue;
             }
-            char sa[32], sc[32];
-            snprintf(sa, sizeof sa, "v%d_%d", n->in[0], e);
-            snprintf(sc, sizeof sc, "v%d_%d", n->nin == 2 ? n->in[1] : n->in[0], e);
-            sb_add(b, "    float v%zu_%d = ", id, e);
+            char sa[40], sc[40];
+            snprintf(sa, sizeof sa, "v%d_%d_%d", n->in[0], u, e);
+            snprintf(sc, sizeof sc, "v%d_%d_%d", n->nin == 2 ? n->in[1] : n->in[0], u, e);
+            sb_add(b, "    const float v%zu_%d_%d = ", id, u, e);
             emit_expr(b, n, sa, sc);
             sb_add(b, ";\n");
         }
     }
+}
+
+/* stores of the full-shape (not reduced) outputs of one copy */
+static void emit_stores(sbuf *b, const plan_t *P, int vec, const char *idx, int u)
+{
+    for (int o = 0; o < P->nout; o++) {
+        if (P->R > 0 && P->out_red[o])
+            continue;
+        int nid = P->out_node[o];
+        /* each output element is written once per launch: stream the stores
+         * (and the read of an accumulating output) past the caches */
+        if (vec == 4) {
+            if (P->out_beta[o])
+                sb_add(b, "    { pgf4 *p = (pgf4 *)(out%d + %s); pgf4 t = __builtin_nontemporal_load(p);"
+                          " t.x += v%d_%d_0; t.y += v%d_%d_1; t.z += v%d_%d_2; t.w += v%d_%d_3;"
+                          " __builtin_nontemporal_store(t, p); }\n",
+                       o, idx, nid, u, nid, u, nid, u, nid, u);
+            else
+                sb_add(b, "    __builtin_nontemporal_store((pgf4){v%d_%d_0, v%d_%d_1, v%d_%d_2, v%d_%d_3}, (pgf4 *)(out%d + %s));\n",
+                       nid, u, nid, u, nid, u, nid, u, o, idx);
+        } else {
+            if (P->out_beta[o])
+                sb_add(b, "    __builtin_nontemporal_store(__builtin_nontemporal_load(out%d + %s) + v%d_%d_0, out%d + %s);\n",
+                       o, idx, nid, u, o, idx);
+            else
+                sb_add(b, "    __builtin_nontemporal_store(v%d_%d_0, out%d + %s);\n", nid, u, o, idx);
+        }
+    }
+}
+
+/* the device math helpers (kernels/pgmath.h), embedded by the build */
+extern const char pgk_math_source[];
+
+static void emit_prologue(sbuf *b, const plan_t *P)
+{
+    for (int i = 0; i < P->nin; i++)
+        if (P->in_used[i])
+            sb_add(b, "  const float *__restrict__ in%d = a.in[%d];\n", i, i);
+    for (int o = 0; o < P->nout; o++)
+        if (!(P->R > 0 && P->out_red[o]))
+            sb_add(b, "  float *__restrict__ out%d = a.out[%d];\n", o, o);
 }
 
 static char *gen_source(const pg_jit_graph *g, const plan_t *P, const bool *reach)
@@ -750,47 +801,43 @@ static char *gen_source(const pg_jit_graph *g, const plan_t *P, const bool *reac
     bool red = P->R > 0;
     bool wide = P->numel >= ((int64_t)1 << 31);
     sb_add(&b, "// picograd-amd fused elementwise kernel (generated)\n");
-    sb_add(&b, "typedef %s IDX;\n", wide ? "long long" : "unsigned int");
+    sb_add(&b, "%s\n", pgk_math_source);
+    sb_add(&b, "typedef %s IDX;\n", wide ? "unsigned long long" : "unsigned int");
+    sb_add(&b, "typedef float pgf4 __attribute__((ext_vector_type(4)));\n");
     sb_add(&b, "struct PgArgs { const float *in[%d]; float *out[%d]; float *part[%d]; };\n", MAXIO * 2, MAXIO * 2,
            MAXIO * 2);
-    sb_add(&b, "__device__ __forceinline__ float pg_gelu_grad(float x) {\n"
-               "  float erf_term = erff(x * 0.70710678118f);\n"
-               "  float phi = expf(-0.5f * x * x) / 2.50662827463f;\n"
-               "  return 0.5f * (1.0f + erf_term) + x * phi;\n}\n");
     if (!red) {
+        /* grid-stride over the flat loop: two strides per iteration, both
+         * copies' loads issued before either copy's math */
         int vec = P->vec;
         sb_add(&b, "extern \"C\" __global__ void __launch_bounds__(256) pgjit_main(PgArgs a) {\n");
-        sb_add(&b, "  const IDX N = (IDX)%lldLL;\n", (long long)P->numel);
-        sb_add(&b, "  IDX i = ((IDX)blockIdx.x * 256u + threadIdx.x) * %d;\n", vec);
-        sb_add(&b, "  const IDX step = (IDX)gridDim.x * 256u * %d;\n", vec);
-        sb_add(&b, "  for (; i < N; i += step) {\n");
-        emit_body(&b, g, P, reach, vec, "i");
-        for (int o = 0; o < P->nout; o++) {
-            int nid = P->out_node[o];
-            if (vec == 4) {
-                if (P->out_beta[o])
-                    sb_add(&b, "    { float4 *p = (float4 *)(a.out[%d] + i); float4 t = *p;"
-                               " t.x += v%d_0; t.y += v%d_1; t.z += v%d_2; t.w += v%d_3; *p = t; }\n",
-                           o, nid, nid, nid, nid);
-                else
-                    sb_add(&b, "    *(float4 *)(a.out[%d] + i) = make_float4(v%d_0, v%d_1, v%d_2, v%d_3);\n", o,
-                           nid, nid, nid, nid);
-            } else {
-                if (P->out_beta[o])
-                    sb_add(&b, "    a.out[%d][i] += v%d_0;\n", o, nid);
-                else
-                    sb_add(&b, "    a.out[%d][i] = v%d_0;\n", o, nid);
-            }
-        }
+        emit_prologue(&b, P);
+        sb_add(&b, "  const IDX N = (IDX)%lldULL;\n", (long long)P->numel);
+        sb_add(&b, "  const IDX step = (IDX)gridDim.x * 256u * %du;\n", vec);
+        sb_add(&b, "  IDX i = ((IDX)blockIdx.x * 256u + threadIdx.x) * %du;\n", vec);
+        sb_add(&b, "  for (; i + step < N; i += 2u * step) {\n");
+        sb_add(&b, "    const IDX i0 = i, i1 = i + step;\n");
+        emit_loads(&b, P, vec, "i0", 0);
+        emit_loads(&b, P, vec, "i1", 1);
+        emit_compute(&b, g, reach, vec, 0);
+        emit_compute(&b, g, reach, vec, 1);
+        emit_stores(&b, P, vec, "i0", 0);
+        emit_stores(&b, P, vec, "i1", 1);
+        sb_add(&b, "  }\n  if (i < N) {\n    const IDX i0 = i;\n");
+        emit_loads(&b, P, vec, "i0", 0);
+        emit_compute(&b, g, reach, vec, 0);
+        emit_stores(&b, P, vec, "i0", 0);
         sb_add(&b, "  }\n}\n");
         return b.s;
     }
-    /* reduced outputs: [R x C] tiling; 64 column groups x 4 row lanes */
+    /* reduced outputs: [R x C] tiling; 64 column groups x 4 row lanes, each
+     * lane walking rows r, r+4, ... of its block's band, two per iteration */
     int vec = (P->C % 4 == 0 && P->vec == 4) ? 4 : 1;
     sb_add(&b, "extern \"C\" __global__ void __launch_bounds__(256) pgjit_main(PgArgs a) {\n");
-    sb_add(&b, "  const IDX R = (IDX)%lldLL, C = (IDX)%lldLL;\n", (long long)P->R, (long long)P->C);
+    emit_prologue(&b, P);
+    sb_add(&b, "  const IDX R = (IDX)%lldULL, C = (IDX)%lldULL;\n", (long long)P->R, (long long)P->C);
     sb_add(&b, "  const IDX tc = threadIdx.x & 63u, tr = threadIdx.x >> 6;\n");
-    sb_add(&b, "  const IDX c = ((IDX)blockIdx.x * 64u + tc) * %d;\n", vec);
+    sb_add(&b, "  const IDX c = ((IDX)blockIdx.x * 64u + tc) * %du;\n", vec);
     sb_add(&b, "  const IDX rows_per = (R + gridDim.y - 1) / gridDim.y;\n");
     sb_add(&b, "  const IDX r0 = (IDX)blockIdx.y * rows_per;\n");
     sb_add(&b, "  const IDX r1 = r0 + rows_per < R ? r0 + rows_per : R;\n");
@@ -799,26 +846,28 @@ static char *gen_source(const pg_jit_graph *g, const plan_t *P, const bool *reac
             for (int e = 0; e < vec; e++)
                 sb_add(&b, "  float acc%d_%d = 0.0f;\n", o, e);
     sb_add(&b, "  if (c < C) {\n");
-    sb_add(&b, "  for (IDX r = r0 + tr; r < r1; r += 4u) {\n");
-    sb_add(&b, "    const IDX i = r * C + c;\n");
-    emit_body(&b, g, P, reach, vec, "i");
-    for (int o = 0; o < P->nout; o++) {
-        int nid = P->out_node[o];
-        if (P->out_red[o]) {
+    sb_add(&b, "  IDX r = r0 + tr;\n");
+    sb_add(&b, "  for (; r + 4u < r1; r += 8u) {\n");
+    sb_add(&b, "    const IDX i0 = r * C + c, i1 = i0 + 4u * C;\n");
+    emit_loads(&b, P, vec, "i0", 0);
+    emit_loads(&b, P, vec, "i1", 1);
+    emit_compute(&b, g, reach, vec, 0);
+    emit_compute(&b, g, reach, vec, 1);
+    for (int u = 0; u < 2; u++)
+        for (int o = 0; o < P->nout; o++)
+            if (P->out_red[o])
+                for (int e = 0; e < vec; e++)
+                    sb_add(&b, "    acc%d_%d += v%d_%d_%d;\n", o, e, P->out_node[o], u, e);
+    emit_stores(&b, P, vec, "i0", 0);
+    emit_stores(&b, P, vec, "i1", 1);
+    sb_add(&b, "  }\n  if (r < r1) {\n    const IDX i0 = r * C + c;\n");
+    emit_loads(&b, P, vec, "i0", 0);
+    emit_compute(&b, g, reach, vec, 0);
+    for (int o = 0; o < P->nout; o++)
+        if (P->out_red[o])
             for (int e = 0; e < vec; e++)
-                sb_add(&b, "    acc%d_%d += v%d_%d;\n", o, e, nid, e);
-        } else if (vec == 4) {
-            if (P->out_beta[o])
-                sb_add(&b, "    { float4 *p = (float4 *)(a.out[%d] + i); float4 t = *p;"
-                           " t.x += v%d_0; t.y += v%d_1; t.z += v%d_2; t.w += v%d_3; *p = t; }\n",
-                       o, nid, nid, nid, nid);
-            else
-                sb_add(&b, "    *(float4 *)(a.out[%d] + i) = make_float4(v%d_0, v%d_1, v%d_2, v%d_3);\n", o, nid,
-                       nid, nid, nid);
-        } else {
-            sb_add(&b, P->out_beta[o] ? "    a.out[%d][i] += v%d_0;\n" : "    a.out[%d][i] = v%d_0;\n", o, nid);
-        }
-    }
+                sb_add(&b, "    acc%d_%d += v%d_0_%d;\n", o, e, P->out_node[o], e);
+    emit_stores(&b, P, vec, "i0", 0);
     sb_add(&b, "  }\n  }\n");
     /* combine the 4 row lanes in LDS, fixed order, one partial row per block */
     sb_add(&b, "  __shared__ float red[4][%d];\n", 64 * vec);
@@ -836,21 +885,35 @@ static char *gen_source(const pg_jit_graph *g, const plan_t *P, const bool *reac
         sb_add(&b, "  }\n  __syncthreads();\n");
     }
     sb_add(&b, "}\n");
-    /* finisher: out[c] (beta ? += : =) sum over blocks of part[blk][c], in
-     * block order split over 4 row lanes then combined in fixed order */
+    /* finisher: out[c] (beta ? += : =) sum over blocks of part[blk][c].
+     * 16 column lanes x 16 block lanes per workgroup; block lane q sums
+     * partial rows q, q + 16, ... in that order (eight loads in flight, the
+     * adds still in row order) and the 16 lanes are combined in order, so
+     * the result does not depend on the launch shape.  Four columns per
+     * lane when C allows it. */
     sb_add(&b, "extern \"C\" __global__ void __launch_bounds__(256) pgjit_fin(PgArgs a, unsigned nblk) {\n");
-    sb_add(&b, "  const IDX C = (IDX)%lldLL;\n", (long long)P->C);
-    sb_add(&b, "  const IDX tc = threadIdx.x & 63u, tr = threadIdx.x >> 6;\n");
-    sb_add(&b, "  const IDX c = (IDX)blockIdx.x * 64u + tc;\n");
-    sb_add(&b, "  __shared__ float red[4][64];\n");
+    sb_add(&b, "  const IDX C = (IDX)%lldULL;\n", (long long)P->C);
+    sb_add(&b, "  const IDX tc = threadIdx.x & 15u, tr = threadIdx.x >> 4;\n");
+    const char *T = vec == 4 ? "pgf4" : "float";
+    sb_add(&b, "  const IDX c = ((IDX)blockIdx.x * 16u + tc) * %du;\n", vec);
+    sb_add(&b, "  __shared__ %s red[16][17];\n", T);
     for (int o = 0; o < P->nout; o++) {
         if (!P->out_red[o])
             continue;
-        sb_add(&b, "  { float s = 0.0f;\n");
-        sb_add(&b, "    if (c < C) for (unsigned k = tr; k < nblk; k += 4u) s += a.part[%d][(IDX)k * C + c];\n", o);
+        sb_add(&b, "  { const float *__restrict__ pp = a.part[%d];\n", o);
+        sb_add(&b, "    %s s = (%s)(0.0f);\n", T, T);
+        sb_add(&b, "    if (c < C) {\n      unsigned k = tr;\n");
+        sb_add(&b, "      for (; k + 112u < nblk; k += 128u) {\n        %s v[8];\n", T);
+        sb_add(&b, "#pragma unroll\n        for (int q = 0; q < 8; q++) v[q] = *(const %s *)(pp + (IDX)(k + 16u * q) * C + c);\n", T);
+        sb_add(&b, "#pragma unroll\n        for (int q = 0; q < 8; q++) s += v[q];\n      }\n");
+        sb_add(&b, "      for (; k < nblk; k += 16u) s += *(const %s *)(pp + (IDX)k * C + c);\n    }\n", T);
         sb_add(&b, "    red[tr][tc] = s; __syncthreads();\n");
-        sb_add(&b, "    if (tr == 0 && c < C) { float t = ((red[0][tc] + red[1][tc]) + red[2][tc]) + red[3][tc];\n");
-        sb_add(&b, P->out_beta[o] ? "      a.out[%d][c] += t; }\n" : "      a.out[%d][c] = t; }\n", o);
+        sb_add(&b, "    if (tr == 0 && c < C) { %s t = red[0][tc];\n", T);
+        sb_add(&b, "      for (int q = 1; q < 16; q++) t += red[q][tc];\n");
+        if (P->out_beta[o])
+            sb_add(&b, "      *(%s *)(a.out[%d] + c) += t; }\n", T, o);
+        else
+            sb_add(&b, "      *(%s *)(a.out[%d] + c) = t; }\n", T, o);
         sb_add(&b, "    __syncthreads(); }\n");
     }
     sb_add(&b, "}\n");
@@ -909,7 +972,7 @@ static void write_file_atomic(const char *path, const void *p, size_t n)
 static bool compile_source(const char *src, hipModule_t *mod)
 {
     uint64_t h = fnv(src, strlen(src), 14695981039346656037ULL);
-    h = fnv("gfx950-v1", 9, h);
+    h = fnv("gfx950-v4", 9, h);
     char path[600];
     snprintf(path, sizeof path, "%s/%016llx.hsaco", cache_dir(), (unsigned long long)h);
     const char *force = getenv("PG_JIT_FORCE_COMPILE_ERROR");
@@ -1054,11 +1117,13 @@ static centry *get_entry(const pg_jit_graph *g, size_t lnd, const size_t *ls, bo
     } else {
         int vec = (P.C % 4 == 0 && P.vec == 4) ? 4 : 1;
         int64_t cb = (P.C + 64 * vec - 1) / (64 * vec);
-        /* aim for ~4096 blocks in total, at least 8 rows per row lane band */
-        int64_t rb = 4096 / (cb ? cb : 1);
+        /* ~16K short-lived blocks of >= 16 rows (4 per row lane): measured
+         * on the config-2 shape, 16-row bands stream ~8% faster than
+         * 64-row ones, and the extra partial rows cost the finisher ~1 us */
+        int64_t rb = 16384 / (cb ? cb : 1);
         if (rb < 1)
             rb = 1;
-        int64_t max_rb = (P.R + 31) / 32;
+        int64_t max_rb = (P.R + 15) / 16;
         if (rb > max_rb)
             rb = max_rb;
         if (rb < 1)
@@ -1067,7 +1132,7 @@ static centry *get_entry(const pg_jit_graph *g, size_t lnd, const size_t *ls, bo
             rb = 65535;
         e->grid_x = (unsigned)cb;
         e->grid_y = (unsigned)rb;
-        e->fin_grid = (unsigned)((P.C + 63) / 64);
+        e->fin_grid = (unsigned)((P.C + 16 * vec - 1) / (16 * vec));
         size_t off = 0;
         for (int o = 0; o < P.nout; o++) {
             e->part_floats[o] = P.out_red[o] ? (size_t)rb * (size_t)P.C : 0;

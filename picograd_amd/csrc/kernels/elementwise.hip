@@ -7,6 +7,7 @@
 #include <stdint.h>
 
 #include "launch.h"
+#include "pgmath.h"
 
 namespace {
 
@@ -27,33 +28,19 @@ inline int status() { return (int)hipGetLastError(); }
 
 // ---------------------------------------------------------------- math
 
-__device__ __forceinline__ float gelu_f(float x)
-{
-    return 0.5f * x * (1.0f + erff(x * 0.70710678118f));
-}
-
-__device__ __forceinline__ float gelu_grad_f(float x)
-{
-    const float sqrt_2pi = 2.50662827463f;
-    const float inv_sqrt2 = 0.70710678118f;
-    float erf_term = erff(x * inv_sqrt2);
-    float phi = expf(-0.5f * x * x) / sqrt_2pi;
-    return 0.5f * (1.0f + erf_term) + x * phi;
-}
-
 __device__ __forceinline__ float unary_f(int op, float x, float p0, float p1)
 {
     switch (op) {
     case PGK_NEG: return -x;
-    case PGK_EXP: return expf(x);
+    case PGK_EXP: return pgm_exp(x);
     case PGK_LOG: return logf(x);
     case PGK_SQRT: return sqrtf(x);
     case PGK_SIN: return sinf(x);
     case PGK_COS: return cosf(x);
     case PGK_RELU: return x > 0.0f ? x : 0.0f;
-    case PGK_SIGMOID: return 1.0f / (1.0f + expf(-x));
+    case PGK_SIGMOID: return pgm_sigmoid(x);
     case PGK_TANH: return tanhf(x);
-    case PGK_GELU: return gelu_f(x);
+    case PGK_GELU: return pgm_gelu(x);
     case PGK_ERF: return erff(x);
     case PGK_ABS: return fabsf(x);
     case PGK_LEAKY: return x > 0.0f ? x : p0 * x;
@@ -67,22 +54,22 @@ __device__ __forceinline__ float unary_grad_f(int op, float x, float p0, float p
 {
     switch (op) {
     case PGK_NEG: return -1.0f;
-    case PGK_EXP: return expf(x);
+    case PGK_EXP: return pgm_exp(x);
     case PGK_LOG: return 1.0f / x;
     case PGK_SQRT: return 0.5f / sqrtf(x);
     case PGK_SIN: return cosf(x);
     case PGK_COS: return -sinf(x);
     case PGK_RELU: return x > 0.0f ? 1.0f : 0.0f;
     case PGK_SIGMOID: {
-        float s = 1.0f / (1.0f + expf(-x));
+        float s = pgm_sigmoid(x);
         return s * (1.0f - s);
     }
     case PGK_TANH: {
         float t = tanhf(x);
         return 1.0f - t * t;
     }
-    case PGK_GELU: return gelu_grad_f(x);
-    case PGK_ERF: return 1.12837916709551f * expf(-x * x);
+    case PGK_GELU: return pgm_gelu_grad(x);
+    case PGK_ERF: return 1.12837916709551f * pgm_exp(-x * x);
     case PGK_ABS: return x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : 0.0f);
     case PGK_LEAKY: return x > 0.0f ? 1.0f : p0;
     case PGK_CLAMP: return (x >= p0 && x <= p1) ? 1.0f : 0.0f;

@@ -185,10 +185,12 @@ def test_chain2_broadcast_grads_match_oracle(lib, oracle, R, Cc, jit):
     assert max_rel(dx, rdx) <= ELEM_TOL
     assert max_rel(dg, rdg) <= ELEM_TOL
     # dbias: both sums are f32 over R terms in different orders; judge them
-    # against the f64 sum, each within the f32 summation bound
-    bound = 4 * R * np.finfo(np.float32).eps * np.abs(rdx).sum(axis=0) + 1e-30
+    # against the f64 sum of the oracle's addends: the f32 summation bound
+    # plus the elementwise tolerance of the R addends themselves
+    absum = np.abs(rdx.astype(np.float64)).sum(axis=0)
+    bound = (4 * R * np.finfo(np.float32).eps + ELEM_TOL) * absum + 1e-30
     assert np.all(np.abs(db - rdb64) <= bound)
-    assert np.all(np.abs(rdb - rdb64) <= bound)
+    assert np.all(np.abs(rdb - rdb64) <= 4 * R * np.finfo(np.float32).eps * absum + 1e-30)
 
 
 # ---------------------------------------------------------------- GEMM
