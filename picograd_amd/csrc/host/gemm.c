@@ -7,16 +7,19 @@
  * dB += A^T.dC per batch, grads in f32, an unbatched operand accumulating
  * over the batch).
  *
- * f16/bf16 matrices run on the MFMA kernel, which wants both operands with
- * the reduction dim contiguous ("NT").  So:
- *   forward  C  = A . B      : B is staged transposed ([N, K])
- *   dgrad    dA = dC . B^T   : dC is cast to the operand dtype; B as is
- *   wgrad    dB = A^T . dC   : A and dC are staged transposed ([K, M], [N, M])
- * Staging also pads the reduction dim to a multiple of 8 with zeros.  The
- * upstream grad is rounded to the operand dtype (RNE) before the GEMMs:
- * the grads are f32-accumulated products of 16-bit operands, the contract
- * of the reference's hgemm/bgemm (backend/cpu/gemm.c:575-629).
- * f32 operands and 1-D (vector) cases use the f32 FMA kernel.
+ * f16/bf16 matrices run on the MFMA kernel (pgk_gemm16), which reads each
+ * operand where it lies, reduction dim contiguous or not:
+ *   forward  C  = A . B      : A [M, K] K-contiguous, B [K, N] N-contiguous
+ *   dgrad    dA = dC . B^T   : dC [M, N] and B [K, N], both N-contiguous
+ *                              along the reduction
+ *   wgrad    dB = A^T . dC   : A [M, K] and dC [M, N], reduction over M
+ *                              with the output dims contiguous
+ * The only copies are zero-padding of a dimension that is not a multiple of
+ * 8 (16-byte loads) and the upstream grad rounded once to the operand dtype
+ * (RNE), shared by dgrad and wgrad: the grads are f32-accumulated products
+ * of 16-bit operands, the contract of the reference's hgemm/bgemm
+ * (backend/cpu/gemm.c:575-629).  f32 operands and 1-D (vector) cases use
+ * the f32 FMA kernel.
  */
 #define _POSIX_C_SOURCE 200809L
 #include "internal.h"
@@ -81,14 +84,42 @@ static bool mm_shapes(const pg_tensor *a, const pg_tensor *b, mm_shape *s, size_
 
 static void *tmp_alloc(size_t nbytes) { return pgd_malloc(nbytes ? nbytes : 1); }
 
-/* the MFMA GEMM, bracketed by the kernel timer */
-static int gemm16(int dt, size_t m, size_t n, size_t k, const uint16_t *a, size_t lda, size_t sa, const uint16_t *b,
-                  size_t ldb, size_t sb, float *c, size_t ldc, size_t sc, size_t batch, int beta, pgk_stream st)
+/* one MFMA GEMM (pgk_gemm16 semantics), bracketed by the kernel timer; the
+ * k-tail workspace comes from the library scratch (stream-ordered, so
+ * consecutive GEMMs may share it) */
+static bool gemm16(int dt, int ta, int tb, size_t m, size_t n, size_t k, const uint16_t *a, size_t lda, size_t sa,
+                   size_t aext, const uint16_t *b, size_t ldb, size_t sb, size_t bext, float *c, size_t ldc,
+                   size_t sc, size_t batch, int beta, const char *what)
 {
+    size_t wsz = pgk_gemm16_workspace(ta, tb, m, n, k, batch);
+    void *ws = NULL;
+    if (wsz && !(ws = pgd_scratch(1, wsz))) {
+        pgd_set_err("%s: workspace allocation failed", what);
+        return false;
+    }
     int tk = pgd_tbegin(PGD_T_GEMM16);
-    int rc = pgk_gemm16_nt(dt, m, n, k, a, lda, sa, b, ldb, sb, c, ldc, sc, batch, beta, st);
+    int rc = pgk_gemm16(dt, ta, tb, m, n, k, a, lda, sa, aext, b, ldb, sb, bext, c, ldc, sc, batch, beta, ws,
+                        pgd_stream());
     pgd_tend(tk);
-    return rc;
+    return pgd_check(rc, what);
+}
+
+/* 16-bit copy of `rows x cols` (leading dim lds, `batch` matrices `sstride`
+ * apart) padded with zeros to rows_pad x cols_pad; src_dtype 0 casts f32 */
+static uint16_t *stage16(int dt, int src_dtype, const void *src, size_t rows, size_t cols, size_t lds,
+                         size_t rows_pad, size_t cols_pad, size_t batch, size_t sstride, size_t *bytes)
+{
+    *bytes = batch * rows_pad * cols_pad * 2;
+    uint16_t *p = tmp_alloc(*bytes);
+    if (!p)
+        return NULL;
+    if (!pgd_check(pgk_copy_to16(dt, src_dtype, src, rows, cols, lds, p, cols_pad, rows_pad, batch, sstride,
+                                 rows_pad * cols_pad, pgd_stream()),
+                   "stage operand")) {
+        pgd_free(p, *bytes);
+        return NULL;
+    }
+    return p;
 }
 
 pg_tensor *pgm_matmul_forward(const pg_tensor *a, const pg_tensor *b)
@@ -125,28 +156,32 @@ pg_tensor *pgm_matmul_forward(const pg_tensor *a, const pg_tensor *b)
         return c;
     }
     int dt = (int)a->dtype;
-    size_t K8 = up8(K);
-    size_t bb = s.bbat ? s.nbatch : 1;
-    /* B^T staged: [N, K8] per batch */
-    uint16_t *bt = tmp_alloc(bb * N * K8 * 2);
-    const uint16_t *ap = a->dev;
-    uint16_t *apad = NULL;
-    bool ok = bt != NULL;
-    if (ok)
-        ok = pgd_check(pgk_transpose_to16(dt, dt, b->dev, K, N, N, bt, K8, bb, K * N, N * K8, st), "stage B^T");
-    if (ok && K8 != K) {
-        size_t ab = s.abat ? s.nbatch : 1;
-        apad = tmp_alloc(ab * M * K8 * 2);
-        ok = apad && pgd_check(pgk_copy_to16(dt, dt, a->dev, M, K, K, apad, K8, ab, M * K, M * K8, st), "stage A");
+    /* K padded to 8 needs zero columns of A and zero rows of B; N padded
+     * to 8 (B's contiguous dim) needs zero columns of B */
+    size_t K8 = up8(K), N8 = up8(N) < 8 ? 8 : up8(N);
+    size_t ab = s.abat ? s.nbatch : 1, bb = s.bbat ? s.nbatch : 1;
+    const uint16_t *ap = a->dev, *bp = b->dev;
+    uint16_t *apad = NULL, *bpad = NULL;
+    size_t abytes = 0, bbytes = 0;
+    bool ok = true;
+    if (K8 != K) {
+        apad = stage16(dt, dt, a->dev, M, K, K, M, K8, ab, M * K, &abytes);
+        ok = apad != NULL;
         ap = apad;
     }
+    if (ok && (K8 != K || N8 != N)) {
+        bpad = stage16(dt, dt, b->dev, K, N, N, K8, N8, bb, K * N, &bbytes);
+        ok = bpad != NULL;
+        bp = bpad;
+    }
+    size_t ldb = (K8 != K || N8 != N) ? N8 : N;
     if (ok)
-        ok = pgd_check(gemm16(dt, M, N, K8, ap, K8, s.abat ? M * K8 : 0, bt, K8, s.bbat ? N * K8 : 0,
-                                     c->dev, N, sc, s.nbatch, 0, st),
-                       "matmul mfma");
-    pgd_free(bt, bb * N * K8 * 2);
+        ok = gemm16(dt, 0, 1, M, N, K8, ap, K8, s.abat ? M * K8 : 0, M, bp, ldb, s.bbat ? K8 * ldb : 0,
+                    bpad ? N8 : N, c->dev, N, sc, s.nbatch, 0, "matmul mfma");
     if (apad)
-        pgd_free(apad, (s.abat ? s.nbatch : 1) * M * K8 * 2);
+        pgd_free(apad, abytes);
+    if (bpad)
+        pgd_free(bpad, bbytes);
     if (!ok) {
         pga_set_err("matmul: %s", pg_amd_last_error());
         pg_tensor_free(c);
@@ -216,72 +251,61 @@ void pgm_matmul_backward(pg_node *n)
     }
 
     int dt = (int)a->dtype;
-    size_t N8 = up8(N);
-    /* dgrad operand: dC rounded to the operand dtype, [B*M, N8] */
+    /* dC rounded once to the operand dtype, [B*M, N8] (zero columns past N) */
+    size_t N8 = up8(N) < 8 ? 8 : up8(N), K8 = up8(K) < 8 ? 8 : up8(K);
+    size_t gbytes;
+    uint16_t *g16 = stage16(dt, 0, g->dev, B * M, N, N, B * M, N8, 1, 0, &gbytes);
+    if (!g16)
+        return;
     if (ga) {
-        size_t gbytes = B * M * N8 * 2;
-        uint16_t *g16 = tmp_alloc(gbytes);
-        const uint16_t *bp = b->dev;
-        uint16_t *bpad = NULL;
-        size_t bbytes = (s.bbat ? B : 1) * K * N8 * 2;
-        bool ok = g16 && pgd_check(pgk_copy_to16(dt, 0, g->dev, B * M, N, N, g16, N8, 1, 0, 0, st), "stage dC");
-        if (ok && N8 != N) {
-            bpad = tmp_alloc(bbytes);
-            ok = bpad && pgd_check(pgk_copy_to16(dt, dt, b->dev, (s.bbat ? B : 1) * K, N, N, bpad, N8, 1, 0, 0, st),
-                                   "stage B");
-            bp = bpad;
-        }
-        if (ok) {
+        /* dA[M, K] (+)= dC[M, N] . W[K, N]^T: both operands contiguous along
+         * the reduction (N); W padded to N8 zero columns when needed */
+        const uint16_t *wp = b->dev;
+        uint16_t *wpad = NULL;
+        size_t wbytes = 0, wb = s.bbat ? B : 1;
+        if (N8 != N)
+            wp = wpad = stage16(dt, dt, b->dev, K, N, N, K, N8, wb, K * N, &wbytes);
+        if (wp) {
             if (s.abat || B == 1) {
-                pgd_check(gemm16(dt, M, K, N8, g16, N8, M * N8, bp, N8, s.bbat ? K * N8 : 0, ga->dev, K,
-                                        M * K, B, ba, st),
-                          "dgrad");
+                gemm16(dt, 0, 0, M, K, N8, g16, N8, M * N8, M, wp, N8, s.bbat ? K * N8 : 0, K, ga->dev, K, M * K, B,
+                       ba, "dgrad");
             } else {
+                /* unbatched A, batched B: dA accumulates over the batch */
                 for (size_t z = 0; z < B; z++)
-                    pgd_check(gemm16(dt, M, K, N8, g16 + z * M * N8, N8, 0, bp + z * K * N8, N8, 0, ga->dev,
-                                            K, 0, 1, z == 0 ? ba : 1, st),
-                              "dgrad");
+                    gemm16(dt, 0, 0, M, K, N8, g16 + z * M * N8, N8, 0, M, wp + z * K * N8, N8, 0, K, ga->dev, K, 0,
+                           1, z == 0 ? ba : 1, "dgrad");
             }
         }
-        pgd_free(g16, gbytes);
-        if (bpad)
-            pgd_free(bpad, bbytes);
+        if (wpad)
+            pgd_free(wpad, wbytes);
     }
-    /* wgrad operands: A^T [K, M8] and dC^T [N, M8] per batch; when only A is
-     * batched the batch folds into the reduction (M_eff = B*M) */
     if (gb) {
+        /* dW[K, N] (+)= A[M, K]^T . dC[M, N]: reduction over M with K and N
+         * contiguous; A padded to K8 zero columns when needed.  When only
+         * A is batched the batch folds into the reduction (M_eff = B M) */
         bool fold = s.abat && !s.bbat;
-        size_t Bw = fold ? 1 : B;
-        size_t Mw = fold ? B * M : M;
-        size_t M8 = up8(Mw);
-        size_t atb = Bw * K * M8 * 2, gtb = Bw * N * M8 * 2;
-        uint16_t *at = tmp_alloc(atb), *gt = tmp_alloc(gtb);
-        bool ok = at && gt;
-        size_t a_bat = s.abat && !fold ? B : 1;
-        if (ok)
-            ok = pgd_check(pgk_transpose_to16(dt, dt, a->dev, Mw, K, K, at, M8, a_bat, M * K, K * M8, st),
-                           "stage A^T");
-        if (ok && a_bat < Bw) /* A unbatched but B batched: same A^T for every batch */
-            for (size_t z = 1; z < Bw && ok; z++)
-                ok = pgd_d2d(at + z * K * M8, at, K * M8 * 2);
-        if (ok)
-            ok = pgd_check(pgk_transpose_to16(dt, 0, g->dev, Mw, N, N, gt, M8, Bw, Mw * N, N * M8, st),
-                           "stage dC^T");
-        if (ok) {
+        size_t Bw = fold ? 1 : B, Mw = fold ? B * M : M;
+        size_t a_rows = s.abat ? B * M : M;
+        const uint16_t *ap = a->dev;
+        uint16_t *apad = NULL;
+        size_t abytes = 0;
+        if (K8 != K)
+            ap = apad = stage16(dt, dt, a->dev, a_rows, K, K, a_rows, K8, 1, 0, &abytes);
+        if (ap) {
+            size_t sa = (s.abat && !fold) ? M * K8 : 0;
             if (s.bbat || Bw == 1) {
-                pgd_check(gemm16(dt, K, N, M8, at, M8, K * M8, gt, M8, N * M8, gb->dev, N, s.bbat ? K * N : 0,
-                                        Bw, bbeta, st),
-                          "wgrad");
+                gemm16(dt, 1, 1, K, N, Mw, ap, K8 != K ? K8 : K, sa, K8 != K ? K8 : K, g16, N8, Mw * N8, N8, gb->dev,
+                       N, s.bbat ? K * N : 0, Bw, bbeta, "wgrad");
             } else {
                 for (size_t z = 0; z < Bw; z++)
-                    pgd_check(gemm16(dt, K, N, M8, at + z * K * M8, M8, 0, gt + z * N * M8, M8, 0, gb->dev,
-                                            N, 0, 1, z == 0 ? bbeta : 1, st),
-                              "wgrad");
+                    gemm16(dt, 1, 1, K, N, Mw, ap + z * sa, K8 != K ? K8 : K, 0, K8 != K ? K8 : K, g16 + z * Mw * N8,
+                           N8, 0, N8, gb->dev, N, 0, 1, z == 0 ? bbeta : 1, "wgrad");
             }
         }
-        pgd_free(at, atb);
-        pgd_free(gt, gtb);
+        if (apad)
+            pgd_free(apad, abytes);
     }
+    pgd_free(g16, gbytes);
 }
 
 /* ---------------------------------------------------------------- pg_gemm* */
@@ -305,16 +329,24 @@ void pg_gemm_ex(pg_dtype dtype, size_t m, size_t n, size_t k, const void *a, siz
     }
     if (!m || !n)
         return;
-    pgk_stream st = pgd_stream();
     int dt = (int)dtype;
-    size_t K8 = up8(k);
-    size_t abytes = m * K8 * 2, bbytes = n * K8 * 2;
-    uint16_t *ap = tmp_alloc(abytes), *bt = tmp_alloc(bbytes);
-    if (ap && bt && pgd_check(pgk_copy_to16(dt, dt, a, m, k, lda, ap, K8, 1, 0, 0, st), "stage A") &&
-        pgd_check(pgk_transpose_to16(dt, dt, b, k, n, ldb, bt, K8, 1, 0, 0, st), "stage B^T"))
-        pgd_check(gemm16(dt, m, n, K8, ap, K8, 0, bt, K8, 0, c, ldc, 0, 1, 0, st), "pg_gemm_ex");
-    pgd_free(ap, abytes);
-    pgd_free(bt, bbytes);
+    /* A [m, k] (lda) K-contiguous, B [k, n] (ldb) n-contiguous: read in
+     * place when the leading dims and bases allow 16-byte loads and n is a
+     * multiple of 8; otherwise through zero-padded copies */
+    bool direct = !(lda & 7) && !(ldb & 7) && !(((uintptr_t)a | (uintptr_t)b) & 15) && !(n & 7);
+    if (direct) {
+        gemm16(dt, 0, 1, m, n, k, a, lda, 0, m, b, ldb, 0, n, c, ldc, 0, 1, 0, "pg_gemm_ex");
+        return;
+    }
+    size_t K8 = up8(k), N8 = up8(n) < 8 ? 8 : up8(n), ab, bbytes;
+    uint16_t *ap = stage16(dt, dt, a, m, k, lda, m, K8, 1, 0, &ab);
+    uint16_t *bp = ap ? stage16(dt, dt, b, k, n, ldb, K8, N8, 1, 0, &bbytes) : NULL;
+    if (ap && bp)
+        gemm16(dt, 0, 1, m, n, K8, ap, K8, 0, m, bp, N8, 0, N8, c, ldc, 0, 1, 0, "pg_gemm_ex");
+    if (ap)
+        pgd_free(ap, ab);
+    if (bp)
+        pgd_free(bp, bbytes);
 }
 
 void pg_hgemm(size_t m, size_t n, size_t k, const uint16_t *a, size_t lda, const uint16_t *b, size_t ldb, float *c,

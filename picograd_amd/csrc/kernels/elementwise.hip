@@ -339,52 +339,22 @@ __global__ void __launch_bounds__(kBlock) k_cast_from16(int dtype, const uint16_
         dst[j] = from16(dtype, src[j]);
 }
 
-// 64x64 tile transpose through LDS.  Source rows x cols (ld lds) of f32 or
-// 16-bit; destination cols x ldd 16-bit, zero-filled for r in [rows, ldd).
-template <typename TS>
-__global__ void __launch_bounds__(kBlock) k_transpose16(int dtype, const TS *__restrict__ src, size_t rows,
-                                                        size_t cols, size_t lds, uint16_t *__restrict__ dst,
-                                                        size_t ldd, size_t sstride, size_t dstride)
-{
-    __shared__ uint16_t tile[64][66];
-    const TS *s = src + (size_t)blockIdx.z * sstride;
-    uint16_t *d = dst + (size_t)blockIdx.z * dstride;
-    size_t r0 = (size_t)blockIdx.y * 64, c0 = (size_t)blockIdx.x * 64;
-    int tx = threadIdx.x & 63, ty = threadIdx.x >> 6; // 64 x 4
-    for (int yy = ty; yy < 64; yy += 4) {
-        size_t r = r0 + yy, c = c0 + tx;
-        uint16_t v = 0;
-        if (r < rows && c < cols) {
-            if constexpr (sizeof(TS) == 4)
-                v = to16(dtype, (float)s[r * lds + c]);
-            else
-                v = (uint16_t)s[r * lds + c];
-        }
-        tile[yy][tx] = v;
-    }
-    __syncthreads();
-    // write dst[c][r] for c in tile cols, r in tile rows (r up to ldd)
-    for (int yy = ty; yy < 64; yy += 4) {
-        size_t c = c0 + yy, r = r0 + tx;
-        if (c < cols && r < ldd)
-            d[c * ldd + r] = tile[tx][yy];
-    }
-}
-
+// dst[r * ldd + c] = cvt(src[r * lds + c]) for r < rows, c < cols; zeros
+// for the padding rows [rows, rows_pad) and columns [cols, ldd)
 template <typename TS>
 __global__ void __launch_bounds__(kBlock) k_copy16(int dtype, const TS *__restrict__ src, size_t rows, size_t cols,
                                                    size_t lds, uint16_t *__restrict__ dst, size_t ldd,
-                                                   size_t sstride, size_t dstride)
+                                                   size_t rows_pad, size_t sstride, size_t dstride)
 {
     const TS *s = src + (size_t)blockIdx.z * sstride;
     uint16_t *d = dst + (size_t)blockIdx.z * dstride;
-    size_t total = rows * ldd;
+    size_t total = rows_pad * ldd;
     size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     size_t stride = (size_t)gridDim.x * blockDim.x;
     for (size_t j = i; j < total; j += stride) {
         size_t r = j / ldd, c = j % ldd;
         uint16_t v = 0;
-        if (c < cols) {
+        if (r < rows && c < cols) {
             if constexpr (sizeof(TS) == 4)
                 v = to16(dtype, (float)s[r * lds + c]);
             else
@@ -583,40 +553,21 @@ extern "C" int pgk_cast_from16(int dtype, const uint16_t *src, float *dst, size_
     return status();
 }
 
-extern "C" int pgk_transpose_to16(int dtype, int src_dtype, const void *src, size_t rows, size_t cols,
-                                  size_t lds, uint16_t *dst, size_t ldd, size_t batch, size_t sstride,
-                                  size_t dstride, pgk_stream s)
-{
-    if (!rows || !cols || !batch)
-        return 0;
-    if (batch > 65535)
-        return (int)hipErrorInvalidValue;
-    size_t rr = ldd > rows ? ldd : rows; // cover the zero pad rows too
-    dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((rr + 63) / 64), (unsigned)batch);
-    if (src_dtype == 0)
-        hipLaunchKernelGGL(k_transpose16<float>, grid, dim3(kBlock), 0, (hipStream_t)s, dtype,
-                           (const float *)src, rows, cols, lds, dst, ldd, sstride, dstride);
-    else
-        hipLaunchKernelGGL(k_transpose16<uint16_t>, grid, dim3(kBlock), 0, (hipStream_t)s, dtype,
-                           (const uint16_t *)src, rows, cols, lds, dst, ldd, sstride, dstride);
-    return status();
-}
-
 extern "C" int pgk_copy_to16(int dtype, int src_dtype, const void *src, size_t rows, size_t cols, size_t lds,
-                             uint16_t *dst, size_t ldd, size_t batch, size_t sstride, size_t dstride,
-                             pgk_stream s)
+                             uint16_t *dst, size_t ldd, size_t rows_pad, size_t batch, size_t sstride,
+                             size_t dstride, pgk_stream s)
 {
-    if (!rows || !ldd || !batch)
+    if (!rows_pad || !ldd || !batch)
         return 0;
-    if (batch > 65535)
+    if (batch > 65535 || rows > rows_pad || cols > ldd)
         return (int)hipErrorInvalidValue;
-    dim3 grid((unsigned)grid_for(rows * ldd, 4), 1, (unsigned)batch);
+    dim3 grid((unsigned)grid_for(rows_pad * ldd, 4), 1, (unsigned)batch);
     if (src_dtype == 0)
         hipLaunchKernelGGL(k_copy16<float>, grid, dim3(kBlock), 0, (hipStream_t)s, dtype, (const float *)src,
-                           rows, cols, lds, dst, ldd, sstride, dstride);
+                           rows, cols, lds, dst, ldd, rows_pad, sstride, dstride);
     else
         hipLaunchKernelGGL(k_copy16<uint16_t>, grid, dim3(kBlock), 0, (hipStream_t)s, dtype,
-                           (const uint16_t *)src, rows, cols, lds, dst, ldd, sstride, dstride);
+                           (const uint16_t *)src, rows, cols, lds, dst, ldd, rows_pad, sstride, dstride);
     return status();
 }
 

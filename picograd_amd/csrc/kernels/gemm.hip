@@ -1,21 +1,36 @@
 // GEMM kernels for gfx950.
 //
-// k_gemm16_nt: C[i,j] (+)= sum_p A[i,p] * B[j,p] with f16/bf16 operands whose
-// reduction dim is contiguous ("NT"), f32 accumulation in MFMA
-// (v_mfma_f32_32x32x16_{bf16,f16}) and f32 output.  dgrad (dC . W^T) has
-// this layout natively; forward and wgrad operands are staged into it by
-// the transpose kernels.  Block tile BM x BN x 64, four wave64s as 2 x 2,
-// each wave owning a (BM/2) x (BN/2) sub-tile of 32x32 MFMA blocks.
-// Operand tiles go global -> registers -> LDS (double buffered, one barrier
-// per k-tile); the LDS rows are XOR-swizzled in 16-byte chunks so the
-// fragment reads of 8 or 16 consecutive lanes hit distinct banks.
-// Block ids are remapped so the tiles that share operand panels run on the
-// same XCD (and its L2), grouped GROUP_M tile-rows at a time.
+// k_gemm16: C[b][i, j] (beta ? += : =) sum_p A(i, p) B(p, j) with f16/bf16
+// operands, f32 accumulation in MFMA (v_mfma_f32_32x32x16_{bf16,f16}) and
+// f32 output.  Each operand is either "K-contiguous" (its reduction dim is
+// contiguous: A(i, p) = a[i * lda + p], B(p, j) = b[j * ldb + p]) or
+// "MN-contiguous" (A(i, p) = a[p * lda + i], B(p, j) = b[p * ldb + j]), so
+// dgrad (dC . W^T), wgrad (A^T . dC) and the forward product (A . W) all
+// read their operands where they lie, with no transposed copies.
+//
+// Data path, per block tile BM x BN x 64:
+//  - global -> LDS directly (global_load_lds_dwordx4: 64 lanes x 16 bytes
+//    per instruction, no staging registers) into a two-stage LDS ring; the
+//    next k-tile's loads are in flight while the current one is computed;
+//  - K-contiguous tiles sit in LDS as [rows][64] with 16-byte chunks
+//    XOR-swizzled by (r ^ r >> 3) & 7 and reach the MFMA with ds_read_b128;
+//    MN-contiguous tiles sit as [64][rows] with chunks swizzled by
+//    2 (k & 3) and reach it with ds_read_b64_tr_b16, the gfx950 transposing
+//    LDS read (within each 16-lane group, lane i of the result takes element
+//    i % 4 of the 8 bytes lane 4p + i / 4 addressed, for slot p);
+//  - fragment reads for the next 16-wide k step are issued before the MFMAs
+//    of the current one;
+//  - tiles are remapped so the blocks that share operand panels run on one
+//    XCD (and its L2), grouped 8 tile-rows at a time.
+// The k-loop requires K % 64 == 0: the host runs the last K % 64 columns
+// as one more launch over zero-padded copies (beta = 1).
 //
 // k_gemm_f32: plain LDS-tiled f32 FMA GEMM with either operand transposed,
 // for f32 matmuls (not on the bf16/f16 hot path).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <type_traits>
 
 #include "launch.h"
 
@@ -24,12 +39,15 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+#define LDS __attribute__((address_space(3)))
 
-constexpr int BK = 64;       // k elements per tile (8 chunks of 16 bytes)
-constexpr int kThreads = 256;
-constexpr int GROUP_M = 8;
+constexpr int BK = 64;
 
-__device__ __forceinline__ int swz(int chunk, int row) { return chunk ^ ((row & 7) ^ ((row >> 3) & 1)); }
+// s_waitcnt immediate waiting for vmcnt <= n only (gfx9 encoding: vmcnt in
+// bits 3:0 and 15:14; expcnt 6:4 and lgkmcnt 11:8 left at their maxima)
+constexpr int vmcnt_imm(int n) { return (n & 0xF) | 0x70 | 0xF00 | (((n >> 4) & 3) << 14); }
 
 template <bool F16>
 __device__ __forceinline__ f32x16 mfma32(const uint4 &a, const uint4 &b, const f32x16 &c)
@@ -42,72 +60,139 @@ __device__ __forceinline__ f32x16 mfma32(const uint4 &a, const uint4 &b, const f
                                                        __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
-template <int BM, int BN, bool F16>
-__global__ void __launch_bounds__(kThreads) k_gemm16_nt(const uint16_t *__restrict__ A, size_t lda, size_t sA,
-                                                        const uint16_t *__restrict__ B, size_t ldb, size_t sB,
-                                                        float *__restrict__ C, size_t ldc, size_t sC, int M, int N,
-                                                        int K, int beta, int tiles_m, int tiles_n)
+// One wave's 64 x 16-byte global -> LDS copy: lane i's bytes land at
+// M0 + 16 i.  Issued as asm so the compiler's wait insertion does not
+// track it (it would otherwise drain every such load before the next LDS
+// read); the k-loop waits on these loads explicitly.  M0 is reserved to
+// the compiler, which therefore ignores a clobber of it: the GEMM kernels
+// below generate no other M0 use (checked on their gfx950 assembly), so
+// writing it here disturbs nothing.
+__device__ __forceinline__ void dma16(const void *src, LDS uint4 *dst)
 {
-    constexpr int WM = BM / 2, WN = BN / 2;
-    constexpr int FM = WM / 32, FN = WN / 32;
-    constexpr int LA = BM * 8 / kThreads; // 16-byte chunks per thread per k-tile
-    constexpr int LB = BN * 8 / kThreads;
-    __shared__ uint4 smA[2][BM * 8];
-    __shared__ uint4 smB[2][BN * 8];
+    const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)dst);
+    __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src) : "memory");
+}
 
-    // ---- tile assignment: XCD-aware remap, then grouped row-major order
-    int nb = gridDim.x;
-    int pid = blockIdx.x;
+// K-contiguous operand tile: ROWS x 64, rows of eight 16-byte chunks.
+// Load instruction q of wave w fills chunk slots (w NQ + q) 64 .. + 63.
+template <int ROWS, int NT>
+struct TileK {
+    static constexpr int NQ = ROWS * 8 / NT;
+    static_assert(ROWS * 8 % NT == 0, "tile slots must divide by the thread count");
+    __device__ __forceinline__ static int swz(int chunk, int row) { return chunk ^ ((row ^ (row >> 3)) & 7); }
+
+    // rows past `extent` are clamped to its last row (their results are
+    // never stored); 1 <= extent
+    __device__ __forceinline__ static void load(const uint16_t *__restrict__ p, size_t ld, int row0, int extent,
+                                                int k0, LDS uint4 *dst, int tid)
+    {
+        const int lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+            const int base = (wave * NQ + q) * 64;
+            const int slot = base + lane;
+            const int row = slot >> 3;
+            const int logical = swz(slot & 7, row);
+            int gr = row0 + row;
+            gr = gr < extent ? gr : extent - 1;
+            dma16(p + (size_t)gr * ld + k0 + logical * 8, dst + base);
+        }
+    }
+
+    // MFMA operand fragment: rows r0 + lane % 32, k = 16 s + 8 (lane / 32) .. + 7
+    __device__ __forceinline__ static uint4 frag(const LDS uint4 *sm, int r0, int s, int lane)
+    {
+        const int r = r0 + (lane & 31);
+        const u32x4 v = ((const LDS u32x4 *)sm)[r * 8 + swz(2 * s + (lane >> 5), r)];
+        return __builtin_bit_cast(uint4, v);
+    }
+};
+
+// MN-contiguous operand tile: held as [64][ROWS] (k-major rows of ROWS
+// values), 16-byte chunks swizzled by 2 (k & 3) so the four k-rows one
+// transposing read touches fall in distinct banks.
+template <int ROWS, int NT>
+struct TileMN {
+    static constexpr int CPR = ROWS / 8;
+    static constexpr int NQ = BK * CPR / NT;
+    static_assert(BK * CPR % NT == 0, "tile slots must divide by the thread count");
+    __device__ __forceinline__ static int fk(int k) { return (k & 3) << 1; }
+
+    // columns past `extent` are clamped to its last 8 (never stored);
+    // extent % 8 == 0, extent >= 8
+    __device__ __forceinline__ static void load(const uint16_t *__restrict__ p, size_t ld, int row0, int extent,
+                                                int k0, LDS uint4 *dst, int tid)
+    {
+        const int lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+            const int base = (wave * NQ + q) * 64;
+            const int slot = base + lane;
+            const int k = slot / CPR;
+            const int logical = (slot % CPR) ^ fk(k);
+            int mn = row0 + logical * 8;
+            mn = mn < extent ? mn : extent - 8;
+            dma16(p + (size_t)(k0 + k) * ld + mn, dst + base);
+        }
+    }
+
+    // MFMA operand fragment from two ds_read_b64_tr_b16: in 16-lane group g
+    // source lane q points at [k0 + q / 4][R0 + 4 (q % 4)] and result lane i
+    // holds rows R0 + i, k = k0 .. k0 + 3 (R0 = r0 + 16 (g & 1),
+    // k0 = 16 s + 8 (g >> 1) + 4 h for half h)
+    __device__ __forceinline__ static uint4 frag(const LDS uint4 *sm, int r0, int s, int lane)
+    {
+        const int g = (lane >> 4) & 3, q = lane & 15;
+        const int mn = r0 + 16 * (g & 1) + 4 * (q & 3);
+        uint2 h2[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int k = 16 * s + 8 * (g >> 1) + 4 * h + (q >> 2);
+            const int byte = k * ROWS * 2 + (((mn >> 3) ^ fk(k)) << 4) + (mn & 7) * 2;
+            h2[h] = __builtin_bit_cast(
+                uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS v4s *)((const LDS char *)sm + byte)));
+        }
+        return make_uint4(h2[0].x, h2[0].y, h2[1].x, h2[1].y);
+    }
+};
+
+template <int BM, int BN, int WGM, int WGN, bool TA, bool TB, bool F16>
+__global__ void __launch_bounds__(64 * WGM * WGN, 1)
+    k_gemm16(const uint16_t *__restrict__ A, size_t lda, size_t sA, int a_extent, const uint16_t *__restrict__ B,
+             size_t ldb, size_t sB, int b_extent, float *__restrict__ C, size_t ldc, size_t sC, int M, int N, int K,
+             int beta, int tiles_m, int tiles_n)
+{
+    constexpr int NT = 64 * WGM * WGN;
+    constexpr int WM = BM / WGM, WN = BN / WGN;
+    constexpr int FM = WM / 32, FN = WN / 32;
+    using OA = typename std::conditional<TA, TileMN<BM, NT>, TileK<BM, NT>>::type;
+    using OB = typename std::conditional<TB, TileMN<BN, NT>, TileK<BN, NT>>::type;
+    // one array per stage, so each stage index below is a compile-time
+    // choice of array
+    __shared__ uint4 smA0[BM * 8], smA1[BM * 8];
+    __shared__ uint4 smB0[BN * 8], smB1[BN * 8];
+    LDS uint4 *const A0 = (LDS uint4 *)smA0, *const A1 = (LDS uint4 *)smA1;
+    LDS uint4 *const B0 = (LDS uint4 *)smB0, *const B1 = (LDS uint4 *)smB1;
+
+    // tile order: XCD-aware (block ids dealt round-robin to the 8 XCDs are
+    // regrouped so consecutive ids share an XCD), then 8 tile-rows at a time
+    int nb = gridDim.x, pid = blockIdx.x;
     if ((nb & 7) == 0)
         pid = (pid & 7) * (nb >> 3) + (pid >> 3);
-    int per_group = GROUP_M * tiles_n;
-    int group = pid / per_group;
-    int first_m = group * GROUP_M;
-    int gsz = tiles_m - first_m < GROUP_M ? tiles_m - first_m : GROUP_M;
-    int in_group = pid - group * per_group;
-    int tm = first_m + in_group % gsz;
-    int tn = in_group / gsz;
-    const int m0 = tm * BM, n0 = tn * BN;
+    const int GM = 8;
+    const int per_group = GM * tiles_n;
+    const int group = pid / per_group;
+    const int first_m = group * GM;
+    const int gsz = tiles_m - first_m < GM ? tiles_m - first_m : GM;
+    const int in_group = pid - group * per_group;
+    const int m0 = (first_m + in_group % gsz) * BM, n0 = (in_group / gsz) * BN;
 
     const uint16_t *Ab = A + (size_t)blockIdx.z * sA;
     const uint16_t *Bb = B + (size_t)blockIdx.z * sB;
     float *Cb = C + (size_t)blockIdx.z * sC;
 
-    const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int ch = tid & 7;   // chunk this thread stages
-    const int rbase = tid >> 3; // first row this thread stages (+32 per step)
-
-    uint4 ra[LA], rb[LB];
-    const uint4 zero = make_uint4(0, 0, 0, 0);
-
-    auto load_tiles = [&](int k0) {
-        const int kc = k0 + ch * 8;
-        const bool kin = kc < K;
-#pragma unroll
-        for (int i = 0; i < LA; ++i) {
-            int r = m0 + rbase + 32 * i;
-            ra[i] = (kin && r < M) ? *reinterpret_cast<const uint4 *>(Ab + (size_t)r * lda + kc) : zero;
-        }
-#pragma unroll
-        for (int i = 0; i < LB; ++i) {
-            int r = n0 + rbase + 32 * i;
-            rb[i] = (kin && r < N) ? *reinterpret_cast<const uint4 *>(Bb + (size_t)r * ldb + kc) : zero;
-        }
-    };
-    auto store_tiles = [&](int st) {
-#pragma unroll
-        for (int i = 0; i < LA; ++i) {
-            int r = rbase + 32 * i;
-            smA[st][r * 8 + swz(ch, r)] = ra[i];
-        }
-#pragma unroll
-        for (int i = 0; i < LB; ++i) {
-            int r = rbase + 32 * i;
-            smB[st][r * 8 + swz(ch, r)] = rb[i];
-        }
-    };
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WGN, wn = wave % WGN;
 
     f32x16 acc[FM][FN];
 #pragma unroll
@@ -118,43 +203,54 @@ __global__ void __launch_bounds__(kThreads) k_gemm16_nt(const uint16_t *__restri
             for (int e = 0; e < 16; ++e)
                 acc[i][j][e] = 0.0f;
 
-    const int KT = (K + BK - 1) / BK;
-    load_tiles(0);
-    store_tiles(0);
-    __syncthreads();
+    const int KT = K / BK;
+    OA::load(Ab, lda, m0, a_extent, 0, A0, tid);
+    OB::load(Bb, ldb, n0, b_extent, 0, B0, tid);
 
-    const int lrow = lane & 31, lk = lane >> 5;
-    int cur = 0;
-    for (int kt = 0; kt < KT; ++kt) {
-        if (kt + 1 < KT)
-            load_tiles((kt + 1) * BK);
+    auto step = [&](int kt, LDS uint4 *cA, LDS uint4 *cB, LDS uint4 *nA, LDS uint4 *nB) {
+        // this wave's loads of tile kt have landed; after the barrier every
+        // wave's have, and every wave is done reading tile kt-1 (the other
+        // stage).  A bare s_barrier: the fence of __syncthreads() would make
+        // the compiler drain outstanding memory operations first.  The
+        // empty asm statements keep LDS accesses from moving across it.
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        __asm__ volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        __asm__ volatile("" ::: "memory");
+        if (kt + 1 < KT) {
+            OA::load(Ab, lda, m0, a_extent, (kt + 1) * BK, nA, tid);
+            OB::load(Bb, ldb, n0, b_extent, (kt + 1) * BK, nB, tid);
+        }
+        uint4 fa[2][FM], fb[2][FN];
+        auto rd = [&](int s, uint4(&xa)[FM], uint4(&xb)[FN]) {
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+                xa[i] = OA::frag(cA, wm * WM + i * 32, s, lane);
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+                xb[j] = OB::frag(cB, wn * WN + j * 32, s, lane);
+        };
+        rd(0, fa[0], fb[0]);
 #pragma unroll
         for (int s = 0; s < BK / 16; ++s) {
-            const int chunk = s * 2 + lk;
-            uint4 fa[FM], fb[FN];
-#pragma unroll
-            for (int i = 0; i < FM; ++i) {
-                int r = wm * WM + i * 32 + lrow;
-                fa[i] = smA[cur][r * 8 + swz(chunk, r)];
-            }
-#pragma unroll
-            for (int j = 0; j < FN; ++j) {
-                int r = wn * WN + j * 32 + lrow;
-                fb[j] = smB[cur][r * 8 + swz(chunk, r)];
-            }
+            const int cur = s & 1;
+            if (s + 1 < BK / 16)
+                rd(s + 1, fa[cur ^ 1], fb[cur ^ 1]);
 #pragma unroll
             for (int i = 0; i < FM; ++i)
 #pragma unroll
                 for (int j = 0; j < FN; ++j)
-                    acc[i][j] = mfma32<F16>(fa[i], fb[j], acc[i][j]);
+                    acc[i][j] = mfma32<F16>(fa[cur][i], fb[cur][j], acc[i][j]);
         }
+    };
+    for (int kt = 0; kt < KT; kt += 2) {
+        step(kt, A0, B0, A1, B1);
         if (kt + 1 < KT)
-            store_tiles(cur ^ 1);
-        __syncthreads();
-        cur ^= 1;
+            step(kt + 1, A1, B1, A0, B0);
     }
 
-    // ---- epilogue: lane holds column lane%32 of rows (e/4)*8 + (lane/32)*4 + e%4
+    // epilogue: lane holds column lane % 32 of rows (e/4)*8 + (lane/32)*4 + e%4
+    const int lrow = lane & 31, lk = lane >> 5;
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
 #pragma unroll
@@ -167,11 +263,36 @@ __global__ void __launch_bounds__(kThreads) k_gemm16_nt(const uint16_t *__restri
                 const int row = m0 + wm * WM + i * 32 + (e >> 2) * 8 + lk * 4 + (e & 3);
                 if (row < M) {
                     float *p = Cb + (size_t)row * ldc + col;
-                    float v = acc[i][j][e];
+                    const float v = acc[i][j][e];
                     *p = beta ? *p + v : v;
                 }
             }
         }
+    }
+}
+
+// zero-padded copy of the k-slab [k0, k0 + kn) of an operand, kn <= 64:
+// K-contiguous -> dst[r * 64 + c], MN-contiguous -> dst[c * rows_pad + r]
+__global__ void __launch_bounds__(256) k_pack_slab(int mn_major, const uint16_t *__restrict__ src, size_t ld,
+                                                   size_t sstride, int rows, int rows_pad, int k0, int kn,
+                                                   uint16_t *__restrict__ dst, size_t dstride)
+{
+    const uint16_t *s = src + (size_t)blockIdx.z * sstride;
+    uint16_t *d = dst + (size_t)blockIdx.z * dstride;
+    const size_t total = (size_t)rows_pad * 64;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+        int r, c;
+        if (mn_major) {
+            c = (int)(i / rows_pad);
+            r = (int)(i % rows_pad);
+        } else {
+            r = (int)(i / 64);
+            c = (int)(i % 64);
+        }
+        uint16_t v = 0;
+        if (r < rows && c < kn)
+            v = mn_major ? s[(size_t)(k0 + c) * ld + r] : s[(size_t)r * ld + k0 + c];
+        d[i] = v;
     }
 }
 
@@ -231,52 +352,130 @@ __global__ void __launch_bounds__(256) k_gemm_f32(int ta, int tb, int M, int N, 
     }
 }
 
-template <int BM, int BN, bool F16>
-int launch16(size_t m, size_t n, size_t k, const uint16_t *a, size_t lda, size_t sa, const uint16_t *b, size_t ldb,
-             size_t sb, float *c, size_t ldc, size_t sc, size_t batch, int beta, hipStream_t s)
+struct gemm_args {
+    const uint16_t *a;
+    size_t lda, sa;
+    int a_extent;
+    const uint16_t *b;
+    size_t ldb, sb;
+    int b_extent;
+    float *c;
+    size_t ldc, sc;
+    int m, n, k, beta;
+    unsigned batch;
+};
+
+template <int BM, int BN, int WGM, int WGN, bool TA, bool TB, bool F16>
+int launch_tile(const gemm_args &g, hipStream_t s)
 {
-    int tm = (int)((m + BM - 1) / BM), tn = (int)((n + BN - 1) / BN);
-    dim3 grid((unsigned)(tm * tn), 1, (unsigned)batch);
-    hipLaunchKernelGGL((k_gemm16_nt<BM, BN, F16>), grid, dim3(kThreads), 0, s, a, lda, sa, b, ldb, sb, c, ldc, sc,
-                       (int)m, (int)n, (int)k, beta, tm, tn);
+    const int tm = (g.m + BM - 1) / BM, tn = (g.n + BN - 1) / BN;
+    hipLaunchKernelGGL((k_gemm16<BM, BN, WGM, WGN, TA, TB, F16>), dim3((unsigned)(tm * tn), 1, g.batch),
+                       dim3(64 * WGM * WGN), 0, s, g.a, g.lda, g.sa, g.a_extent, g.b, g.ldb, g.sb, g.b_extent, g.c,
+                       g.ldc, g.sc, g.m, g.n, g.k, g.beta, tm, tn);
     return (int)hipGetLastError();
+}
+
+template <bool TA, bool TB, bool F16>
+int launch_layout(const gemm_args &g, hipStream_t s)
+{
+    // 256 x 256 tiles (eight waves, each 128 x 64) whenever they still give
+    // most CUs a tile; else 128 x 128 (four waves, each 64 x 64)
+    const size_t big = (size_t)((g.m + 255) / 256) * ((g.n + 255) / 256) * g.batch;
+    if (big >= 128)
+        return launch_tile<256, 256, 2, 4, TA, TB, F16>(g, s);
+    return launch_tile<128, 128, 2, 2, TA, TB, F16>(g, s);
+}
+
+int launch_any(int f16, int ta, int tb, const gemm_args &g, hipStream_t s)
+{
+    const int sel = (f16 ? 4 : 0) | (ta ? 2 : 0) | (tb ? 1 : 0);
+    switch (sel) {
+    case 0: return launch_layout<false, false, false>(g, s);
+    case 1: return launch_layout<false, true, false>(g, s);
+    case 2: return launch_layout<true, false, false>(g, s);
+    case 3: return launch_layout<true, true, false>(g, s);
+    case 4: return launch_layout<false, false, true>(g, s);
+    case 5: return launch_layout<false, true, true>(g, s);
+    case 6: return launch_layout<true, false, true>(g, s);
+    default: return launch_layout<true, true, true>(g, s);
+    }
 }
 
 } // namespace
 
-extern "C" int pgk_gemm16_nt(int dtype, size_t m, size_t n, size_t k, const uint16_t *a, size_t lda,
-                             size_t stride_a, const uint16_t *b, size_t ldb, size_t stride_b, float *c, size_t ldc,
-                             size_t stride_c, size_t batch, int beta, pgk_stream s)
+extern "C" size_t pgk_gemm16_workspace(int ta, int tb, size_t m, size_t n, size_t k, size_t batch)
+{
+    if (k % BK == 0)
+        return 0;
+    const size_t ma = (m + 7) & ~(size_t)7, nb = (n + 7) & ~(size_t)7;
+    const size_t a = (ta ? 64 * (ma < 8 ? 8 : ma) : 64 * m) * batch;
+    const size_t b = (tb ? 64 * (nb < 8 ? 8 : nb) : 64 * n) * batch;
+    return (a + 64 + b) * sizeof(uint16_t);
+}
+
+extern "C" int pgk_gemm16(int dtype, int ta, int tb, size_t m, size_t n, size_t k, const uint16_t *a, size_t lda,
+                          size_t stride_a, size_t a_extent, const uint16_t *b, size_t ldb, size_t stride_b,
+                          size_t b_extent, float *c, size_t ldc, size_t stride_c, size_t batch, int beta, void *ws,
+                          pgk_stream s)
 {
     if (!m || !n || !batch)
         return 0;
-    if ((lda & 7) || (ldb & 7) || (((uintptr_t)a | (uintptr_t)b) & 15) || (k & 7) || batch > 65535 ||
-        m > 0x7fffffff || n > 0x7fffffff || k > 0x7fffffff)
+    if (m > 0x7fffffff || n > 0x7fffffff || k > 0x7fffffff || batch > 65535)
         return (int)hipErrorInvalidValue;
+    // 16-byte global loads: aligned bases, leading dims and batch strides
+    if ((((uintptr_t)a | (uintptr_t)b) & 15) || (lda & 7) || (ldb & 7) || (stride_a & 7) || (stride_b & 7))
+        return (int)hipErrorInvalidValue;
+    // the clamped loads stay inside [0, extent) of each operand
+    if (!a_extent || !b_extent || (ta && ((a_extent & 7) || a_extent < m)) || (tb && ((b_extent & 7) || b_extent < n)) ||
+        (!ta && a_extent < m) || (!tb && b_extent < n) || a_extent > 0x7fffffff || b_extent > 0x7fffffff)
+        return (int)hipErrorInvalidValue;
+    hipStream_t st = (hipStream_t)s;
+    const int f16 = dtype == 1;
+    const size_t kmain = k - k % BK, ktail = k % BK;
     if (!k) { // empty reduction: C = beta ? C : 0
         if (beta)
             return 0;
         for (size_t z = 0; z < batch; ++z)
             for (size_t r = 0; r < m; ++r) {
-                hipError_t e = hipMemsetAsync(c + z * stride_c + r * ldc, 0, n * sizeof(float), (hipStream_t)s);
+                hipError_t e = hipMemsetAsync(c + z * stride_c + r * ldc, 0, n * sizeof(float), st);
                 if (e)
                     return (int)e;
             }
         return 0;
     }
-    hipStream_t st = (hipStream_t)s;
-    // big tiles when they still give every CU work; else 128 x 128
-    size_t big_tiles = ((m + 255) / 256) * ((n + 127) / 128) * batch;
-    bool f16 = dtype == 1;
-    if (big_tiles >= 192)
-        return f16 ? launch16<256, 128, true>(m, n, k, a, lda, stride_a, b, ldb, stride_b, c, ldc, stride_c, batch,
-                                              beta, st)
-                   : launch16<256, 128, false>(m, n, k, a, lda, stride_a, b, ldb, stride_b, c, ldc, stride_c, batch,
-                                               beta, st);
-    return f16 ? launch16<128, 128, true>(m, n, k, a, lda, stride_a, b, ldb, stride_b, c, ldc, stride_c, batch, beta,
-                                          st)
-               : launch16<128, 128, false>(m, n, k, a, lda, stride_a, b, ldb, stride_b, c, ldc, stride_c, batch, beta,
-                                           st);
+    if (kmain) {
+        gemm_args g = {a, lda, stride_a, (int)a_extent, b, ldb, stride_b, (int)b_extent, c, ldc, stride_c,
+                       (int)m, (int)n, (int)kmain, beta, (unsigned)batch};
+        int rc = launch_any(f16, ta, tb, g, st);
+        if (rc)
+            return rc;
+    }
+    if (ktail) {
+        if (!ws)
+            return (int)hipErrorInvalidValue;
+        // last k-slab of each operand, zero-padded to 64 (and to a multiple
+        // of 8 columns for an MN-contiguous copy), then one more launch
+        const size_t ma = ta ? (((m + 7) & ~(size_t)7) < 8 ? 8 : ((m + 7) & ~(size_t)7)) : m;
+        const size_t nbp = tb ? (((n + 7) & ~(size_t)7) < 8 ? 8 : ((n + 7) & ~(size_t)7)) : n;
+        uint16_t *pa = (uint16_t *)ws;
+        const size_t asz = 64 * ma;
+        uint16_t *pb = pa + ((asz * batch + 63) & ~(size_t)63);
+        const size_t bsz = 64 * nbp;
+        const unsigned ga = (unsigned)((asz + 255) / 256 < 4096 ? (asz + 255) / 256 : 4096);
+        const unsigned gb = (unsigned)((bsz + 255) / 256 < 4096 ? (bsz + 255) / 256 : 4096);
+        hipLaunchKernelGGL(k_pack_slab, dim3(ga, 1, (unsigned)batch), dim3(256), 0, st, ta, a, lda, stride_a, (int)m,
+                           (int)ma, (int)kmain, (int)ktail, pa, asz);
+        hipLaunchKernelGGL(k_pack_slab, dim3(gb, 1, (unsigned)batch), dim3(256), 0, st, tb, b, ldb, stride_b, (int)n,
+                           (int)nbp, (int)kmain, (int)ktail, pb, bsz);
+        int rc = (int)hipGetLastError();
+        if (rc)
+            return rc;
+        gemm_args g = {pa, ta ? ma : (size_t)64, asz, (int)(ta ? ma : m), pb, tb ? nbp : (size_t)64, bsz,
+                       (int)(tb ? nbp : n), c, ldc, stride_c, (int)m, (int)n, BK, kmain ? 1 : beta,
+                       (unsigned)batch};
+        return launch_any(f16, ta, tb, g, st);
+    }
+    return 0;
 }
 
 extern "C" int pgk_gemm_f32(int ta, int tb, size_t m, size_t n, size_t k, const float *a, size_t lda,

@@ -68,28 +68,33 @@ int pgk_sum_axis_f32(const float *x, float *y, size_t outer, size_t len, size_t 
 int pgk_cast_to16(int dtype, const float *src, uint16_t *dst, size_t n, pgk_stream s);
 int pgk_cast_from16(int dtype, const uint16_t *src, float *dst, size_t n, pgk_stream s);
 /*
- * Staging for the MFMA GEMMs: dst[c * ldd + r] = cvt(src[r * lds + c]) for a
- * rows x cols source (transposed copy), dst padded with zeros for
- * r in [rows, ldd) when pad != 0.  src_dtype 0 = f32 (rounded to dtype),
- * else 16-bit of the same dtype.  batch copies use the given strides.
+ * Operand staging for the MFMA GEMM (only where a dimension needs padding
+ * to a multiple of 8, and for the f32 -> 16-bit cast of an upstream grad):
+ * dst[r * ldd + c] = cvt(src[r * lds + c]) for r < rows, c < cols, zeros
+ * for rows [rows, rows_pad) and columns [cols, ldd).  src_dtype 0 = f32
+ * (rounded to dtype), else 16-bit of the same dtype; batch copies use the
+ * given strides.
  */
-int pgk_transpose_to16(int dtype, int src_dtype, const void *src, size_t rows, size_t cols,
-                       size_t lds, uint16_t *dst, size_t ldd, size_t batch, size_t sstride,
-                       size_t dstride, pgk_stream s);
-/* dst[r * ldd + c] = cvt(src[r * lds + c]), zero pad for c in [cols, ldd) */
 int pgk_copy_to16(int dtype, int src_dtype, const void *src, size_t rows, size_t cols, size_t lds,
-                  uint16_t *dst, size_t ldd, size_t batch, size_t sstride, size_t dstride,
+                  uint16_t *dst, size_t ldd, size_t rows_pad, size_t batch, size_t sstride, size_t dstride,
                   pgk_stream s);
 
 /*
- * C[b][i, j] (beta ? += : =) sum_p A[b][i, p] * B[b][j, p]
- * f16/bf16 operands, both with the reduction dim contiguous ("NT"), f32
- * accumulate and output.  lda/ldb multiples of 8, bases 16-byte aligned,
- * k padded with zeros up to a multiple of 8 (the staging kernels ensure it).
+ * C[b][i, j] (beta ? += : =) sum_p A(i, p) B(p, j), f16 (dtype 1) or bf16
+ * (dtype 2) operands, f32 accumulate and output.
+ *   ta = 0: A(i, p) = a[i * lda + p]    ta = 1: A(i, p) = a[p * lda + i]
+ *   tb = 0: B(p, j) = b[j * ldb + p]    tb = 1: B(p, j) = b[p * ldb + j]
+ * Requirements: a, b 16-byte aligned; lda, ldb, batch strides multiples of
+ * 8.  a_extent / b_extent bound the loads along each operand's i (j) dim:
+ * at least m (n), and for an operand with that dim contiguous (ta / tb) a
+ * multiple of 8 whose columns [m, a_extent) may be read (zero-padding or
+ * real data; never used in the result).  When k % 64 != 0, `ws` must hold
+ * pgk_gemm16_workspace(...) bytes (it stages the last k-slab).
  */
-int pgk_gemm16_nt(int dtype, size_t m, size_t n, size_t k, const uint16_t *a, size_t lda,
-                  size_t stride_a, const uint16_t *b, size_t ldb, size_t stride_b, float *c,
-                  size_t ldc, size_t stride_c, size_t batch, int beta, pgk_stream s);
+size_t pgk_gemm16_workspace(int ta, int tb, size_t m, size_t n, size_t k, size_t batch);
+int pgk_gemm16(int dtype, int ta, int tb, size_t m, size_t n, size_t k, const uint16_t *a, size_t lda,
+               size_t stride_a, size_t a_extent, const uint16_t *b, size_t ldb, size_t stride_b, size_t b_extent,
+               float *c, size_t ldc, size_t stride_c, size_t batch, int beta, void *ws, pgk_stream s);
 
 /* f32 GEMM, C (beta ? += : =) op(A) op(B); ta/tb select A^T / B^T
  * (A(i,p) = ta ? a[p*lda+i] : a[i*lda+p], same for B(p,j)). */

@@ -238,6 +238,54 @@ def test_matmul_backward_16bit_matches_oracle(lib, oracle, dtype, M, K, N):
         lib.pg_node_free(n)
 
 
+@pytest.mark.parametrize("dtype", [BF16, F16])
+@pytest.mark.parametrize("abat,wbat", [(True, True), (True, False), (False, True)])
+def test_matmul_backward_batched_matches_oracle(lib, oracle, dtype, abat, wbat):
+    """Batched 16-bit matmul backward (autograd.c:592-610): both operands
+    batched; only A batched (the batch folds into the wgrad reduction);
+    only W batched (dA accumulates over the batch).  K and N ragged, so the
+    k-tail and padding paths run."""
+    Bt, M, K, N = 3, 72, 40, 100
+    rng = np.random.default_rng(Bt * 100 + abat * 10 + wbat)
+    ash = (Bt, M, K) if abat else (M, K)
+    wsh = (Bt, K, N) if wbat else (K, N)
+    a16 = oracle.cast16(dtype, rng.standard_normal(ash).astype(np.float32))
+    w16 = oracle.cast16(dtype, (0.05 * rng.standard_normal(wsh)).astype(np.float32))
+    dc = rng.standard_normal((Bt, M, N)).astype(np.float32)
+    na, nw = lib.var(a16, dtype=dtype), lib.var(w16, dtype=dtype)
+    c = lib.op("matmul", na, nw)
+    assert lib.shape(lib.node(c).value) == (Bt, M, N)
+    seed = lib.tensor(dc)
+    lib.pg_amd_backward_from(c, seed)
+    dA, dW = lib.grad(na), lib.grad(nw)
+    dc16 = oracle.cast16(dtype, dc)
+    ra = [oracle.gemm(dtype, dc16[z], w16[z] if wbat else w16, tb=True, f64=True) for z in range(Bt)]
+    rw = [oracle.gemm(dtype, a16[z] if abat else a16, dc16[z], ta=True, f64=True) for z in range(Bt)]
+    ref_dA = np.stack(ra) if abat else np.sum(ra, axis=0)
+    ref_dW = np.stack(rw) if wbat else np.sum(rw, axis=0)
+    assert rel_fro(dA, ref_dA) <= 1e-5
+    assert rel_fro(dW, ref_dW) <= 1e-5
+    lib.pg_tensor_free(seed)
+    for n in (c, na, nw):
+        lib.pg_node_free(n)
+
+
+@pytest.mark.parametrize("dtype", [BF16, F16])
+@pytest.mark.parametrize("M,K,N", [(520, 256, 264), (300, 200, 10), (8, 64, 8), (1, 8, 1)])
+def test_matmul_forward_16bit_matches_oracle(lib, oracle, dtype, M, K, N):
+    """pg_matmul on 16-bit operands (matmul.c:186-284): f32 output of
+    f32-accumulated products; tiles of both sizes, padded N (the 10-wide
+    output layer of config 5) and single-element edges."""
+    rng = np.random.default_rng(M + K + N)
+    a16 = oracle.cast16(dtype, rng.standard_normal((M, K)).astype(np.float32))
+    w16 = oracle.cast16(dtype, rng.standard_normal((K, N)).astype(np.float32))
+    na, nw = lib.var(a16, dtype=dtype), lib.var(w16, dtype=dtype)
+    c = lib.op("matmul", na, nw)
+    assert rel_fro(lib.value(c), oracle.gemm(dtype, a16, w16, f64=True)) <= 1e-5
+    for n in (c, na, nw):
+        lib.pg_node_free(n)
+
+
 # ---------------------------------------------------------------- JIT API
 
 def _jit_run(lib, build, inputs):
