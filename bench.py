@@ -233,6 +233,15 @@ def bench_c2(L, ev, steps, warmup, R=16384, Cc=4096):
     }
 
 
+def _ref_threads() -> int:
+    """Threads of the reference's pool: PICOGRAD_THREADS, else the online
+    CPU count capped at 64 (thread/pool.c:59, :99-141)."""
+    env = os.environ.get("PICOGRAD_THREADS")
+    if env and env.isdigit() and int(env) > 0:
+        return min(int(env), 64)
+    return min(os.cpu_count() or 1, 64)
+
+
 def cpu_c2(rows=2048, Cc=4096, budget_s=20.0):
     """The reference CPU path (oracle/_ref) on a row sample of config 2."""
     from oracle_lib import REF_SO
@@ -253,8 +262,7 @@ def cpu_c2(rows=2048, Cc=4096, budget_s=20.0):
         R.pg_node_free(n)
     t = float(np.median(times))
     nbytes = 16 * rows * Cc + 8 * Cc
-    threads = int(os.environ.get("PICOGRAD_THREADS", min(os.cpu_count() or 1, 64)))
-    return {"value": nbytes / t / 1e9, "unit": "GB/s", "cores": threads, "kind": "reference",
+    return {"value": nbytes / t / 1e9, "unit": "GB/s", "cores": _ref_threads(), "kind": "reference",
             "sample": f"config 2 at [{rows},{Cc}] (of [16384,{Cc}]), reference pg_backward "
                       f"(hybrid JIT + eager, the pool capped at 64 threads; the JIT loop, "
                       f"GELU' and dbias loops are single-threaded), median of {len(times)}",
@@ -333,6 +341,104 @@ def cpu_c3(M=1024, K=4096, N=4096, budget_s=20.0):
     return {"value": flops / t / 1e12, "unit": "TFLOP/s", "sample": f"M={M} of 8192", "ms": t * 1e3}
 
 
+# ---------------------------------------------------------------- config 5
+
+C5_DIMS = (1024, 4096, 4096, 4096, 10)
+C5_BATCH = 4096
+
+
+def c5_counts(dims=C5_DIMS, batch=C5_BATCH):
+    """GEMM FLOP per step (forward, wgrad of every layer, dgrad of layers
+    2..L) and SGD bytes (p, buf read + write, g read = 20 B per parameter,
+    plus the 2 B bf16 weight copy written for each weight the GEMMs read
+    unpadded)."""
+    kn = [dims[i] * dims[i + 1] for i in range(len(dims) - 1)]
+    fwd = 2 * batch * sum(kn)
+    bwd = 2 * batch * sum(kn) + 2 * batch * sum(kn[1:])
+    params = sum(kn) + sum(dims[1:])
+    shadow = sum(k for k, i in zip(kn, range(len(kn))) if dims[i] % 8 == 0 and dims[i + 1] % 8 == 0)
+    return fwd, bwd, params, 20 * params + 2 * shadow
+
+
+def bench_c5(L, ev, steps, warmup, dims=C5_DIMS, batch=C5_BATCH):
+    """Config 5: forward + pg_backward + pg_sgd_step of the bf16-GEMM MLP."""
+    from picograd_amd.capi import BF16, shape_arg
+    from picograd_amd.mlp import Mlp
+    log(f"[c5] MLP {dims}, batch {batch}, bf16 GEMM operands, f32 masters")
+    L.pg_seed(46)
+    nd, sh = shape_arg((batch, dims[0]))
+    x = L._check(L.pg_var_normal(nd, sh, 0.0, 1.0, False))
+    nd, sh = shape_arg((batch, dims[-1]))
+    t = L._check(L.pg_var_normal(nd, sh, 0.0, 1.0, False))
+    mlp = Mlp.seeded(L, dims, BF16)
+    loss0 = mlp.step(x, t, keep_loss=True)
+    first = float(L.value(loss0)[0])
+    L.pg_node_free(loss0)
+    for _ in range(max(0, warmup - 1)):
+        mlp.step(x, t)
+    L.sync()
+    L.pg_amd_timer_reset()
+    L.pg_amd_timer_enable(1)
+    ev.time(lambda: mlp.step(x, t), steps)
+    L.pg_amd_timer_enable(0)
+    g_ms, g_n = timer_ms(L, T_GEMM16)
+    s_ms, s_n = timer_ms(L, T_SGD)
+    j_ms, j_n = timer_ms(L, T_JIT_MAIN)
+    f_ms, f_n = timer_ms(L, T_JIT_FIN)
+    L.pg_amd_timer_reset()
+    ms = ev.time(lambda: mlp.step(x, t), steps)
+    lossN = mlp.step(x, t, keep_loss=True)
+    last = float(L.value(lossN)[0])
+    L.pg_node_free(lossN)
+    mlp.free()
+    L.pg_node_free(x)
+    L.pg_node_free(t)
+    L.sync()
+    fwd, bwd, params, sgd_bytes = c5_counts(dims, batch)
+    step_ms = ms / steps
+    gemm_ms = g_ms / steps
+    sgd_ms = s_ms / max(s_n, 1)
+    return {"steps_per_s": 1e3 / step_ms, "step_ms": step_ms, "gemm_flop": fwd + bwd,
+            "step_tflops": (fwd + bwd) / (step_ms * 1e-3) / 1e12,
+            "gemm_ms_per_step": gemm_ms, "gemm_tflops": (fwd + bwd) / (gemm_ms * 1e-3) / 1e12,
+            "gemm_launches_per_step": g_n / steps,
+            "sgd_ms": sgd_ms, "sgd_gbs": sgd_bytes / (sgd_ms * 1e-3) / 1e9, "sgd_bytes": sgd_bytes,
+            "params": params, "fused_bwd_ms_per_step": (j_ms + f_ms) / steps,
+            "loss_first": first, "loss_last": last, "steps_run": 1 + max(0, warmup - 1) + 2 * steps + 1}
+
+
+def cpu_c5(dims=C5_DIMS, batch=C5_BATCH, budget_s=25.0):
+    """The reference's CPU path for config 5 at full shape in f32 (its matmul
+    cannot take bf16 weights with f32 activations): pg_ag_matmul + add +
+    gelu layers, mse, pg_backward, pg_sgd_step, timed per step."""
+    from oracle_lib import REF_SO
+    from picograd_amd.capi import F32, PgLib, shape_arg
+    from picograd_amd.mlp import Mlp
+    if not REF_SO.exists():
+        return None
+    R = PgLib(REF_SO, device=False)
+    R.pg_seed(46)
+    nd, sh = shape_arg((batch, dims[0]))
+    x = R._check(R.pg_var_normal(nd, sh, 0.0, 1.0, False))
+    nd, sh = shape_arg((batch, dims[-1]))
+    t = R._check(R.pg_var_normal(nd, sh, 0.0, 1.0, False))
+    mlp = Mlp.seeded(R, dims, F32)
+    times = []
+    t0 = time.perf_counter()
+    # another step only while it fits the budget (one step is ~10-20 s)
+    while len(times) < 3 and (not times or time.perf_counter() - t0 + times[-1] < budget_s):
+        s = time.perf_counter()
+        mlp.step(x, t)
+        times.append(time.perf_counter() - s)
+    mlp.free()
+    R.pg_node_free(x)
+    R.pg_node_free(t)
+    sec = float(np.median(times))
+    return {"value": 1.0 / sec, "unit": "steps/s", "cores": _ref_threads(),
+            "kind": "reference", "sample": f"{len(times)} full config-5 steps in f32 (first included)",
+            "ms": sec * 1e3}
+
+
 # ---------------------------------------------------------------- config 1
 
 def bench_c1(L, iters=2000):
@@ -372,7 +478,7 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="c2,c3,c1")
+    ap.add_argument("--only", default="c2,c3,c1,c5")
     ap.add_argument("--calib", action="store_true",
                     help="first run a plain copy kernel of known size (the HBM counter calibration)")
     ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 counter passes")
@@ -406,6 +512,9 @@ def main(argv=None):
     if "c1" in only:
         extra["c1_chain_64x64"] = bench_c1(L)
         log(f"[c1] {extra['c1_chain_64x64']}")
+    if "c5" in only:
+        extra["c5_mlp_train_step"] = bench_c5(L, ev, max(3, a.steps // 2), a.warmup)
+        log(f"[c5] {extra['c5_mlp_train_step']}")
     cpu = None
     if not a.no_cpu:
         log("[cpu] reference CPU path, config 2 sample")
@@ -415,6 +524,11 @@ def main(argv=None):
             c3cpu = cpu_c3()
             if c3cpu:
                 extra.setdefault("c3_bf16_dgrad_wgrad", {})["cpu_reference"] = c3cpu
+        if "c5" in only and cpu is not None:
+            log("[cpu] reference CPU path, config 5 (f32)")
+            c5cpu = cpu_c5()
+            if c5cpu:
+                extra.setdefault("c5_mlp_train_step", {})["cpu_reference"] = c5cpu
     out = {
         "metric": "fused-bwd HBM GB/s",
         "value": round(c2["gbs"], 2),

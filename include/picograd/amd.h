@@ -37,6 +37,20 @@ void pg_amd_release_cached(void);
  * run the backward.  The fused loss-suffix JIT does not apply here. */
 void pg_amd_backward_from(pg_node *root, const pg_tensor *seed);
 
+/* Mixed-precision matmul of f32 nodes, A [M, K] . B [K, N] -> f32 [M, N],
+ * computed on the MFMA units: both operands are rounded to `dtype`
+ * (PG_DTYPE_BF16 or PG_DTYPE_F16, round to nearest even) and the products
+ * accumulated in f32.  Backward rounds the upstream grad the same way and
+ * accumulates f32 grads into both operands: dA += q(dC).q(B)^T,
+ * dB += q(A)^T.q(dC).  The rounded copy of each operand is kept with its
+ * storage and reused until the tensor is written again; pg_sgd_step
+ * rewrites it for a parameter in the same pass as the update, so the GEMMs
+ * of a bf16-weight layer read bf16 weights without a cast per step.
+ * Returns NULL (pg_autograd_last_error) for other dtypes or shapes.
+ * The reference's matmul requires one dtype on both sides
+ * (ops/matmul.c:191) and has no cast op, so it has no counterpart. */
+pg_node *pg_amd_ag_matmul16(pg_node *a, pg_node *b, pg_dtype dtype);
+
 /* JIT compile statistics: programs compiled by hiprtc, and cache lookups
  * that found a loaded kernel. */
 size_t pg_amd_jit_compiles(void);

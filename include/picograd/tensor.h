@@ -31,6 +31,11 @@ typedef struct pg_data_ref {
     void *ptr;     /* device allocation */
     size_t nbytes;
     int refs;
+    /* ---- appended: 16-bit (RNE) copy of f32 elements kept beside the
+     * storage for the MFMA GEMMs (pg_amd_ag_matmul16); library-internal */
+    void *shadow;
+    int shadow_dtype;  /* PG_DTYPE_F16 or PG_DTYPE_BF16 */
+    bool shadow_stale; /* an in-place write happened after it was made */
 } pg_data_ref;
 
 typedef struct pg_tensor {

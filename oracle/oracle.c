@@ -377,3 +377,105 @@ float orc_mse_grad_scale(size_t ndim, const size_t *shape, bool mean)
         return 2.0f;
     return 2.0f * (1.0f / (float)shape[ndim - 1]);
 }
+
+/* ---------------- config-5 MLP training step ---------------- */
+
+void orc_mlp_step(int dtype, size_t L, const size_t *dims, size_t batch,
+                  const float *x, const float *target, float *const *W,
+                  float *const *b, float *const *Wbuf, float *const *bbuf,
+                  float *const *dW, float *const *db, float lr,
+                  float momentum, float dampening, float weight_decay,
+                  bool nesterov, float *loss, int nthreads)
+{
+    /* forward (nn.c:117-125 per layer: matmul then broadcast bias add;
+     * gelu activations.c:166-173 between layers):
+     *   z_l = q(h_{l-1}) . q(W_l) + b_l,  h_l = gelu(z_l),  out = z_L
+     * q rounds to dtype (identity for ORC_F32); products accumulate in f32. */
+    size_t B = batch, maxd = 0;
+    for (size_t l = 0; l <= L; l++)
+        if (dims[l] > maxd)
+            maxd = dims[l];
+    float **z = calloc(L + 1, sizeof *z), **h = calloc(L + 1, sizeof *h);
+    float *qw = malloc(maxd * maxd * sizeof(float));
+    float *qh = malloc(B * maxd * sizeof(float));
+    float *g = malloc(B * maxd * sizeof(float));
+    float *gprev = malloc(B * maxd * sizeof(float));
+    for (size_t l = 1; l <= L; l++) {
+        z[l] = malloc(B * dims[l] * sizeof(float));
+        h[l] = malloc(B * dims[l] * sizeof(float));
+    }
+    h[0] = (float *)x;
+    for (size_t l = 1; l <= L; l++) {
+        size_t K = dims[l - 1], N = dims[l];
+        memcpy(qh, h[l - 1], B * K * sizeof(float));
+        orc_round_f32(dtype, qh, B * K);
+        memcpy(qw, W[l - 1], K * N * sizeof(float));
+        orc_round_f32(dtype, qw, K * N);
+        orc_gemm_acc32(ORC_F32, 0, 0, B, N, K, qh, K, qw, N, z[l], N, 0, nthreads);
+        for (size_t i = 0; i < B; i++)
+            for (size_t j = 0; j < N; j++) {
+                z[l][i * N + j] += b[l - 1][j];
+                h[l][i * N + j] = orc_gelu(z[l][i * N + j]);
+            }
+    }
+    /* loss = mean_all((out - t)^2): sum over rows, then the mean over the
+     * last axis (autograd.c:1018-1043, :1758-1771) */
+    size_t NL = dims[L];
+    double acc = 0.0;
+    for (size_t i = 0; i < B * NL; i++) {
+        double d = (double)z[L][i] - (double)target[i];
+        acc += d * d;
+    }
+    *loss = (float)(acc / (double)NL);
+    /* d(loss)/d(out): the fused suffix hands g = 1/NL to mul(d, d), whose
+     * two operand grads g*d add up (autograd.c:2166-2297, :2289-2295) */
+    const float scale = 1.0f / (float)NL;
+    for (size_t i = 0; i < B * NL; i++) {
+        float d = z[L][i] - target[i];
+        g[i] = scale * d + scale * d;
+    }
+    for (size_t l = L; l >= 1; l--) {
+        size_t K = dims[l - 1], N = dims[l];
+        /* g = dL/dz_l.  Bias grad: rows summed in order (autograd.c:364-387) */
+        for (size_t j = 0; j < N; j++)
+            db[l - 1][j] = 0.0f;
+        for (size_t i = 0; i < B; i++)
+            for (size_t j = 0; j < N; j++)
+                db[l - 1][j] += g[i * N + j];
+        /* GEMM grads of the matmul (autograd.c:561-706) on rounded operands:
+         * dW = q(h_{l-1})^T . q(g),  dh_{l-1} = q(g) . q(W_l)^T */
+        float *qg = malloc(B * N * sizeof(float));
+        memcpy(qg, g, B * N * sizeof(float));
+        orc_round_f32(dtype, qg, B * N);
+        memcpy(qh, h[l - 1], B * K * sizeof(float));
+        orc_round_f32(dtype, qh, B * K);
+        orc_gemm_acc32(ORC_F32, 1, 0, K, N, B, qh, K, qg, N, dW[l - 1], N, 0, nthreads);
+        if (l > 1) {
+            memcpy(qw, W[l - 1], K * N * sizeof(float));
+            orc_round_f32(dtype, qw, K * N);
+            orc_gemm_acc32(ORC_F32, 0, 1, B, K, N, qg, N, qw, N, gprev, K, 0, nthreads);
+            /* through gelu (grad_gelu, autograd.c:794-801) */
+            for (size_t i = 0; i < B * K; i++)
+                g[i] = gprev[i] * gelu_grad(z[l - 1][i]);
+        }
+        free(qg);
+    }
+    /* one SGD step per parameter, W_l then b_l (sgd.c:111-162) */
+    for (size_t l = 1; l <= L; l++) {
+        size_t K = dims[l - 1], N = dims[l];
+        orc_sgd_step(W[l - 1], dW[l - 1], Wbuf[l - 1], K * N, lr, momentum,
+                     dampening, weight_decay, nesterov);
+        orc_sgd_step(b[l - 1], db[l - 1], bbuf[l - 1], N, lr, momentum,
+                     dampening, weight_decay, nesterov);
+    }
+    for (size_t l = 1; l <= L; l++) {
+        free(z[l]);
+        free(h[l]);
+    }
+    free(z);
+    free(h);
+    free(qw);
+    free(qh);
+    free(g);
+    free(gprev);
+}

@@ -20,6 +20,10 @@
  *   orc_chain1_backward               golden C1 grads (JIT on and off)
  *   orc_chain2_backward               golden C2 grads at a reduced shape
  *   orc_mse_grad_scale                golden mse/mean_all graphs
+ *   orc_mlp_step                      golden two-step f32 MLP training run
+ *                                     of the reference (ORC_F32); the 16-bit
+ *                                     modes differ only by orc_round_f32 on
+ *                                     the GEMM operands, pinned above
  * No function here is "parity unpinned".
  */
 #ifndef PG_ORACLE_H
@@ -92,6 +96,30 @@ void orc_chain2_backward(const float *x, const float *bias, const float *g,
 /* Forward values used by the chains (activations.c:113-173). */
 float orc_gelu(float x);
 float orc_sigmoid(float x);
+
+/*
+ * Config-5 training step of an L-layer MLP, in place.  dims[0..L] are the
+ * layer widths, W[l] [dims[l], dims[l+1]] and b[l] [dims[l+1]] the f32
+ * master parameters, Wbuf/bbuf their momentum buffers (zeros before the
+ * first step), x [batch, dims[0]], target [batch, dims[L]].
+ *   forward   z_l = q(h_{l-1}).q(W_l) + b_l, h_l = gelu(z_l), out = z_L
+ *             (nn.c:117-125 linear, activations.c:166-173 gelu)
+ *   loss      mse(out, target, mean) (autograd.c:1758-1771, mean over the
+ *             last axis only)
+ *   backward  bias grads row-ordered sums (autograd.c:364-387); dW =
+ *             q(h)^T.q(g), dh = q(g).q(W)^T (autograd.c:561-706); gelu'
+ *             (autograd.c:794-801); no grad for x
+ *   update    orc_sgd_step per parameter, W_l then b_l (sgd.c:111-162)
+ * q rounds to dtype (RNE), the identity for ORC_F32 -- where this is the
+ * reference's own f32 step, pinned by a golden run of the reference.
+ * dW/db receive the grads; *loss the forward loss before the update.
+ */
+void orc_mlp_step(int dtype, size_t L, const size_t *dims, size_t batch,
+                  const float *x, const float *target, float *const *W,
+                  float *const *b, float *const *Wbuf, float *const *bbuf,
+                  float *const *dW, float *const *db, float lr,
+                  float momentum, float dampening, float weight_decay,
+                  bool nesterov, float *loss, int nthreads);
 
 /*
  * Upstream-grad scale that pg_ag_mse(pred, tgt, mean) hands to d = pred-tgt:

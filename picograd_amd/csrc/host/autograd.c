@@ -98,6 +98,12 @@ static pg_node *attach(pg_tensor *value, size_t np, pg_node **parents, void (*bw
     return n;
 }
 
+pg_node *pga_attach(pg_tensor *value, size_t np, pg_node **parents, void (*bwd)(pg_node *), void *ctx,
+                    pg_ag_op_t op)
+{
+    return attach(value, np, parents, bwd, ctx, op);
+}
+
 pg_node *pg_var_from_data(size_t ndim, const size_t *shape, const float *data, bool rg)
 {
     return node_wrap(pg_tensor_from_data(ndim, shape, data), rg);

@@ -360,3 +360,148 @@ void pg_bgemm(size_t m, size_t n, size_t k, const uint16_t *a, size_t lda, const
 {
     pg_gemm_ex(PG_DTYPE_BF16, m, n, k, a, lda, b, ldb, c, ldc);
 }
+
+/* ---------------------------------------------------------------- matmul16
+ *
+ * Mixed-precision matmul of f32 operands on the MFMA kernel: C = q(A).q(B)
+ * with q = RNE rounding to f16/bf16 and f32 accumulation; backward
+ * dA (+)= q(dC).q(B)^T and dB (+)= q(A)^T.q(dC) into f32 grads.  The
+ * reference has no cast op and its matmul needs one dtype on both sides
+ * (ops/matmul.c:191), so a bf16-weight network over f32 activations has no
+ * reference spelling; this is the linear layer such a network needs.
+ *
+ * q(X) is the 16-bit shadow kept with X's storage (pgt_shadow16): made once
+ * per tensor, shared by forward, dgrad and wgrad, and rewritten by
+ * pg_sgd_step in the pass that updates a parameter -- the bf16 weight
+ * storage of the layer.  Only a dimension that is not a multiple of 8 (the
+ * 16-byte loads) takes a zero-padded copy per call instead.
+ */
+
+typedef struct {
+    int dt;
+} mm16_ctx;
+
+static bool mm16_dims(const pg_tensor *a, const pg_tensor *b, size_t *M, size_t *K, size_t *N)
+{
+    if (a->ndim != 2 || b->ndim != 2 || a->shape[1] != b->shape[0])
+        return false;
+    *M = a->shape[0];
+    *K = a->shape[1];
+    *N = b->shape[1];
+    return true;
+}
+
+/* q(t) as a [rows_pad, cols_pad] matrix whose first rows x cols hold the
+ * rounded elements: the shadow when no padding is needed, else a padded
+ * copy returned in *owned (*bytes long) */
+static const uint16_t *operand16(pg_tensor *t, int dt, size_t rows, size_t cols, size_t rows_pad, size_t cols_pad,
+                                 uint16_t **owned, size_t *bytes)
+{
+    *owned = NULL;
+    *bytes = 0;
+    if (rows == rows_pad && cols == cols_pad)
+        return pgt_shadow16(t, (pg_dtype)dt);
+    *owned = stage16(dt, 0, t->dev, rows, cols, cols, rows_pad, cols_pad, 1, 0, bytes);
+    return *owned;
+}
+
+static void mm16_backward(pg_node *n)
+{
+    pg_node *pa = n->parents[0], *pb = n->parents[1];
+    pg_tensor *a = pa->value, *b = pb->value;
+    const pg_tensor *g = n->grad;
+    const int dt = ((const mm16_ctx *)n->ctx)->dt;
+    size_t M, K, N;
+    if ((!pa->requires_grad && !pb->requires_grad) || !mm16_dims(a, b, &M, &K, &N) || !M || !N || !K)
+        return;
+    size_t K8 = up8(K), N8 = up8(N);
+    size_t gbytes;
+    uint16_t *g16 = stage16(dt, 0, g->dev, M, N, N, M, N8, 1, 0, &gbytes);
+    if (!g16)
+        return;
+    if (pa->requires_grad) {
+        int beta;
+        pg_tensor *ga = pga_grad_for_write(pa, &beta);
+        uint16_t *own;
+        size_t ob;
+        const uint16_t *qb = operand16(b, dt, K, N, K, N8, &own, &ob);
+        if (ga && qb)
+            gemm16(dt, 0, 0, M, K, N8, g16, N8, 0, M, qb, N8, 0, K, ga->dev, K, 0, 1, beta, "matmul16 dgrad");
+        if (own)
+            pgd_free(own, ob);
+    }
+    if (pb->requires_grad) {
+        int beta;
+        pg_tensor *gb = pga_grad_for_write(pb, &beta);
+        uint16_t *own;
+        size_t ob;
+        const uint16_t *qa = operand16(a, dt, M, K, M, K8, &own, &ob);
+        if (gb && qa)
+            gemm16(dt, 1, 1, K, N, M, qa, K8, 0, K8, g16, N8, 0, N8, gb->dev, N, 0, 1, beta, "matmul16 wgrad");
+        if (own)
+            pgd_free(own, ob);
+    }
+    pgd_free(g16, gbytes);
+}
+
+pg_node *pg_amd_ag_matmul16(pg_node *a, pg_node *b, pg_dtype dtype)
+{
+    if (!a || !b || !a->value || !b->value) {
+        pga_set_err("matmul16: null operand");
+        return NULL;
+    }
+    pg_tensor *av = a->value, *bv = b->value;
+    size_t M, K, N;
+    if (dtype != PG_DTYPE_F16 && dtype != PG_DTYPE_BF16) {
+        pga_set_err("matmul16: dtype must be PG_DTYPE_F16 or PG_DTYPE_BF16");
+        return NULL;
+    }
+    if (av->dtype != PG_DTYPE_F32 || bv->dtype != PG_DTYPE_F32 || !pgt_is_contiguous(av) ||
+        !pgt_is_contiguous(bv)) {
+        pga_set_err("matmul16: operands must be contiguous f32");
+        return NULL;
+    }
+    if (!mm16_dims(av, bv, &M, &K, &N)) {
+        pga_set_err("matmul16: needs A [M, K] and B [K, N]");
+        return NULL;
+    }
+    if (!pgd_ok()) {
+        pga_set_err("matmul16: no device");
+        return NULL;
+    }
+    pgt_materialize(av);
+    pgt_materialize(bv);
+    pg_tensor *c = pgt_alloc(PG_DTYPE_F32, 2, (size_t[]){M, N});
+    if (!c)
+        return NULL;
+    const int dt = (int)dtype;
+    bool ok = true;
+    if (!K) {
+        ok = pgd_check(pgk_fill_f32(c->dev, M * N, 0.0f, pgd_stream()), "matmul16");
+    } else if (M && N) {
+        /* K padded to 8 needs zero columns of q(A) and zero rows of q(B);
+         * N padded to 8 (B's contiguous dim) zero columns of q(B) */
+        size_t K8 = up8(K), N8 = up8(N);
+        uint16_t *oa = NULL, *ob = NULL;
+        size_t oab = 0, obb = 0;
+        const uint16_t *qa = operand16(av, dt, M, K, M, K8, &oa, &oab);
+        const uint16_t *qb = qa ? operand16(bv, dt, K, N, K8, N8, &ob, &obb) : NULL;
+        ok = qa && qb && gemm16(dt, 0, 1, M, N, K8, qa, K8, 0, M, qb, N8, 0, N8, c->dev, N, 0, 1, 0, "matmul16");
+        if (oa)
+            pgd_free(oa, oab);
+        if (ob)
+            pgd_free(ob, obb);
+    }
+    if (!ok) {
+        pga_set_err("matmul16: %s", pg_amd_last_error());
+        pg_tensor_free(c);
+        return NULL;
+    }
+    mm16_ctx *cx = malloc(sizeof *cx);
+    if (!cx) {
+        pg_tensor_free(c);
+        return NULL;
+    }
+    cx->dt = dt;
+    return pga_attach(c, 2, (pg_node *[]){a, b}, mm16_backward, cx, PG_AG_OP_MATMUL);
+}

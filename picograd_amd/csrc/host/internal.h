@@ -46,6 +46,13 @@ void pgt_set_contig_strides(pg_tensor *t);
 bool pgt_is_contiguous(const pg_tensor *t);
 /* materialise a pending zero (grad tensors) */
 void pgt_materialize(pg_tensor *t);
+/* 16-bit (RNE) copy of an f32 tensor's elements, kept with its storage:
+ * made on first use, remade after an in-place write marked it stale
+ * (pgt_touch), rewritten by pg_sgd_step in the pass that updates the
+ * elements.  NULL (device error set) on failure. */
+const uint16_t *pgt_shadow16(pg_tensor *t, pg_dtype dt);
+/* records an in-place write of t's elements: its shadow is stale */
+void pgt_touch(pg_tensor *t);
 
 /* ---- RNG (tensor.c) ---- */
 void pg_rng_uniform_host(float *out, size_t n, float low, float high);
@@ -58,6 +65,11 @@ bool pga_op_fusible(pg_ag_op_t op);
  * the writer must overwrite (grad fresh or logically zero), 1 to add */
 pg_tensor *pga_grad_for_write(pg_node *n, int *beta);
 void pga_backward_node(pg_node *n); /* eager device backward of one node */
+/* a new op node over `parents` (retained); takes ownership of value and of
+ * ctx (freed with free()); without grad mode or a grad-requiring parent the
+ * node is a plain constant and ctx is freed at once */
+pg_node *pga_attach(pg_tensor *value, size_t np, pg_node **parents, void (*bwd)(pg_node *), void *ctx,
+                    pg_ag_op_t op);
 
 typedef struct { size_t axis; bool keepdim; } pga_red_ctx;
 typedef struct { float p0, p1; } pga_param_ctx;

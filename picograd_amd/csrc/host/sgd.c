@@ -119,7 +119,16 @@ void pg_sgd_step(pg_sgd *opt)
         segs[ns].p = p->value->dev;
         segs[ns].g = g->dev;
         segs[ns].buf = c.momentum != 0.0f ? opt->st[i].buf->dev : NULL;
-        segs[ns].shadow = NULL;
+        /* a 16-bit shadow of the parameter (kept for the MFMA GEMMs) is
+         * rewritten from the updated values in the same pass */
+        pg_data_ref *r = p->value->data_ref;
+        bool shadow = r && r->shadow && p->value->dev == r->ptr && p->value->numel * 4 == r->nbytes;
+        segs[ns].shadow = shadow ? r->shadow : NULL;
+        segs[ns].shadow_dtype = shadow ? r->shadow_dtype : 0;
+        if (shadow)
+            r->shadow_stale = false;
+        else
+            pgt_touch(p->value);
         segs[ns].n = p->value->numel;
         ns++;
     }

@@ -84,8 +84,11 @@ void pg_tensor_free(pg_tensor *t)
     if (!t)
         return;
     if (t->data_ref && --t->data_ref->refs == 0) {
-        pgd_free(t->data_ref->ptr, t->data_ref->nbytes);
-        free(t->data_ref);
+        pg_data_ref *r = t->data_ref;
+        pgd_free(r->ptr, r->nbytes);
+        if (r->shadow)
+            pgd_free(r->shadow, r->nbytes / 2);
+        free(r);
     }
     free(t->data_raw);
     free(t);
@@ -247,6 +250,35 @@ pg_tensor *pg_tensor_normal(size_t ndim, const size_t *shape, float mean, float 
     return from_host_gen(ndim, shape, 1, mean, stddev);
 }
 
+void pgt_touch(pg_tensor *t)
+{
+    if (t && t->data_ref)
+        t->data_ref->shadow_stale = true;
+}
+
+const uint16_t *pgt_shadow16(pg_tensor *t, pg_dtype dt)
+{
+    if (!t || !t->data_ref || t->dtype != PG_DTYPE_F32 || (dt != PG_DTYPE_F16 && dt != PG_DTYPE_BF16)) {
+        pgd_set_err("shadow16: needs an f32 tensor and a 16-bit dtype");
+        return NULL;
+    }
+    pg_data_ref *r = t->data_ref;
+    size_t n = r->nbytes / 4;
+    if (r->shadow && r->shadow_dtype == (int)dt && !r->shadow_stale)
+        return r->shadow;
+    if (!r->shadow) {
+        r->shadow = pgd_malloc(n ? n * 2 : 1);
+        if (!r->shadow)
+            return NULL;
+    }
+    r->shadow_dtype = (int)dt;
+    pgt_materialize(t);
+    if (!pgd_check(pgk_cast_to16((int)dt, r->ptr, r->shadow, n, pgd_stream()), "shadow16"))
+        return NULL;
+    r->shadow_stale = false;
+    return r->shadow;
+}
+
 pg_tensor *pg_tensor_clone(const pg_tensor *t)
 {
     if (!t)
@@ -272,6 +304,7 @@ void pg_tensor_fill(pg_tensor *t, float value)
     if (!t)
         return;
     t->pg_flags &= ~PG_TENSOR_ZERO_PENDING;
+    pgt_touch(t);
     fill_value(t, value);
 }
 
@@ -284,6 +317,7 @@ void pg_tensor_copy_from(pg_tensor *dst, const pg_tensor *src)
         return;
     }
     dst->pg_flags &= ~PG_TENSOR_ZERO_PENDING;
+    pgt_touch(dst);
     pgd_d2d(dst->dev, src->dev, src->numel * src->elem_size);
 }
 
@@ -348,6 +382,7 @@ bool pg_tensor_copy_from_host(pg_tensor *t, const void *src)
     if (!t || !src)
         return false;
     t->pg_flags &= ~PG_TENSOR_ZERO_PENDING;
+    pgt_touch(t);
     return pgd_h2d(t->dev, src, t->numel * t->elem_size);
 }
 

@@ -398,7 +398,8 @@ __global__ void __launch_bounds__(kBlock) k_sgd(sgd_table tab, float lr, float m
     size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     size_t stride = (size_t)gridDim.x * blockDim.x;
     bool has_buf = sg.buf != nullptr;
-    bool aligned = ((((uintptr_t)sg.p) | ((uintptr_t)sg.g) | ((uintptr_t)sg.buf)) & 15) == 0;
+    bool aligned = ((((uintptr_t)sg.p) | ((uintptr_t)sg.g) | ((uintptr_t)sg.buf)) & 15) == 0 &&
+                   (((uintptr_t)sg.shadow) & 7) == 0;
     size_t n4 = aligned ? n / 4 : 0;
     for (size_t j = i; j < n4; j += stride) {
         float4 p = reinterpret_cast<float4 *>(sg.p)[j];
@@ -413,10 +414,10 @@ __global__ void __launch_bounds__(kBlock) k_sgd(sgd_table tab, float lr, float m
             reinterpret_cast<float4 *>(sg.buf)[j] = b;
         if (sg.shadow) {
             ushort4 o;
-            o.x = f32_to_bf16(p.x);
-            o.y = f32_to_bf16(p.y);
-            o.z = f32_to_bf16(p.z);
-            o.w = f32_to_bf16(p.w);
+            o.x = to16(sg.shadow_dtype, p.x);
+            o.y = to16(sg.shadow_dtype, p.y);
+            o.z = to16(sg.shadow_dtype, p.z);
+            o.w = to16(sg.shadow_dtype, p.w);
             reinterpret_cast<ushort4 *>(sg.shadow)[j] = o;
         }
     }
@@ -427,7 +428,7 @@ __global__ void __launch_bounds__(kBlock) k_sgd(sgd_table tab, float lr, float m
         if (has_buf)
             sg.buf[j] = b;
         if (sg.shadow)
-            sg.shadow[j] = f32_to_bf16(p);
+            sg.shadow[j] = to16(sg.shadow_dtype, p);
     }
 }
 

@@ -107,7 +107,8 @@ typedef struct {
     float *p;
     const float *g;
     float *buf;       /* NULL when momentum == 0 */
-    uint16_t *shadow; /* optional bf16 copy of p written after the update */
+    uint16_t *shadow; /* optional 16-bit copy of p written after the update */
+    int shadow_dtype; /* 1 = f16, 2 = bf16 (RNE) */
     size_t n;
 } pgk_sgd_seg;
 int pgk_sgd_multi(const pgk_sgd_seg *segs, int nseg, float lr, float momentum, float dampening,

@@ -9,7 +9,7 @@ outputs as small .npz files (no pickles).  The committed fixtures are data
 only; the tests compare the oracle (oracle/liboracle.so) and, on the GPU,
 the MI355X library against them.
 
-    python tests/golden/make_golden.py      # needs oracle/_ref built
+    python tests/golden/make_golden.py [case ...]   # needs oracle/_ref built
 
 Every case names the reference code it exercises.
 """
@@ -297,19 +297,80 @@ def mse(R: PgLib) -> dict:
     return out
 
 
-def main() -> int:
+MLP_DIMS = (48, 64, 64, 64, 10)
+MLP_BATCH = 32
+MLP_SGD = (0.01, 0.9, 0.0, 1e-4, True)
+
+
+def mlp(R: PgLib) -> dict:
+    """Config 5 in f32 at a reduced shape: two training steps of
+    linear(nn.c:117-125: matmul then broadcast bias add) + gelu layers, mse
+    (mean) loss, pg_backward (JIT on) and a Nesterov pg_sgd_step
+    (opt/sgd.c:111-162) with the config-5 hyper-parameters."""
+    rng = np.random.default_rng(5)
+    dims, B = MLP_DIMS, MLP_BATCH
+    out = {"dims": np.array(dims, np.int64)}
+    x = rng.standard_normal((B, dims[0])).astype(np.float32)
+    t = rng.standard_normal((B, dims[-1])).astype(np.float32)
+    out.update(x=x, t=t)
+    Ws, bs = [], []
+    for i in range(len(dims) - 1):
+        lim = 1.0 / np.sqrt(dims[i])
+        Ws.append(rng.uniform(-lim, lim, (dims[i], dims[i + 1])).astype(np.float32))
+        bs.append((0.1 * rng.standard_normal(dims[i + 1])).astype(np.float32))
+        out[f"W{i}_0"], out[f"b{i}_0"] = Ws[-1], bs[-1]
+    nW = [R.var(w) for w in Ws]
+    nb = [R.var(b) for b in bs]
+    opt = R.pg_sgd_new(C.byref(SgdCfg(*MLP_SGD)))
+    for w, b in zip(nW, nb):
+        R.pg_sgd_add_param(opt, w)
+        R.pg_sgd_add_param(opt, b)
+    nx, nt = R.var(x, requires_grad=False), R.var(t, requires_grad=False)
+    for step in (1, 2):
+        R.pg_sgd_zero_grad(opt)
+        h, made = nx, []
+        for i in range(len(Ws)):
+            mm = R.op("matmul", h, nW[i])
+            z = R.op("add", mm, nb[i])
+            made += [mm, z]
+            if i + 1 < len(Ws):
+                h = R.op("gelu", z)
+                made.append(h)
+            else:
+                h = z
+        loss = R.pg_ag_mse(h, nt, True)
+        R.pg_backward(loss)
+        out[f"loss_{step}"] = R.value(loss)
+        for i in range(len(Ws)):
+            out[f"dW{i}_{step}"], out[f"db{i}_{step}"] = R.grad(nW[i]), R.grad(nb[i])
+        R.pg_sgd_step(opt)
+        for i in range(len(Ws)):
+            out[f"W{i}_{step}"], out[f"b{i}_{step}"] = R.value(nW[i]), R.value(nb[i])
+        _free(R, loss, *reversed(made))
+    R.pg_sgd_free(opt)
+    _free(R, nx, nt, *nW, *nb)
+    return out
+
+
+CASES = {
+    "rng": rng_streams,
+    "convert": lambda R: conversions(),
+    "sgd": sgd_trajectories,
+    "chain1": chain1,
+    "chain2": chain2,
+    "gemm": gemms,
+    "matmul_bwd": matmul_backward,
+    "mse": mse,
+    "mlp": mlp,
+}
+
+
+def main(argv: list[str]) -> int:
+    """Writes every case, or only the ones named on the command line."""
     R = ref_lib()
-    cases = {
-        "rng": rng_streams(R),
-        "convert": conversions(),
-        "sgd": sgd_trajectories(R),
-        "chain1": chain1(R),
-        "chain2": chain2(R),
-        "gemm": gemms(R),
-        "matmul_bwd": matmul_backward(R),
-        "mse": mse(R),
-    }
-    for name, arrays in cases.items():
+    names = argv or list(CASES)
+    for name in names:
+        arrays = CASES[name](R)
         path = HERE / f"{name}.npz"
         np.savez_compressed(path, **arrays)
         print(f"wrote {path.relative_to(ROOT)} ({path.stat().st_size} bytes)")
@@ -317,4 +378,4 @@ def main() -> int:
 
 
 if __name__ == "__main__":
-    sys.exit(main())
+    sys.exit(main(sys.argv[1:]))

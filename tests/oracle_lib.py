@@ -41,6 +41,9 @@ class Oracle:
             "orc_gelu": (_fl, [_fl]),
             "orc_sigmoid": (_fl, [_fl]),
             "orc_mse_grad_scale": (_fl, [_sz, C.POINTER(_sz), C.c_bool]),
+            "orc_mlp_step": (None, [_ip, _sz, C.POINTER(_sz), _sz, _vp, _vp, C.POINTER(_vp), C.POINTER(_vp),
+                                    C.POINTER(_vp), C.POINTER(_vp), C.POINTER(_vp), C.POINTER(_vp), _fl, _fl,
+                                    _fl, _fl, C.c_bool, C.POINTER(_fl), _ip]),
         }
         for name, (res, args) in protos.items():
             fn = getattr(L, name)
@@ -100,6 +103,24 @@ class Oracle:
         self.orc_chain2_backward(x.ctypes.data, bias.ctypes.data, g.ctypes.data, R, Cc,
                                  dx.ctypes.data, dg.ctypes.data, db.ctypes.data, db64.ctypes.data)
         return dx, dg, db, db64
+
+    def mlp_step(self, dtype: int, x, target, Ws, bs, Wbufs, bbufs, lr, mu, damp, wd, nesterov,
+                 threads: int = 8):
+        """One orc_mlp_step: updates Ws, bs, Wbufs, bbufs in place (f32 contiguous
+        arrays); returns (loss, dWs, dbs)."""
+        L = len(Ws)
+        dims = [Ws[0].shape[0]] + [w.shape[1] for w in Ws]
+        dWs = [np.empty_like(w) for w in Ws]
+        dbs = [np.empty_like(b) for b in bs]
+        arrs = [Ws, bs, Wbufs, bbufs, dWs, dbs]
+        for group in arrs:
+            for a in group:
+                assert a.dtype == np.float32 and a.flags.c_contiguous
+        ptrs = [(C.c_void_p * L)(*[a.ctypes.data for a in group]) for group in arrs]
+        loss = C.c_float()
+        self.orc_mlp_step(dtype, L, (C.c_size_t * (L + 1))(*dims), x.shape[0], x.ctypes.data,
+                          target.ctypes.data, *ptrs, lr, mu, damp, wd, nesterov, C.byref(loss), threads)
+        return loss.value, dWs, dbs
 
 
 def bf16_to_f32(h: np.ndarray) -> np.ndarray:

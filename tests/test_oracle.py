@@ -294,3 +294,70 @@ def test_mse_scale_matches_reference(oracle):
     assert np.allclose(s_sum * d, g["dpred_sum"], rtol=1e-6, atol=0)
     assert np.allclose(g["loss_mean"], (d.astype(np.float64) ** 2).sum() / 10, rtol=1e-5)
     assert not np.allclose(2.0 / 60 * d, g["dpred_mean"], rtol=1e-3)
+
+
+# ---------------------------------------------------------------- MLP step
+
+def _mlp_run(oracle, g, dtype, steps=2, nesterov=True):
+    L = len(g["dims"]) - 1
+    Ws = [g[f"W{i}_0"].copy() for i in range(L)]
+    bs = [g[f"b{i}_0"].copy() for i in range(L)]
+    Wb = [np.zeros_like(w) for w in Ws]
+    bb = [np.zeros_like(b) for b in bs]
+    hist = []
+    for _ in range(steps):
+        loss, dW, db = oracle.mlp_step(dtype, g["x"], g["t"], Ws, bs, Wb, bb, 0.01, 0.9, 0.0, 1e-4, nesterov)
+        hist.append((loss, dW, db, [w.copy() for w in Ws], [b.copy() for b in bs]))
+    return hist
+
+
+def _mlp_errors(g, hist):
+    """(loss rel, worst grad rel-Frobenius, worst updated-param max rel)"""
+    L = len(g["dims"]) - 1
+    el, eg, ep = 0.0, 0.0, 0.0
+    for s, (loss, dW, db, Ws, bs) in enumerate(hist, start=1):
+        ref = float(g[f"loss_{s}"][0])
+        el = max(el, abs(loss - ref) / abs(ref))
+        for i in range(L):
+            eg = max(eg, rel_fro(dW[i], g[f"dW{i}_{s}"]), rel_fro(db[i], g[f"db{i}_{s}"]))
+            for got, key in ((Ws[i], f"W{i}_{s}"), (bs[i], f"b{i}_{s}")):
+                want = g[key].astype(np.float64)
+                ep = max(ep, float(np.abs(got - want).max() / np.abs(want).max()))
+    return el, eg, ep
+
+
+def test_mlp_step_matches_reference(oracle):
+    """orc_mlp_step in f32 reproduces two training steps of the reference's
+    own MLP (linear + gelu layers, mse, pg_backward, Nesterov pg_sgd_step):
+    loss, every weight and bias grad, and the updated parameters.  The
+    remaining differences come from the GEMM summation order (the reference
+    blocks k by 256 with AVX-512 partial sums, the oracle sums in k order)."""
+    g = golden("mlp")
+    el, eg, ep = _mlp_errors(g, _mlp_run(oracle, g, 0))
+    assert el < 1e-6, el
+    assert eg < 2e-6, eg
+    assert ep < 1e-6, ep
+
+
+def test_mlp_step_planted_mistakes_are_caught(oracle):
+    """The same comparison rejects plausible mistakes: GEMM operands rounded
+    where the reference keeps f32, and the update without Nesterov."""
+    g = golden("mlp")
+    _, eg, _ = _mlp_errors(g, _mlp_run(oracle, g, BF16, steps=1))
+    assert eg > 1e-3, eg
+    _, _, ep = _mlp_errors(g, _mlp_run(oracle, g, 0, steps=1, nesterov=False))
+    assert ep > 1e-5, ep
+
+
+def test_mlp_step_bf16_close_to_f32(oracle):
+    """The 16-bit mode differs from the f32 step by operand rounding only:
+    grads stay within a few bf16 ulps (rel Frobenius < 2e-2) of the f32 run,
+    and the f16 mode, with 3 more mantissa bits, lands 8x closer."""
+    g = golden("mlp")
+    ref = _mlp_run(oracle, g, 0, steps=1)[0]
+    errs = {}
+    for dt in (F16, BF16):
+        run = _mlp_run(oracle, g, dt, steps=1)[0]
+        errs[dt] = max(rel_fro(a, b) for a, b in zip(run[1] + run[2], ref[1] + ref[2]))
+    assert errs[BF16] < 2e-2, errs
+    assert errs[F16] < errs[BF16] / 4, errs
