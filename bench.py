@@ -360,17 +360,18 @@ def c5_counts(dims=C5_DIMS, batch=C5_BATCH):
     return fwd, bwd, params, 20 * params + 2 * shadow
 
 
-def bench_c5(L, ev, steps, warmup, dims=C5_DIMS, batch=C5_BATCH):
-    """Config 5: forward + pg_backward + pg_sgd_step of the bf16-GEMM MLP."""
+def bench_c5(L, ev, steps, warmup, dims=C5_DIMS, batch=C5_BATCH, fused=True):
+    """Config 5: forward + pg_backward + pg_sgd_step of the bf16-GEMM MLP,
+    layers as pg_amd_ag_linear16 nodes (fused) or matmul16 + add + gelu."""
     from picograd_amd.capi import BF16, shape_arg
     from picograd_amd.mlp import Mlp
-    log(f"[c5] MLP {dims}, batch {batch}, bf16 GEMM operands, f32 masters")
+    log(f"[c5] MLP {dims}, batch {batch}, bf16 GEMM operands, f32 masters, fused={fused}")
     L.pg_seed(46)
     nd, sh = shape_arg((batch, dims[0]))
     x = L._check(L.pg_var_normal(nd, sh, 0.0, 1.0, False))
     nd, sh = shape_arg((batch, dims[-1]))
     t = L._check(L.pg_var_normal(nd, sh, 0.0, 1.0, False))
-    mlp = Mlp.seeded(L, dims, BF16)
+    mlp = Mlp.seeded(L, dims, BF16, fused=fused)
     loss0 = mlp.step(x, t, keep_loss=True)
     first = float(L.value(loss0)[0])
     L.pg_node_free(loss0)
@@ -385,6 +386,7 @@ def bench_c5(L, ev, steps, warmup, dims=C5_DIMS, batch=C5_BATCH):
     s_ms, s_n = timer_ms(L, T_SGD)
     j_ms, j_n = timer_ms(L, T_JIT_MAIN)
     f_ms, f_n = timer_ms(L, T_JIT_FIN)
+    a_ms, a_n = timer_ms(L, T_STAGE)
     L.pg_amd_timer_reset()
     ms = ev.time(lambda: mlp.step(x, t), steps)
     lossN = mlp.step(x, t, keep_loss=True)
@@ -404,6 +406,7 @@ def bench_c5(L, ev, steps, warmup, dims=C5_DIMS, batch=C5_BATCH):
             "gemm_launches_per_step": g_n / steps,
             "sgd_ms": sgd_ms, "sgd_gbs": sgd_bytes / (sgd_ms * 1e-3) / 1e9, "sgd_bytes": sgd_bytes,
             "params": params, "fused_bwd_ms_per_step": (j_ms + f_ms) / steps,
+            "act_bwd_ms_per_step": a_ms / steps,
             "loss_first": first, "loss_last": last, "steps_run": 1 + max(0, warmup - 1) + 2 * steps + 1}
 
 
@@ -513,7 +516,9 @@ def main(argv=None):
         extra["c1_chain_64x64"] = bench_c1(L)
         log(f"[c1] {extra['c1_chain_64x64']}")
     if "c5" in only:
-        extra["c5_mlp_train_step"] = bench_c5(L, ev, max(3, a.steps // 2), a.warmup)
+        c5 = bench_c5(L, ev, max(3, a.steps // 2), a.warmup, fused=True)
+        c5["unfused_graph"] = bench_c5(L, ev, max(3, a.steps // 2), a.warmup, fused=False)
+        extra["c5_mlp_train_step"] = c5
         log(f"[c5] {extra['c5_mlp_train_step']}")
     cpu = None
     if not a.no_cpu:

@@ -51,6 +51,28 @@ void pg_amd_backward_from(pg_node *root, const pg_tensor *seed);
  * (ops/matmul.c:191) and has no cast op, so it has no counterpart. */
 pg_node *pg_amd_ag_matmul16(pg_node *a, pg_node *b, pg_dtype dtype);
 
+/* Activation codes of pg_amd_ag_linear16: the reference's PG_ACT_* values
+ * (backend/cpu/gemm.h:37-39). */
+#ifndef PG_ACT_NONE
+#define PG_ACT_NONE 0
+#define PG_ACT_RELU 1
+#define PG_ACT_GELU 2
+#endif
+
+/* Linear layer out = act(q(x).q(W) + b) with x [M, K], W [K, N], b [N]
+ * (or NULL), all f32 nodes, q and the f32 accumulation as in
+ * pg_amd_ag_matmul16, act one of PG_ACT_*.  One MFMA GEMM computes it: its
+ * epilogue adds the bias, applies the activation, keeps the pre-activation
+ * for the backward and writes out's 16-bit copy for the next layer.
+ * Backward: dz = dout * act'(pre-activation) (GELU' and ReLU' as
+ * pg_ag_gelu / pg_ag_relu), db += column sums of dz, dx += q(dz).q(W)^T,
+ * dW += q(x)^T.q(dz) -- the grads of matmul16 + add + act, in fewer passes.
+ * The reference computes this forward in pg_cpu_gemm_fused
+ * (backend/cpu/gemm.c:685-726, the fused path of nn.c:46-90) without an
+ * autograd form; it has no counterpart in the autograd ABI.
+ * Returns NULL (pg_autograd_last_error) for bad shapes, dtype or act. */
+pg_node *pg_amd_ag_linear16(pg_node *x, pg_node *w, pg_node *b, int act, pg_dtype dtype);
+
 /* JIT compile statistics: programs compiled by hiprtc, and cache lookups
  * that found a loaded kernel. */
 size_t pg_amd_jit_compiles(void);

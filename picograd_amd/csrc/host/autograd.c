@@ -161,7 +161,10 @@ void pg_node_free(pg_node *n)
             continue;
         pg_tensor_free(t->value);
         pg_tensor_free(t->grad);
-        free(t->ctx);
+        if (t->backward == pgm_linear16_backward)
+            pgm_linear16_free_ctx(t->ctx);
+        else
+            free(t->ctx);
         if (sp + t->nparents > cap) {
             while (sp + t->nparents > cap)
                 cap *= 2;
@@ -539,7 +542,11 @@ static pg_node *ag_reduce(pg_node *a, size_t axis, bool keepdim, bool mean)
     if (!v)
         return NULL;
     float scale = mean ? 1.0f / (float)len : 1.0f;
-    if (!pgd_check(pgk_sum_axis_f32((const float *)t->dev, (float *)v->dev, outer, len, inner, scale, pgd_stream()),
+    size_t wsz = pgk_sum_axis_workspace(outer, len, inner);
+    void *ws = wsz ? pgd_scratch(2, wsz) : NULL;
+    if ((wsz && !ws) ||
+        !pgd_check(pgk_sum_axis_f32((const float *)t->dev, (float *)v->dev, outer, len, inner, scale, ws,
+                                    pgd_stream()),
                    "reduce")) {
         pg_tensor_free(v);
         return NULL;

@@ -84,12 +84,12 @@ static bool mm_shapes(const pg_tensor *a, const pg_tensor *b, mm_shape *s, size_
 
 static void *tmp_alloc(size_t nbytes) { return pgd_malloc(nbytes ? nbytes : 1); }
 
-/* one MFMA GEMM (pgk_gemm16 semantics), bracketed by the kernel timer; the
- * k-tail workspace comes from the library scratch (stream-ordered, so
- * consecutive GEMMs may share it) */
-static bool gemm16(int dt, int ta, int tb, size_t m, size_t n, size_t k, const uint16_t *a, size_t lda, size_t sa,
-                   size_t aext, const uint16_t *b, size_t ldb, size_t sb, size_t bext, float *c, size_t ldc,
-                   size_t sc, size_t batch, int beta, const char *what)
+/* one MFMA GEMM (pgk_gemm16 semantics, optional epilogue), bracketed by the
+ * kernel timer; the split-K partials and k-tail slabs come from the library
+ * scratch (stream-ordered, so consecutive GEMMs may share it) */
+static bool gemm16x(int dt, int ta, int tb, size_t m, size_t n, size_t k, const uint16_t *a, size_t lda, size_t sa,
+                    size_t aext, const uint16_t *b, size_t ldb, size_t sb, size_t bext, float *c, size_t ldc,
+                    size_t sc, size_t batch, int beta, const pgk_epi *epi, const char *what)
 {
     size_t wsz = pgk_gemm16_workspace(ta, tb, m, n, k, batch);
     void *ws = NULL;
@@ -98,10 +98,17 @@ static bool gemm16(int dt, int ta, int tb, size_t m, size_t n, size_t k, const u
         return false;
     }
     int tk = pgd_tbegin(PGD_T_GEMM16);
-    int rc = pgk_gemm16(dt, ta, tb, m, n, k, a, lda, sa, aext, b, ldb, sb, bext, c, ldc, sc, batch, beta, ws,
+    int rc = pgk_gemm16(dt, ta, tb, m, n, k, a, lda, sa, aext, b, ldb, sb, bext, c, ldc, sc, batch, beta, epi, ws,
                         pgd_stream());
     pgd_tend(tk);
     return pgd_check(rc, what);
+}
+
+static bool gemm16(int dt, int ta, int tb, size_t m, size_t n, size_t k, const uint16_t *a, size_t lda, size_t sa,
+                   size_t aext, const uint16_t *b, size_t ldb, size_t sb, size_t bext, float *c, size_t ldc,
+                   size_t sc, size_t batch, int beta, const char *what)
+{
+    return gemm16x(dt, ta, tb, m, n, k, a, lda, sa, aext, b, ldb, sb, bext, c, ldc, sc, batch, beta, NULL, what);
 }
 
 /* 16-bit copy of `rows x cols` (leading dim lds, `batch` matrices `sstride`
@@ -113,6 +120,15 @@ static uint16_t *stage16(int dt, int src_dtype, const void *src, size_t rows, si
     uint16_t *p = tmp_alloc(*bytes);
     if (!p)
         return NULL;
+    if (src_dtype == 0 && rows == rows_pad && cols == cols_pad && lds == cols &&
+        (batch == 1 || sstride == rows * cols)) {
+        /* no padding: a flat cast (16-byte loads and stores) */
+        if (!pgd_check(pgk_cast_to16(dt, src, p, batch * rows * cols, pgd_stream()), "stage operand")) {
+            pgd_free(p, *bytes);
+            return NULL;
+        }
+        return p;
+    }
     if (!pgd_check(pgk_copy_to16(dt, src_dtype, src, rows, cols, lds, p, cols_pad, rows_pad, batch, sstride,
                                  rows_pad * cols_pad, pgd_stream()),
                    "stage operand")) {
@@ -504,4 +520,173 @@ pg_node *pg_amd_ag_matmul16(pg_node *a, pg_node *b, pg_dtype dtype)
     }
     cx->dt = dt;
     return pga_attach(c, 2, (pg_node *[]){a, b}, mm16_backward, cx, PG_AG_OP_MATMUL);
+}
+
+/* ---------------------------------------------------------------- linear16
+ *
+ * out = act(q(x).q(W) + b) as one MFMA GEMM whose epilogue adds the bias,
+ * applies the activation and writes out, the pre-activation z (kept for the
+ * backward) and out's 16-bit copy (the next layer's GEMM operand): the
+ * forward of the reference's pg_cpu_gemm_fused (backend/cpu/gemm.c:685-726,
+ * bias + act after f32 accumulation; nn.c:46-90 builds its linear layers on
+ * it) with autograd.  Backward: one pass forms dz = dout * act'(z), writes it
+ * RNE-16-bit for the GEMMs and sums its columns into db; then
+ * dx += q(dz).q(W)^T and dW += q(x)^T.q(dz).
+ */
+
+typedef struct {
+    int dt, act;
+    pg_tensor *z; /* pre-activation, NULL for act NONE or when no grad is needed */
+} lin16_ctx;
+
+void pgm_linear16_free_ctx(void *ctx)
+{
+    lin16_ctx *cx = ctx;
+    if (cx)
+        pg_tensor_free(cx->z);
+    free(cx);
+}
+
+void pgm_linear16_backward(pg_node *n)
+{
+    pg_node *px = n->parents[0], *pw = n->parents[1], *pb = n->nparents > 2 ? n->parents[2] : NULL;
+    pg_tensor *x = px->value, *w = pw->value;
+    const lin16_ctx *cx = n->ctx;
+    const int dt = cx->dt;
+    size_t M, K, N;
+    if (!mm16_dims(x, w, &M, &K, &N) || !M || !N)
+        return;
+    const size_t K8 = up8(K), N8 = up8(N);
+    const size_t dzb = M * N8 * 2;
+    uint16_t *dz16 = tmp_alloc(dzb);
+    if (!dz16)
+        return;
+    float *db = NULL;
+    int dbeta = 0;
+    if (pb && pb->requires_grad) {
+        pg_tensor *gb = pga_grad_for_write(pb, &dbeta);
+        db = gb ? gb->dev : NULL;
+    }
+    size_t wsz = db ? pgk_act_bwd16_workspace(M, N) : 0;
+    void *ws = wsz ? pgd_scratch(3, wsz) : NULL;
+    int tk = pgd_tbegin(PGD_T_STAGE);
+    bool ok = (!wsz || ws) &&
+              pgd_check(pgk_act_bwd16(cx->act, n->grad->dev, cx->z ? cx->z->dev : NULL, M, N, dz16, N8, dt, db,
+                                      dbeta, ws, pgd_stream()),
+                        "linear16 act backward");
+    pgd_tend(tk);
+    if (ok && K && px->requires_grad) {
+        int beta;
+        pg_tensor *gx = pga_grad_for_write(px, &beta);
+        uint16_t *own;
+        size_t ob;
+        const uint16_t *qw = operand16(w, dt, K, N, K, N8, &own, &ob);
+        if (gx && qw)
+            gemm16(dt, 0, 0, M, K, N8, dz16, N8, 0, M, qw, N8, 0, K, gx->dev, K, 0, 1, beta, "linear16 dgrad");
+        if (own)
+            pgd_free(own, ob);
+    }
+    if (ok && K && pw->requires_grad) {
+        int beta;
+        pg_tensor *gw = pga_grad_for_write(pw, &beta);
+        uint16_t *own;
+        size_t ob;
+        const uint16_t *qx = operand16(x, dt, M, K, M, K8, &own, &ob);
+        if (gw && qx)
+            gemm16(dt, 1, 1, K, N, M, qx, K8, 0, K8, dz16, N8, 0, N8, gw->dev, N, 0, 1, beta, "linear16 wgrad");
+        if (own)
+            pgd_free(own, ob);
+    }
+    pgd_free(dz16, dzb);
+}
+
+pg_node *pg_amd_ag_linear16(pg_node *x, pg_node *w, pg_node *b, int act, pg_dtype dtype)
+{
+    if (!x || !w || !x->value || !w->value || (b && !b->value)) {
+        pga_set_err("linear16: null operand");
+        return NULL;
+    }
+    if (dtype != PG_DTYPE_F16 && dtype != PG_DTYPE_BF16) {
+        pga_set_err("linear16: dtype must be PG_DTYPE_F16 or PG_DTYPE_BF16");
+        return NULL;
+    }
+    if (act < PGK_ACT_NONE || act > PGK_ACT_GELU) {
+        pga_set_err("linear16: act must be PG_ACT_NONE, PG_ACT_RELU or PG_ACT_GELU (0, 1, 2)");
+        return NULL;
+    }
+    pg_tensor *xv = x->value, *wv = w->value, *bv = b ? b->value : NULL;
+    size_t M, K, N;
+    if (xv->dtype != PG_DTYPE_F32 || wv->dtype != PG_DTYPE_F32 || !pgt_is_contiguous(xv) || !pgt_is_contiguous(wv) ||
+        (bv && (bv->dtype != PG_DTYPE_F32 || !pgt_is_contiguous(bv)))) {
+        pga_set_err("linear16: operands must be contiguous f32");
+        return NULL;
+    }
+    if (!mm16_dims(xv, wv, &M, &K, &N) || (bv && bv->numel != N)) {
+        pga_set_err("linear16: needs x [M, K], W [K, N] and b [N]");
+        return NULL;
+    }
+    if (!pgd_ok()) {
+        pga_set_err("linear16: no device");
+        return NULL;
+    }
+    pgt_materialize(xv);
+    pgt_materialize(wv);
+    if (bv)
+        pgt_materialize(bv);
+    const int dt = (int)dtype;
+    const bool grad = pg_autograd_is_grad_enabled() &&
+                      (x->requires_grad || w->requires_grad || (b && b->requires_grad));
+    pg_tensor *out = pgt_alloc(PG_DTYPE_F32, 2, (size_t[]){M, N});
+    pg_tensor *z = (grad && act != PGK_ACT_NONE) ? pgt_alloc(PG_DTYPE_F32, 2, (size_t[]){M, N}) : NULL;
+    lin16_ctx *cx = malloc(sizeof *cx);
+    bool ok = out && cx && (z || !grad || act == PGK_ACT_NONE);
+    /* out's 16-bit copy, kept as its shadow (rows of N need N % 8 == 0 to be
+     * a GEMM operand in place) */
+    if (ok && N % 8 == 0 && M * N) {
+        pg_data_ref *r = out->data_ref;
+        r->shadow = pgd_malloc(M * N * 2);
+        r->shadow_dtype = dt;
+        r->shadow_stale = true;
+        ok = r->shadow != NULL;
+    }
+    if (ok && M && N) {
+        pgk_epi epi = {bv ? (const float *)bv->dev : NULL, act, z ? (float *)z->dev : NULL,
+                       out->data_ref->shadow, dt};
+        if (!K) {
+            ok = gemm16x(dt, 0, 1, M, N, 0, NULL, 8, 0, M, NULL, 8, 0, up8(N), out->dev, N, 0, 1, 0, &epi,
+                         "linear16");
+        } else {
+            size_t K8 = up8(K), N8 = up8(N);
+            uint16_t *oa = NULL, *ob = NULL;
+            size_t oab = 0, obb = 0;
+            const uint16_t *qx = operand16(xv, dt, M, K, M, K8, &oa, &oab);
+            const uint16_t *qw = qx ? operand16(wv, dt, K, N, K8, N8, &ob, &obb) : NULL;
+            ok = qx && qw &&
+                 gemm16x(dt, 0, 1, M, N, K8, qx, K8, 0, M, qw, N8, 0, N8, out->dev, N, 0, 1, 0, &epi, "linear16");
+            if (oa)
+                pgd_free(oa, oab);
+            if (ob)
+                pgd_free(ob, obb);
+        }
+        if (ok && out->data_ref->shadow)
+            out->data_ref->shadow_stale = false;
+    }
+    if (!ok) {
+        pga_set_err("linear16: %s", pg_amd_last_error());
+        pg_tensor_free(out);
+        pg_tensor_free(z);
+        free(cx);
+        return NULL;
+    }
+    cx->dt = dt;
+    cx->act = act;
+    cx->z = z;
+    pg_node *parents[3] = {x, w, b};
+    pg_node *n = pga_attach(out, b ? 3 : 2, parents, pgm_linear16_backward, NULL, PG_AG_OP_MATMUL);
+    if (n && n->backward) {
+        n->ctx = cx;
+    } else {
+        pgm_linear16_free_ctx(cx);
+    }
+    return n;
 }

@@ -77,6 +77,10 @@ typedef struct { float p0, p1; } pga_param_ctx;
 /* ---- matmul helpers (gemm.c) ---- */
 pg_tensor *pgm_matmul_forward(const pg_tensor *a, const pg_tensor *b);
 void pgm_matmul_backward(pg_node *n);
+/* pg_amd_ag_linear16's backward and the destructor of its node context
+ * (the kept pre-activation), called by pg_node_free */
+void pgm_linear16_backward(pg_node *n);
+void pgm_linear16_free_ctx(void *ctx);
 
 /* ---- JIT internals used by the walker (jit.c) ---- */
 typedef struct pgj_region pgj_region;

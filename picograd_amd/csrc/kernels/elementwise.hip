@@ -7,6 +7,7 @@
 #include <stdint.h>
 
 #include "launch.h"
+#include "convert16.h"
 #include "pgmath.h"
 
 namespace {
@@ -87,92 +88,6 @@ __device__ __forceinline__ float binary_f(int op, float a, float b)
     }
 }
 
-// ---------------------------------------------------------------- casts
-// f32 -> bf16: round to nearest even on the raw bits; a NaN becomes the
-// positive quiet NaN 0x7FC0 | bit 16 (the reference's convert.h rule).
-__device__ __forceinline__ uint16_t f32_to_bf16(float f)
-{
-    uint32_t x = __float_as_uint(f);
-    if ((x & 0x7F800000u) == 0x7F800000u && (x & 0x7FFFFFu) != 0)
-        return (uint16_t)(0x7FC0u | ((x >> 16) & 1u));
-    return (uint16_t)((x + 0x7FFFu + ((x >> 16) & 1u)) >> 16);
-}
-
-// f32 -> f16, IEEE round to nearest even including subnormals; NaN keeps
-// its top payload bits and is quieted.
-__device__ __forceinline__ uint16_t f32_to_f16(float f)
-{
-    uint32_t x = __float_as_uint(f);
-    uint32_t sign = (x >> 16) & 0x8000u;
-    uint32_t ex = (x >> 23) & 0xFFu;
-    uint32_t man = x & 0x7FFFFFu;
-    if (ex == 255) {
-        if (man == 0)
-            return (uint16_t)(sign | 0x7C00u);
-        uint32_t q = sign | 0x7C00u | (man >> 13);
-        if ((q & 0x3FFu) == 0)
-            q |= 1u;
-        return (uint16_t)(q | 0x200u);
-    }
-    int e = (int)ex - 112;
-    if (e >= 31)
-        return (uint16_t)(sign | 0x7C00u);
-    if (e <= 0) {
-        if (e < -10)
-            return (uint16_t)sign;
-        man |= 0x800000u;
-        uint32_t sh = (uint32_t)(1 - e) + 13u;
-        uint32_t keep = man >> sh;
-        uint32_t rem = man & ((1u << sh) - 1u);
-        uint32_t half = 1u << (sh - 1u);
-        if (rem > half || (rem == half && (keep & 1u)))
-            keep++;
-        return (uint16_t)(sign | keep);
-    }
-    uint32_t r = man + 0xFFFu + ((man >> 13) & 1u);
-    if (r & 0x800000u) {
-        r = 0;
-        e++;
-    }
-    if (e >= 31)
-        return (uint16_t)(sign | 0x7C00u);
-    return (uint16_t)(sign | ((uint32_t)e << 10) | (r >> 13));
-}
-
-// f16 -> f32 on the raw bits (exact; NaN payloads kept as they are)
-__device__ __forceinline__ float f16_to_f32(uint16_t h)
-{
-    uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
-    uint32_t ex = ((uint32_t)h >> 10) & 0x1Fu;
-    uint32_t man = (uint32_t)h & 0x3FFu;
-    if (ex == 0) {
-        if (man == 0)
-            return __uint_as_float(sign);
-        int e = 1;
-        while ((man & 0x400u) == 0) {
-            man <<= 1;
-            e--;
-        }
-        man &= 0x3FFu;
-        return __uint_as_float(sign | ((uint32_t)(e + 112) << 23) | (man << 13));
-    }
-    if (ex == 31)
-        return __uint_as_float(sign | 0x7F800000u | (man << 13));
-    return __uint_as_float(sign | ((ex + 112u) << 23) | (man << 13));
-}
-
-__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
-
-__device__ __forceinline__ uint16_t to16(int dtype, float f)
-{
-    return dtype == 1 ? f32_to_f16(f) : f32_to_bf16(f);
-}
-
-__device__ __forceinline__ float from16(int dtype, uint16_t h)
-{
-    return dtype == 1 ? f16_to_f32(h) : bf16_to_f32(h);
-}
-
 // ---------------------------------------------------------------- kernels
 
 __global__ void __launch_bounds__(kBlock) k_fill_f32(float *__restrict__ dst, size_t n, float v)
@@ -200,8 +115,25 @@ __global__ void __launch_bounds__(kBlock) k_unary(int op, const float *__restric
 {
     size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     size_t stride = (size_t)gridDim.x * blockDim.x;
-    for (size_t j = i; j < n; j += stride)
+    const bool vec = ((((uintptr_t)x) | ((uintptr_t)y)) & 15) == 0;
+    size_t n4 = vec ? n / 4 : 0;
+    for (size_t j = i; j < n4; j += stride) {
+        float4 v = reinterpret_cast<const float4 *>(x)[j];
+        v.x = unary_f(op, v.x, p0, p1);
+        v.y = unary_f(op, v.y, p0, p1);
+        v.z = unary_f(op, v.z, p0, p1);
+        v.w = unary_f(op, v.w, p0, p1);
+        reinterpret_cast<float4 *>(y)[j] = v;
+    }
+    for (size_t j = n4 * 4 + i; j < n; j += stride)
         y[j] = unary_f(op, x[j], p0, p1);
+}
+
+__device__ __forceinline__ float unary_bwd_elem(int op, float g, float x, float d, float p0, float p1,
+                                                float scale, int beta)
+{
+    float v = scale * g * unary_grad_f(op, x, p0, p1);
+    return beta ? d + v : v;
 }
 
 __global__ void __launch_bounds__(kBlock) k_unary_bwd(int op, const float *__restrict__ g,
@@ -210,11 +142,20 @@ __global__ void __launch_bounds__(kBlock) k_unary_bwd(int op, const float *__res
 {
     size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     size_t stride = (size_t)gridDim.x * blockDim.x;
-    for (size_t j = i; j < n; j += stride) {
-        float xv = x ? x[j] : 0.0f;
-        float v = scale * g[j] * unary_grad_f(op, xv, p0, p1);
-        dx[j] = beta ? dx[j] + v : v;
+    const bool vec = x && ((((uintptr_t)g) | ((uintptr_t)x) | ((uintptr_t)dx)) & 15) == 0;
+    size_t n4 = vec ? n / 4 : 0;
+    for (size_t j = i; j < n4; j += stride) {
+        const float4 gv = reinterpret_cast<const float4 *>(g)[j];
+        const float4 xv = reinterpret_cast<const float4 *>(x)[j];
+        float4 d = beta ? reinterpret_cast<const float4 *>(dx)[j] : make_float4(0, 0, 0, 0);
+        d.x = unary_bwd_elem(op, gv.x, xv.x, d.x, p0, p1, scale, beta);
+        d.y = unary_bwd_elem(op, gv.y, xv.y, d.y, p0, p1, scale, beta);
+        d.z = unary_bwd_elem(op, gv.z, xv.z, d.z, p0, p1, scale, beta);
+        d.w = unary_bwd_elem(op, gv.w, xv.w, d.w, p0, p1, scale, beta);
+        reinterpret_cast<float4 *>(dx)[j] = d;
     }
+    for (size_t j = n4 * 4 + i; j < n; j += stride)
+        dx[j] = unary_bwd_elem(op, g[j], x ? x[j] : 0.0f, beta ? dx[j] : 0.0f, p0, p1, scale, beta);
 }
 
 __device__ __forceinline__ void unravel2(const pgk_bcast &bc, size_t idx, int64_t &oa, int64_t &ob)
@@ -240,6 +181,52 @@ __global__ void __launch_bounds__(kBlock) k_binary(int op, const float *__restri
         int64_t oa, ob;
         unravel2(bc, j, oa, ob);
         y[j] = binary_f(op, a[oa], b[ob]);
+    }
+}
+
+// Broadcast binary op, 4 outputs per lane along the last dim: the output is
+// rows x C (C = last dim, a multiple of 4); each operand's last-dim stride
+// is 1 (float4 load) or 0 (one value splat); its row offset comes from the
+// leading dims.  The host checks that every row offset of a stride-1
+// operand is a multiple of 4 and the bases are 16-byte aligned.
+__global__ void __launch_bounds__(kBlock) k_binary_rows4(int op, const float *__restrict__ a,
+                                                         const float *__restrict__ b, float *__restrict__ y,
+                                                         size_t rows, size_t c4, pgk_bcast bc)
+{
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    size_t stride = (size_t)gridDim.x * blockDim.x;
+    const int nl = bc.ndim - 1;
+    const bool avec = bc.sa[nl] != 0, bvec = bc.sb[nl] != 0;
+    const size_t n4 = rows * c4;
+    for (size_t j = i; j < n4; j += stride) {
+        size_t r = j / c4, c = (j - r * c4) * 4;
+        int64_t oa = 0, ob = 0;
+        for (int d = nl - 1; d >= 0; --d) {
+            int64_t sd = bc.shape[d];
+            int64_t q = (int64_t)(r % (size_t)sd);
+            r /= (size_t)sd;
+            oa += q * bc.sa[d];
+            ob += q * bc.sb[d];
+        }
+        float4 va, vb;
+        if (avec) {
+            va = *reinterpret_cast<const float4 *>(a + oa + c);
+        } else {
+            const float s0 = a[oa];
+            va = make_float4(s0, s0, s0, s0);
+        }
+        if (bvec) {
+            vb = *reinterpret_cast<const float4 *>(b + ob + c);
+        } else {
+            const float s1 = b[ob];
+            vb = make_float4(s1, s1, s1, s1);
+        }
+        float4 o;
+        o.x = binary_f(op, va.x, vb.x);
+        o.y = binary_f(op, va.y, vb.y);
+        o.z = binary_f(op, va.z, vb.z);
+        o.w = binary_f(op, va.w, vb.w);
+        reinterpret_cast<float4 *>(y)[j] = o;
     }
 }
 
@@ -294,21 +281,58 @@ __global__ void __launch_bounds__(kBlock) k_expand_into(float *dst, const float 
     }
 }
 
-// y[o, i] = scale * sum_l x[o, l, i]; one thread per output, l ascending.
-__global__ void __launch_bounds__(kBlock) k_sum_axis(const float *__restrict__ x, float *__restrict__ y,
-                                                     size_t outer, size_t len, size_t inner, float scale)
+// y[o, i] = scale * sum_l x[o, l, i] in two deterministic stages: the
+// reduced axis is cut into `slices` runs of slice_len; stage 1 writes one
+// partial per (slice, o, i) (consecutive lanes take consecutive i, so rows
+// are read coalesced), stage 2 adds the partials of each output in slice
+// order.  slices == 1 writes y directly.
+__global__ void __launch_bounds__(kBlock) k_sum_axis_part(const float *__restrict__ x, float *__restrict__ part,
+                                                          size_t outer, size_t len, size_t inner, size_t slices,
+                                                          size_t slice_len, float scale)
 {
     size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     size_t stride = (size_t)gridDim.x * blockDim.x;
-    size_t total = outer * inner;
+    const size_t n = outer * inner, total = slices * n;
     for (size_t j = i; j < total; j += stride) {
-        size_t o = j / inner, in = j % inner;
-        const float *p = x + o * len * inner + in;
+        const size_t sl = j / n, oi = j - sl * n;
+        const size_t o = oi / inner, in = oi - o * inner;
+        const size_t l0 = sl * slice_len, l1 = l0 + slice_len < len ? l0 + slice_len : len;
+        const float *p = x + (o * len) * inner + in;
         float acc = 0.0f;
-        for (size_t l = 0; l < len; ++l)
+#pragma unroll 8
+        for (size_t l = l0; l < l1; ++l)
             acc += p[l * inner];
+        part[j] = slices == 1 ? acc * scale : acc;
+    }
+}
+
+__global__ void __launch_bounds__(kBlock) k_sum_axis_fin(const float *__restrict__ part, float *__restrict__ y,
+                                                         size_t n, size_t slices, float scale)
+{
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t j = i; j < n; j += stride) {
+        float acc = 0.0f;
+#pragma unroll 8
+        for (size_t sl = 0; sl < slices; ++sl)
+            acc += part[sl * n + j];
         y[j] = acc * scale;
     }
+}
+
+// slices for a reduction: about 2^18 partial sums, runs of at least 64
+inline void sum_axis_plan(size_t outer, size_t len, size_t inner, size_t *slices, size_t *slice_len)
+{
+    size_t n = outer * inner;
+    size_t want = n ? ((size_t)1 << 18) / n : 1;
+    size_t most = len / 64;
+    size_t sl = want < most ? want : most;
+    if (sl < 1)
+        sl = 1;
+    *slice_len = (len + sl - 1) / sl;
+    *slices = *slice_len ? (len + *slice_len - 1) / *slice_len : 1;
+    if (*slices < 1)
+        *slices = 1;
 }
 
 __global__ void __launch_bounds__(kBlock) k_cast_to16(int dtype, const float *__restrict__ src,
@@ -316,17 +340,19 @@ __global__ void __launch_bounds__(kBlock) k_cast_to16(int dtype, const float *__
 {
     size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     size_t stride = (size_t)gridDim.x * blockDim.x;
-    size_t n4 = n / 4;
-    for (size_t j = i; j < n4; j += stride) {
-        float4 v = reinterpret_cast<const float4 *>(src)[j];
-        ushort4 o;
-        o.x = to16(dtype, v.x);
-        o.y = to16(dtype, v.y);
-        o.z = to16(dtype, v.z);
-        o.w = to16(dtype, v.w);
-        reinterpret_cast<ushort4 *>(dst)[j] = o;
+    const bool vec = ((((uintptr_t)src) | ((uintptr_t)dst)) & 15) == 0;
+    size_t n8 = vec ? n / 8 : 0;
+    for (size_t j = i; j < n8; j += stride) {
+        const float4 v0 = reinterpret_cast<const float4 *>(src)[2 * j];
+        const float4 v1 = reinterpret_cast<const float4 *>(src)[2 * j + 1];
+        uint4 o;
+        o.x = (uint32_t)to16(dtype, v0.x) | ((uint32_t)to16(dtype, v0.y) << 16);
+        o.y = (uint32_t)to16(dtype, v0.z) | ((uint32_t)to16(dtype, v0.w) << 16);
+        o.z = (uint32_t)to16(dtype, v1.x) | ((uint32_t)to16(dtype, v1.y) << 16);
+        o.w = (uint32_t)to16(dtype, v1.z) | ((uint32_t)to16(dtype, v1.w) << 16);
+        reinterpret_cast<uint4 *>(dst)[j] = o;
     }
-    for (size_t j = n4 * 4 + i; j < n; j += stride)
+    for (size_t j = n8 * 8 + i; j < n; j += stride)
         dst[j] = to16(dtype, src[j]);
 }
 
@@ -432,6 +458,104 @@ __global__ void __launch_bounds__(kBlock) k_sgd(sgd_table tab, float lr, float m
     }
 }
 
+// ---------------------------------------------------------------- linear backward
+// dz = g * act'(z) (act 0: dz = g) for a [m, n] f32 grad, written as RNE
+// 16-bit rows of ldd (ldd % 8 == 0) with zeros in columns [n, ldd).  A
+// block is 16 x 16 lanes over 128 columns: lane (cx, ry) takes columns
+// 8 cx .. 8 cx + 7 of rows ry, ry + 16, ... of the block's `rpb` rows, so a
+// wave reads 4 rows of 512 contiguous bytes per load.  With part given,
+// the block's column sums (the 16 row lanes added in ry order) go to
+// part[row block][n]; k_colsum_fin adds the row blocks in order
+// (deterministic).
+__device__ __forceinline__ float act_grad(int act, float z)
+{
+    if (act == 1)
+        return z > 0.0f ? 1.0f : 0.0f;
+    if (act == 2)
+        return pgm_gelu_grad(z);
+    return 1.0f;
+}
+
+__global__ void __launch_bounds__(kBlock) k_act_bwd16(int act, const float *__restrict__ g,
+                                                      const float *__restrict__ z, size_t m, size_t n,
+                                                      uint16_t *__restrict__ d16, size_t ldd, int dtype,
+                                                      float *__restrict__ part, size_t rpb)
+{
+    __shared__ float red[16][129];
+    const int cx = threadIdx.x & 15, ry = threadIdx.x >> 4;
+    const size_t c0 = (size_t)blockIdx.x * 128 + (size_t)cx * 8;
+    const size_t rb = (size_t)blockIdx.y * rpb, re = rb + rpb < m ? rb + rpb : m;
+    const bool vec = c0 + 8 <= n && (n & 3) == 0 && ((((uintptr_t)g) | ((uintptr_t)z)) & 15) == 0;
+    float acc[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+        acc[q] = 0.0f;
+    if (c0 < ldd) {
+#pragma unroll 2
+        for (size_t r = rb + ry; r < re; r += 16) {
+            float gv[8], zv[8];
+            const size_t off = r * n + c0;
+            if (vec) {
+                const float4 g0 = *reinterpret_cast<const float4 *>(g + off);
+                const float4 g1 = *reinterpret_cast<const float4 *>(g + off + 4);
+                gv[0] = g0.x, gv[1] = g0.y, gv[2] = g0.z, gv[3] = g0.w;
+                gv[4] = g1.x, gv[5] = g1.y, gv[6] = g1.z, gv[7] = g1.w;
+                if (act) {
+                    const float4 z0 = *reinterpret_cast<const float4 *>(z + off);
+                    const float4 z1 = *reinterpret_cast<const float4 *>(z + off + 4);
+                    zv[0] = z0.x, zv[1] = z0.y, zv[2] = z0.z, zv[3] = z0.w;
+                    zv[4] = z1.x, zv[5] = z1.y, zv[6] = z1.z, zv[7] = z1.w;
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    const bool in = c0 + q < n;
+                    gv[q] = in ? g[off + q] : 0.0f;
+                    zv[q] = (in && act) ? z[off + q] : 0.0f;
+                }
+            }
+            uint32_t w[4];
+#pragma unroll
+            for (int q = 0; q < 8; q += 2) {
+                const float d0 = act ? gv[q] * act_grad(act, zv[q]) : gv[q];
+                const float d1 = act ? gv[q + 1] * act_grad(act, zv[q + 1]) : gv[q + 1];
+                acc[q] += d0;
+                acc[q + 1] += d1;
+                w[q / 2] = (uint32_t)to16(dtype, d0) | ((uint32_t)to16(dtype, d1) << 16);
+            }
+            // columns past n hold g = 0, so they store zeros
+            *reinterpret_cast<uint4 *>(d16 + r * ldd + c0) = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+    }
+    if (part) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+            red[ry][cx * 8 + q] = acc[q];
+        __syncthreads();
+        if (threadIdx.x < 128) {
+            const size_t col = (size_t)blockIdx.x * 128 + threadIdx.x;
+            float sum = 0.0f;
+#pragma unroll
+            for (int y = 0; y < 16; ++y)
+                sum += red[y][threadIdx.x];
+            if (col < n)
+                part[(size_t)blockIdx.y * n + col] = sum;
+        }
+    }
+}
+
+__global__ void __launch_bounds__(64) k_colsum_fin(const float *__restrict__ part, size_t nblk, size_t n,
+                                                   float *__restrict__ out, int beta)
+{
+    for (size_t c = (size_t)blockIdx.x * blockDim.x + threadIdx.x; c < n; c += (size_t)gridDim.x * blockDim.x) {
+        float acc = 0.0f;
+#pragma unroll 8
+        for (size_t b = 0; b < nblk; ++b)
+            acc += part[b * n + c];
+        out[c] = beta ? out[c] + acc : acc;
+    }
+}
+
 } // namespace
 
 // ---------------------------------------------------------------- launchers
@@ -478,6 +602,18 @@ extern "C" int pgk_binary_f32(int op, const float *a, const float *b, float *y, 
         n *= (size_t)bc->shape[d];
     if (!n)
         return 0;
+    const int nl = bc->ndim - 1;
+    bool rows4 = bc->ndim >= 1 && bc->shape[nl] % 4 == 0 && (bc->sa[nl] == 0 || bc->sa[nl] == 1) &&
+                 (bc->sb[nl] == 0 || bc->sb[nl] == 1) &&
+                 (((uintptr_t)a | (uintptr_t)b | (uintptr_t)y) & 15) == 0;
+    for (int d = 0; rows4 && d < nl; ++d)
+        rows4 = (bc->sa[nl] == 0 || bc->sa[d] % 4 == 0) && (bc->sb[nl] == 0 || bc->sb[d] % 4 == 0);
+    if (rows4) {
+        size_t c4 = (size_t)bc->shape[nl] / 4;
+        hipLaunchKernelGGL(k_binary_rows4, dim3(grid_for(n / 4, 2)), dim3(kBlock), 0, (hipStream_t)s, op, a, b,
+                           y, n / 4 / c4, c4, *bc);
+        return status();
+    }
     hipLaunchKernelGGL(k_binary, dim3(grid_for(n, 4)), dim3(kBlock), 0, (hipStream_t)s, op, a, b, y, n, *bc);
     return status();
 }
@@ -526,14 +662,29 @@ extern "C" int pgk_expand_into_f32(float *dst, const float *src, const pgk_bcast
     return status();
 }
 
+extern "C" size_t pgk_sum_axis_workspace(size_t outer, size_t len, size_t inner)
+{
+    size_t slices, slice_len;
+    sum_axis_plan(outer, len, inner, &slices, &slice_len);
+    return slices > 1 ? slices * outer * inner * sizeof(float) : 0;
+}
+
 extern "C" int pgk_sum_axis_f32(const float *x, float *y, size_t outer, size_t len, size_t inner, float scale,
-                                pgk_stream s)
+                                void *ws, pgk_stream s)
 {
     size_t n = outer * inner;
     if (!n)
         return 0;
-    hipLaunchKernelGGL(k_sum_axis, dim3(grid_for(n)), dim3(kBlock), 0, (hipStream_t)s, x, y, outer, len, inner,
-                       scale);
+    size_t slices, slice_len;
+    sum_axis_plan(outer, len, inner, &slices, &slice_len);
+    if (slices > 1 && !ws)
+        return (int)hipErrorInvalidValue;
+    float *part = slices > 1 ? (float *)ws : y;
+    hipLaunchKernelGGL(k_sum_axis_part, dim3(grid_for(slices * n)), dim3(kBlock), 0, (hipStream_t)s, x, part,
+                       outer, len, inner, slices, slice_len, scale);
+    if (slices > 1)
+        hipLaunchKernelGGL(k_sum_axis_fin, dim3(grid_for(n)), dim3(kBlock), 0, (hipStream_t)s, part, y, n, slices,
+                           scale);
     return status();
 }
 
@@ -594,4 +745,46 @@ extern "C" int pgk_sgd_multi(const pgk_sgd_seg *segs, int nseg, float lr, float 
             return st;
     }
     return 0;
+}
+
+// rows per block of k_act_bwd16: a multiple of 16 giving about 2048 blocks
+// (fewer for narrow grads)
+static size_t act_bwd_rpb(size_t m, size_t ldd)
+{
+    const size_t xb = (ldd + 127) / 128;
+    size_t nrb = 2048 / (xb ? xb : 1);
+    if (nrb > 64)
+        nrb = 64; // the finisher adds at most 64 partials per column
+    if (nrb < 1)
+        nrb = 1;
+    size_t rpb = (m + nrb - 1) / nrb;
+    rpb = (rpb + 15) & ~(size_t)15;
+    return rpb < 16 ? 16 : rpb;
+}
+
+extern "C" size_t pgk_act_bwd16_workspace(size_t m, size_t n)
+{
+    const size_t ldd = (n + 7) & ~(size_t)7;
+    const size_t rpb = act_bwd_rpb(m, ldd);
+    return ((m + rpb - 1) / rpb) * n * sizeof(float);
+}
+
+extern "C" int pgk_act_bwd16(int act, const float *g, const float *z, size_t m, size_t n, uint16_t *d16, size_t ldd,
+                             int dtype, float *db, int db_beta, void *ws, pgk_stream s)
+{
+    if (!m || !n)
+        return 0;
+    if ((ldd & 7) || ldd < n || (((uintptr_t)d16) & 15) || (act && !z) || (db && !ws) || act < 0 || act > 2)
+        return (int)hipErrorInvalidValue;
+    const size_t rpb = act_bwd_rpb(m, ldd), nrb = (m + rpb - 1) / rpb;
+    if (nrb > 65535)
+        return (int)hipErrorInvalidValue;
+    const unsigned gx = (unsigned)((ldd + 127) / 128);
+    float *part = db ? (float *)ws : nullptr;
+    hipLaunchKernelGGL(k_act_bwd16, dim3(gx, (unsigned)nrb), dim3(kBlock), 0, (hipStream_t)s, act, g, z, m, n, d16,
+                       ldd, dtype, part, rpb);
+    if (db)
+        hipLaunchKernelGGL(k_colsum_fin, dim3((unsigned)((n + 63) / 64)), dim3(64), 0, (hipStream_t)s, part, nrb, n,
+                           db, db_beta);
+    return status();
 }

@@ -32,7 +32,9 @@
 
 #include <type_traits>
 
+#include "convert16.h"
 #include "launch.h"
+#include "pgmath.h"
 
 namespace {
 
@@ -41,9 +43,19 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef short v4s __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 #define LDS __attribute__((address_space(3)))
 
 constexpr int BK = 64;
+
+__device__ __forceinline__ float act_f(int act, float v)
+{
+    if (act == PGK_ACT_RELU)
+        return v > 0.0f ? v : 0.0f;
+    if (act == PGK_ACT_GELU)
+        return pgm_gelu(v);
+    return v;
+}
 
 // s_waitcnt immediate waiting for vmcnt <= n only (gfx9 encoding: vmcnt in
 // bits 3:0 and 15:14; expcnt 6:4 and lgkmcnt 11:8 left at their maxima)
@@ -156,11 +168,11 @@ struct TileMN {
     }
 };
 
-template <int BM, int BN, int WGM, int WGN, bool TA, bool TB, bool F16>
+template <int BM, int BN, int WGM, int WGN, bool TA, bool TB, bool F16, bool EPI>
 __global__ void __launch_bounds__(64 * WGM * WGN, 1)
     k_gemm16(const uint16_t *__restrict__ A, size_t lda, size_t sA, int a_extent, const uint16_t *__restrict__ B,
              size_t ldb, size_t sB, int b_extent, float *__restrict__ C, size_t ldc, size_t sC, int M, int N, int K,
-             int beta, int tiles_m, int tiles_n)
+             int beta, int tiles_m, int tiles_n, pgk_epi epi)
 {
     constexpr int NT = 64 * WGM * WGN;
     constexpr int WM = BM / WGM, WN = BN / WGN;
@@ -251,23 +263,106 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1)
 
     // epilogue: lane holds column lane % 32 of rows (e/4)*8 + (lane/32)*4 + e%4
     const int lrow = lane & 31, lk = lane >> 5;
+    if constexpr (EPI) {
+        // Through LDS, 32 rows of the wave's WM x WN tile at a time: the
+        // accumulators land row-major in a per-wave [32][WN + 8] f32 region
+        // (in the operand stages, free after the k-loop) and come back as
+        // float4 along a row, so bias, activation and the three stores (out,
+        // pre-activation, 16-bit out) run 4 columns per lane with 16-byte
+        // (8-byte for 16-bit) stores.  Every index into acc stays static.
+        static_assert(WN == 64, "one lane group of 16 x 4 columns per row");
+        constexpr int RS = WN + 8;
+        constexpr int RPA = (BM * 8 * 16) / (32 * RS * 4); // regions per stage array
+        static_assert(RPA >= 1 && WGM * WGN <= 4 * RPA && BM == BN, "epilogue regions fit the stages");
+        const int arr = wave / RPA, slot = wave % RPA;
+        LDS char *abase = arr == 0 ? (LDS char *)A0 : arr == 1 ? (LDS char *)A1 : arr == 2 ? (LDS char *)B0 : (LDS char *)B1;
+        LDS float *reg = (LDS float *)(abase + slot * (32 * RS * 4));
+        const int c4 = (lane & 15) * 4;
+        const int gcol = n0 + wn * WN + c4;
+        float bias4[4];
 #pragma unroll
-    for (int i = 0; i < FM; ++i) {
+        for (int q = 0; q < 4; ++q)
+            bias4[q] = (epi.bias && gcol + q < N) ? epi.bias[gcol + q] : 0.0f;
+        const bool v4 = (ldc & 3) == 0 && gcol + 3 < N && (((uintptr_t)Cb) & 15) == 0 &&
+                        (((uintptr_t)epi.z) & 15) == 0 && (((uintptr_t)epi.c16) & 7) == 0;
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
-            const int col = n0 + wn * WN + j * 32 + lrow;
-            if (col >= N)
-                continue;
+        for (int i = 0; i < FM; ++i) {
+            __syncthreads(); // the k-loop's (or the previous pass') LDS reads are done
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int row = m0 + wm * WM + i * 32 + (e >> 2) * 8 + lk * 4 + (e & 3);
-                if (row < M) {
-                    float *p = Cb + (size_t)row * ldc + col;
-                    const float v = acc[i][j][e];
-                    *p = beta ? *p + v : v;
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e)
+                    reg[((e >> 2) * 8 + lk * 4 + (e & 3)) * RS + j * 32 + lrow] = acc[i][j][e];
+            __syncthreads();
+            for (int t = 0; t < 8; ++t) {
+                const int row = (lane >> 4) + 4 * t;
+                const int grow = m0 + wm * WM + i * 32 + row;
+                if (grow >= M || gcol >= N)
+                    continue;
+                const f32x4 a4 = *(const LDS f32x4 *)(reg + row * RS + c4);
+                const float zv[4] = {a4[0] + bias4[0], a4[1] + bias4[1], a4[2] + bias4[2], a4[3] + bias4[3]};
+                float o[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    o[q] = act_f(epi.act, zv[q]);
+                const size_t off = (size_t)grow * ldc + gcol;
+                if (v4) {
+                    *reinterpret_cast<float4 *>(Cb + off) = make_float4(o[0], o[1], o[2], o[3]);
+                    if (epi.z)
+                        *reinterpret_cast<float4 *>(epi.z + off) = make_float4(zv[0], zv[1], zv[2], zv[3]);
+                    if (epi.c16)
+                        *reinterpret_cast<uint2 *>(epi.c16 + off) =
+                            make_uint2((uint32_t)to16(epi.dtype16, o[0]) | ((uint32_t)to16(epi.dtype16, o[1]) << 16),
+                                       (uint32_t)to16(epi.dtype16, o[2]) | ((uint32_t)to16(epi.dtype16, o[3]) << 16));
+                } else {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        if (gcol + q >= N)
+                            break;
+                        Cb[off + q] = o[q];
+                        if (epi.z)
+                            epi.z[off + q] = zv[q];
+                        if (epi.c16)
+                            epi.c16[off + q] = to16(epi.dtype16, o[q]);
+                    }
                 }
             }
         }
+    } else {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const int col = n0 + wn * WN + j * 32 + lrow;
+                if (col >= N)
+                    continue;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int row = m0 + wm * WM + i * 32 + (e >> 2) * 8 + lk * 4 + (e & 3);
+                    if (row < M) {
+                        float *p = Cb + (size_t)row * ldc + col;
+                        const float v = acc[i][j][e];
+                        *p = beta ? *p + v : v;
+                    }
+                }
+            }
+        }
+    }
+}
+
+// the same epilogue as a pass over a finished C (split-K or k-tail runs)
+__global__ void __launch_bounds__(256) k_bias_act(float *__restrict__ c, size_t ldc, int m, int n, pgk_epi epi)
+{
+    const size_t mn = (size_t)m * n;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < mn; i += (size_t)gridDim.x * blockDim.x) {
+        const size_t r = i / n, col = i - r * n, off = r * ldc + col;
+        const float v = c[off] + (epi.bias ? epi.bias[col] : 0.0f);
+        const float o = act_f(epi.act, v);
+        c[off] = o;
+        if (epi.z)
+            epi.z[off] = v;
+        if (epi.c16)
+            epi.c16[off] = to16(epi.dtype16, o);
     }
 }
 
@@ -293,6 +388,33 @@ __global__ void __launch_bounds__(256) k_pack_slab(int mn_major, const uint16_t 
         if (r < rows && c < kn)
             v = mn_major ? s[(size_t)(k0 + c) * ld + r] : s[(size_t)r * ld + k0 + c];
         d[i] = v;
+    }
+}
+
+// split-K finish: C = (beta ? C : 0) + sum over the `splits` partial
+// products (each m x n, dense), added in split order
+__global__ void __launch_bounds__(256) k_splitk_sum(const float *__restrict__ part, int splits, int m, int n,
+                                                    float *__restrict__ c, size_t ldc, int beta)
+{
+    const size_t mn = (size_t)m * n;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < mn; i += (size_t)gridDim.x * blockDim.x) {
+        float acc = 0.0f;
+        for (int z = 0; z < splits; ++z)
+            acc += part[(size_t)z * mn + i];
+        const size_t r = i / n, col = i - r * n;
+        float *p = c + r * ldc + col;
+        *p = beta ? *p + acc : acc;
+    }
+}
+
+// C rows of an empty reduction: zeros
+__global__ void __launch_bounds__(256) k_zero_rows(float *__restrict__ c, size_t ldc, size_t sc, int m, int n)
+{
+    float *cb = c + (size_t)blockIdx.z * sc;
+    const size_t mn = (size_t)m * n;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < mn; i += (size_t)gridDim.x * blockDim.x) {
+        const size_t r = i / n, col = i - r * n;
+        cb[r * ldc + col] = 0.0f;
     }
 }
 
@@ -363,27 +485,28 @@ struct gemm_args {
     size_t ldc, sc;
     int m, n, k, beta;
     unsigned batch;
+    bool small_tiles; // 128 x 128 tiles whatever the count (split-K runs)
 };
 
-template <int BM, int BN, int WGM, int WGN, bool TA, bool TB, bool F16>
-int launch_tile(const gemm_args &g, hipStream_t s)
+template <int BM, int BN, int WGM, int WGN, bool TA, bool TB, bool F16, bool EPI>
+int launch_tile(const gemm_args &g, const pgk_epi &epi, hipStream_t s)
 {
     const int tm = (g.m + BM - 1) / BM, tn = (g.n + BN - 1) / BN;
-    hipLaunchKernelGGL((k_gemm16<BM, BN, WGM, WGN, TA, TB, F16>), dim3((unsigned)(tm * tn), 1, g.batch),
+    hipLaunchKernelGGL((k_gemm16<BM, BN, WGM, WGN, TA, TB, F16, EPI>), dim3((unsigned)(tm * tn), 1, g.batch),
                        dim3(64 * WGM * WGN), 0, s, g.a, g.lda, g.sa, g.a_extent, g.b, g.ldb, g.sb, g.b_extent, g.c,
-                       g.ldc, g.sc, g.m, g.n, g.k, g.beta, tm, tn);
+                       g.ldc, g.sc, g.m, g.n, g.k, g.beta, tm, tn, epi);
     return (int)hipGetLastError();
 }
 
-template <bool TA, bool TB, bool F16>
-int launch_layout(const gemm_args &g, hipStream_t s)
+template <bool TA, bool TB, bool F16, bool EPI = false>
+int launch_layout(const gemm_args &g, hipStream_t s, const pgk_epi &epi = pgk_epi{})
 {
     // 256 x 256 tiles (eight waves, each 128 x 64) whenever they still give
     // most CUs a tile; else 128 x 128 (four waves, each 64 x 64)
     const size_t big = (size_t)((g.m + 255) / 256) * ((g.n + 255) / 256) * g.batch;
-    if (big >= 128)
-        return launch_tile<256, 256, 2, 4, TA, TB, F16>(g, s);
-    return launch_tile<128, 128, 2, 2, TA, TB, F16>(g, s);
+    if (big >= 128 && !g.small_tiles)
+        return launch_tile<256, 256, 2, 4, TA, TB, F16, EPI>(g, epi, s);
+    return launch_tile<128, 128, 2, 2, TA, TB, F16, EPI>(g, epi, s);
 }
 
 int launch_any(int f16, int ta, int tb, const gemm_args &g, hipStream_t s)
@@ -403,7 +526,30 @@ int launch_any(int f16, int ta, int tb, const gemm_args &g, hipStream_t s)
 
 } // namespace
 
-extern "C" size_t pgk_gemm16_workspace(int ta, int tb, size_t m, size_t n, size_t k, size_t batch)
+// Split-K for GEMMs with few output tiles and a long reduction (the N = 10
+// layer of an MLP and its weight grad, a weight grad with a short output
+// dim): `splits` slices of the 64-aligned part of k run as a batch into
+// dense partials, then k_splitk_sum adds them in slice order into C
+// (deterministic).  256 x 256 tiles fill the chip at one per CU, so a GEMM
+// with 128 of them is not split; 128 x 128 tiles (four waves, under half a
+// CU's registers) are split towards two per CU.  0 = not split.
+static int splitk_plan(size_t m, size_t n, size_t kmain, size_t batch)
+{
+    if (batch != 1 || kmain < 1024)
+        return 0;
+    const size_t big = ((m + 255) / 256) * ((n + 255) / 256);
+    const size_t tiles = ((m + 127) / 128) * ((n + 127) / 128);
+    if (big >= 128 || tiles >= 512 || (tiles >= 128 && kmain < 2048))
+        return 0;
+    const size_t chunks = kmain / BK;
+    size_t want = (512 + tiles - 1) / tiles, most = kmain / 512;
+    size_t sp = want < most ? want : most;
+    while (sp > 1 && chunks % sp)
+        --sp;
+    return sp > 1 ? (int)sp : 0;
+}
+
+static size_t tail_ws(int ta, int tb, size_t m, size_t n, size_t k, size_t batch)
 {
     if (k % BK == 0)
         return 0;
@@ -413,13 +559,23 @@ extern "C" size_t pgk_gemm16_workspace(int ta, int tb, size_t m, size_t n, size_
     return (a + 64 + b) * sizeof(uint16_t);
 }
 
+extern "C" size_t pgk_gemm16_workspace(int ta, int tb, size_t m, size_t n, size_t k, size_t batch)
+{
+    const int sp = splitk_plan(m, n, k - k % BK, batch);
+    const size_t part = sp ? (((size_t)sp * m * n * sizeof(float) + 255) & ~(size_t)255) : 0;
+    return part + tail_ws(ta, tb, m, n, k, batch);
+}
+
 extern "C" int pgk_gemm16(int dtype, int ta, int tb, size_t m, size_t n, size_t k, const uint16_t *a, size_t lda,
                           size_t stride_a, size_t a_extent, const uint16_t *b, size_t ldb, size_t stride_b,
-                          size_t b_extent, float *c, size_t ldc, size_t stride_c, size_t batch, int beta, void *ws,
-                          pgk_stream s)
+                          size_t b_extent, float *c, size_t ldc, size_t stride_c, size_t batch, int beta,
+                          const pgk_epi *epi, void *ws, pgk_stream s)
 {
     if (!m || !n || !batch)
         return 0;
+    const bool has_epi = epi && (epi->bias || epi->act != PGK_ACT_NONE || epi->z || epi->c16);
+    if (has_epi && (beta || batch != 1 || (epi->c16 && epi->dtype16 != 1 && epi->dtype16 != 2)))
+        return (int)hipErrorInvalidValue;
     if (m > 0x7fffffff || n > 0x7fffffff || k > 0x7fffffff || batch > 65535)
         return (int)hipErrorInvalidValue;
     // 16-byte global loads: aligned bases, leading dims and batch strides
@@ -432,32 +588,56 @@ extern "C" int pgk_gemm16(int dtype, int ta, int tb, size_t m, size_t n, size_t 
     hipStream_t st = (hipStream_t)s;
     const int f16 = dtype == 1;
     const size_t kmain = k - k % BK, ktail = k % BK;
+    const size_t mn = m * n;
+    const unsigned gmn = (unsigned)((mn + 255) / 256 < 2048 ? (mn + 255) / 256 : 2048);
     if (!k) { // empty reduction: C = beta ? C : 0
-        if (beta)
-            return 0;
-        for (size_t z = 0; z < batch; ++z)
-            for (size_t r = 0; r < m; ++r) {
-                hipError_t e = hipMemsetAsync(c + z * stride_c + r * ldc, 0, n * sizeof(float), st);
-                if (e)
-                    return (int)e;
-            }
-        return 0;
+        if (!beta)
+            hipLaunchKernelGGL(k_zero_rows, dim3(gmn, 1, (unsigned)batch), dim3(256), 0, st, c, ldc, stride_c,
+                               (int)m, (int)n);
+        if (has_epi)
+            hipLaunchKernelGGL(k_bias_act, dim3(gmn), dim3(256), 0, st, c, ldc, (int)m, (int)n, *epi);
+        return (int)hipGetLastError();
     }
-    if (kmain) {
+    const int sp = splitk_plan(m, n, kmain, batch);
+    // the epilogue rides on the GEMM when one launch of the forward layout
+    // finishes C; otherwise it is a pass over C afterwards
+    if (has_epi && !sp && !ktail && !ta && tb) {
+        gemm_args g = {a, lda, stride_a, (int)a_extent, b, ldb, stride_b, (int)b_extent, c, ldc, stride_c,
+                       (int)m, (int)n, (int)kmain, 0, 1u};
+        return f16 ? launch_layout<false, true, true, true>(g, st, *epi)
+                   : launch_layout<false, true, false, true>(g, st, *epi);
+    }
+    const size_t part_bytes = sp ? (((size_t)sp * m * n * sizeof(float) + 255) & ~(size_t)255) : 0;
+    if ((sp || ktail) && !ws)
+        return (int)hipErrorInvalidValue;
+    int rc = 0;
+    if (kmain && sp) {
+        // slice z covers k in [z * ks, (z + 1) * ks): operand offsets along
+        // the reduction, dense [m, n] partials
+        const size_t ks = kmain / (size_t)sp;
+        float *part = (float *)ws;
+        gemm_args g = {a, lda, ta ? ks * lda : ks, (int)a_extent, b, ldb, tb ? ks * ldb : ks, (int)b_extent, part, n,
+                       m * n, (int)m, (int)n, (int)ks, 0, (unsigned)sp, true};
+        rc = launch_any(f16, ta, tb, g, st);
+        if (rc)
+            return rc;
+        hipLaunchKernelGGL(k_splitk_sum, dim3(gmn), dim3(256), 0, st, part, sp, (int)m, (int)n, c, ldc, beta);
+        rc = (int)hipGetLastError();
+        if (rc)
+            return rc;
+    } else if (kmain) {
         gemm_args g = {a, lda, stride_a, (int)a_extent, b, ldb, stride_b, (int)b_extent, c, ldc, stride_c,
                        (int)m, (int)n, (int)kmain, beta, (unsigned)batch};
-        int rc = launch_any(f16, ta, tb, g, st);
+        rc = launch_any(f16, ta, tb, g, st);
         if (rc)
             return rc;
     }
     if (ktail) {
-        if (!ws)
-            return (int)hipErrorInvalidValue;
         // last k-slab of each operand, zero-padded to 64 (and to a multiple
         // of 8 columns for an MN-contiguous copy), then one more launch
         const size_t ma = ta ? (((m + 7) & ~(size_t)7) < 8 ? 8 : ((m + 7) & ~(size_t)7)) : m;
         const size_t nbp = tb ? (((n + 7) & ~(size_t)7) < 8 ? 8 : ((n + 7) & ~(size_t)7)) : n;
-        uint16_t *pa = (uint16_t *)ws;
+        uint16_t *pa = (uint16_t *)((char *)ws + part_bytes);
         const size_t asz = 64 * ma;
         uint16_t *pb = pa + ((asz * batch + 63) & ~(size_t)63);
         const size_t bsz = 64 * nbp;
@@ -467,13 +647,19 @@ extern "C" int pgk_gemm16(int dtype, int ta, int tb, size_t m, size_t n, size_t 
                            (int)ma, (int)kmain, (int)ktail, pa, asz);
         hipLaunchKernelGGL(k_pack_slab, dim3(gb, 1, (unsigned)batch), dim3(256), 0, st, tb, b, ldb, stride_b, (int)n,
                            (int)nbp, (int)kmain, (int)ktail, pb, bsz);
-        int rc = (int)hipGetLastError();
+        rc = (int)hipGetLastError();
         if (rc)
             return rc;
         gemm_args g = {pa, ta ? ma : (size_t)64, asz, (int)(ta ? ma : m), pb, tb ? nbp : (size_t)64, bsz,
                        (int)(tb ? nbp : n), c, ldc, stride_c, (int)m, (int)n, BK, kmain ? 1 : beta,
                        (unsigned)batch};
-        return launch_any(f16, ta, tb, g, st);
+        rc = launch_any(f16, ta, tb, g, st);
+        if (rc)
+            return rc;
+    }
+    if (has_epi) {
+        hipLaunchKernelGGL(k_bias_act, dim3(gmn), dim3(256), 0, st, c, ldc, (int)m, (int)n, *epi);
+        return (int)hipGetLastError();
     }
     return 0;
 }

@@ -60,9 +60,12 @@ int pgk_reduce_into_f32(float *dst, size_t dst_numel, const float *src, const pg
 int pgk_expand_into_f32(float *dst, const float *src, const pgk_bcast *bc, float scale, int beta,
                         pgk_stream s);
 
-/* forward reductions: y[o, i] = scale * sum_l x[o, l, i] */
+/* forward reductions: y[o, i] = scale * sum_l x[o, l, i], summed in
+ * fixed slices of l and then across slices (deterministic).  ws holds
+ * pgk_sum_axis_workspace() bytes (none needed when that is 0). */
+size_t pgk_sum_axis_workspace(size_t outer, size_t len, size_t inner);
 int pgk_sum_axis_f32(const float *x, float *y, size_t outer, size_t len, size_t inner,
-                     float scale, pgk_stream s);
+                     float scale, void *ws, pgk_stream s);
 
 /* dtype casts with the reference's RNE bit rules; dtype 1 = f16, 2 = bf16 */
 int pgk_cast_to16(int dtype, const float *src, uint16_t *dst, size_t n, pgk_stream s);
@@ -92,15 +95,39 @@ int pgk_copy_to16(int dtype, int src_dtype, const void *src, size_t rows, size_t
  * pgk_gemm16_workspace(...) bytes (it stages the last k-slab).
  */
 size_t pgk_gemm16_workspace(int ta, int tb, size_t m, size_t n, size_t k, size_t batch);
+
+/* Optional epilogue of pgk_gemm16 (one matrix, beta = 0): with
+ * v = sum_p A(i, p) B(p, j) + bias[j], it writes C[i, j] = act(v),
+ * z[i, j] = v and c16[i, j] = RNE-16-bit(act(v)) (z, c16 at C's leading
+ * dim; each NULL to skip).  act codes follow the reference's
+ * backend/cpu/gemm.h:37-39. */
+enum { PGK_ACT_NONE = 0, PGK_ACT_RELU = 1, PGK_ACT_GELU = 2 };
+typedef struct {
+    const float *bias; /* [n] or NULL */
+    int act;
+    float *z;
+    uint16_t *c16;
+    int dtype16; /* 1 = f16, 2 = bf16 */
+} pgk_epi;
 int pgk_gemm16(int dtype, int ta, int tb, size_t m, size_t n, size_t k, const uint16_t *a, size_t lda,
                size_t stride_a, size_t a_extent, const uint16_t *b, size_t ldb, size_t stride_b, size_t b_extent,
-               float *c, size_t ldc, size_t stride_c, size_t batch, int beta, void *ws, pgk_stream s);
+               float *c, size_t ldc, size_t stride_c, size_t batch, int beta, const pgk_epi *epi, void *ws,
+               pgk_stream s);
 
 /* f32 GEMM, C (beta ? += : =) op(A) op(B); ta/tb select A^T / B^T
  * (A(i,p) = ta ? a[p*lda+i] : a[i*lda+p], same for B(p,j)). */
 int pgk_gemm_f32(int ta, int tb, size_t m, size_t n, size_t k, const float *a, size_t lda,
                  size_t stride_a, const float *b, size_t ldb, size_t stride_b, float *c,
                  size_t ldc, size_t stride_c, size_t batch, int beta, pgk_stream s);
+
+/* Backward of an activation feeding a 16-bit GEMM: dz = g * act'(z) over
+ * a [m, n] f32 grad (act PGK_ACT_*; z the pre-activation, unused for
+ * PGK_ACT_NONE), written RNE to d16 rows of ldd (ldd % 8 == 0, zero columns
+ * past n); when db is given, db[j] (beta ? += : =) sum_i dz[i, j] in a
+ * fixed order (ws holds pgk_act_bwd16_workspace bytes). */
+size_t pgk_act_bwd16_workspace(size_t m, size_t n);
+int pgk_act_bwd16(int act, const float *g, const float *z, size_t m, size_t n, uint16_t *d16, size_t ldd,
+                  int dtype, float *db, int db_beta, void *ws, pgk_stream s);
 
 /* multi-tensor SGD */
 typedef struct {

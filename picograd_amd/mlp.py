@@ -11,6 +11,9 @@ dtype F32 runs the reference's own f32 graph (pg_ag_matmul).  BF16/F16 run
 the layer's matmul through pg_amd_ag_matmul16: f32 master weights and
 activations, GEMM operands rounded to the 16-bit dtype, f32 accumulation;
 the 16-bit weight copy is rewritten by pg_sgd_step in the update pass.
+With fused=True (16-bit only) each layer is one pg_amd_ag_linear16 node --
+the same arithmetic with bias and gelu in the GEMM epilogue and the bias
+grad, gelu' and the 16-bit grad cast in one backward pass.
 """
 from __future__ import annotations
 
@@ -20,13 +23,17 @@ import numpy as np
 
 from .capi import F32, PgLib, SgdCfg, shape_arg
 
+ACT_NONE, ACT_RELU, ACT_GELU = 0, 1, 2  # PG_ACT_* (backend/cpu/gemm.h:37-39)
+
 
 class Mlp:
     def __init__(self, lib: PgLib, Ws, bs, dtype: int = F32,
-                 sgd=(0.01, 0.9, 0.0, 1e-4, True)):
+                 sgd=(0.01, 0.9, 0.0, 1e-4, True), fused: bool = False):
         """Ws, bs: lists of parameter nodes (f32 leaves with requires_grad),
         W_l [d_l, d_{l+1}], b_l [d_{l+1}]; the optimiser retains them."""
-        self.lib, self.dtype = lib, dtype
+        if fused and dtype == F32:
+            raise ValueError("fused layers run 16-bit GEMM operands (dtype F16 or BF16)")
+        self.lib, self.dtype, self.fused = lib, dtype, fused
         self.Ws, self.bs = list(Ws), list(bs)
         self.opt = lib.pg_sgd_new(C.byref(SgdCfg(*sgd)))
         if not self.opt:
@@ -61,6 +68,12 @@ class Mlp:
         """Output node and the intermediate nodes to free after the step."""
         L = self.lib
         h, made = x, []
+        if self.fused:
+            for i, (w, b) in enumerate(zip(self.Ws, self.bs)):
+                act = ACT_GELU if i + 1 < len(self.Ws) else ACT_NONE
+                h = L._check(L.pg_amd_ag_linear16(h, w, b, act, self.dtype))
+                made.append(h)
+            return h, made
         for i, (w, b) in enumerate(zip(self.Ws, self.bs)):
             mm = self._matmul(h, w)
             made.append(mm)

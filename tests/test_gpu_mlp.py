@@ -112,6 +112,88 @@ def test_matmul16_kept_copy_follows_writes(lib, oracle):
     lib.pg_node_free(eye)
 
 
+# ---------------------------------------------------------------- linear16
+
+def _act_np(act, z):
+    from scipy.special import erf
+    z = z.astype(np.float64)
+    if act == 1:
+        return np.maximum(z, 0.0), (z > 0).astype(np.float64)
+    if act == 2:
+        cdf = 0.5 * (1.0 + erf(z / np.sqrt(2.0)))
+        return z * cdf, cdf + z * np.exp(-0.5 * z * z) / np.sqrt(2.0 * np.pi)
+    return z, np.ones_like(z)
+
+
+@pytest.mark.parametrize("dt", [BF16, F16])
+@pytest.mark.parametrize("act", [0, 1, 2])
+@pytest.mark.parametrize("M,K,N,bias", [(256, 192, 256, True), (70, 50, 10, True), (64, 128, 72, False),
+                                        (512, 4096, 16, True)])
+def test_linear16_matches_oracle(lib, oracle, dt, act, M, K, N, bias):
+    """out = act(q(x).q(W) + b) and its grads: dz = dout * act'(z),
+    db = sum_rows dz, dx = q(dz).q(W)^T, dW = q(x)^T.q(dz).  The shapes
+    cover the fused GEMM epilogue (one launch), the epilogue pass after a
+    k-tail (K = 50) or split-K (K = 4096, N = 16), and padded N = 10."""
+    print(f"linear16 dt={dt} act={act} M={M} K={K} N={N} bias={bias}", flush=True)
+    rng = np.random.default_rng(M + 3 * K + 7 * N + act)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w = (rng.standard_normal((K, N)) / np.sqrt(K)).astype(np.float32)
+    b = (0.3 * rng.standard_normal(N)).astype(np.float32)
+    g = rng.standard_normal((M, N)).astype(np.float32)
+    nx, nw = lib.var(x), lib.var(w)
+    nb = lib.var(b) if bias else None
+    out = lib._check(lib.pg_amd_ag_linear16(nx, nw, nb, act, dt))
+    ng = lib.var(g, requires_grad=False)
+    prod = lib.op("mul", out, ng)
+    loss = lib.op("sum_all", prod)
+    lib.pg_backward(loss)
+    qx, qw = _round(oracle, dt, x), _round(oracle, dt, w)
+    z = oracle.gemm(F32, qx, qw).astype(np.float64) + (b if bias else 0.0)
+    o, d = _act_np(act, z)
+    got = lib.value(out)
+    assert rel_fro(got, o) < GEMM_TOL
+    if act == 1:
+        # ReLU' is a step: where z is within rounding of 0 the device's sign
+        # decides, and out > 0 exactly when its z > 0
+        d = (got > 0).astype(np.float64)
+    dz = g.astype(np.float64) * d
+    qdz = _round(oracle, dt, dz.astype(np.float32))
+    assert rel_fro(lib.grad(nx), oracle.gemm(F32, qdz, qw, tb=True)) < GEMM_TOL
+    assert rel_fro(lib.grad(nw), oracle.gemm(F32, qx, qdz, ta=True)) < GEMM_TOL
+    if bias:
+        assert rel_fro(lib.grad(nb), dz.sum(axis=0)) < GEMM_TOL
+    for n in (loss, prod, ng, out, nx, nw) + ((nb,) if bias else ()):
+        lib.pg_node_free(n)
+
+
+def test_linear16_output_feeds_next_layer(lib, oracle):
+    """Two stacked layers: the second reads the first's 16-bit output copy
+    written by the GEMM epilogue; the result equals rounding the first
+    layer's f32 output."""
+    rng = np.random.default_rng(21)
+    x = rng.standard_normal((128, 64)).astype(np.float32)
+    w1 = (rng.standard_normal((64, 96)) / 8).astype(np.float32)
+    w2 = (rng.standard_normal((96, 40)) / 10).astype(np.float32)
+    nx, n1, n2 = lib.var(x, requires_grad=False), lib.var(w1), lib.var(w2)
+    h = lib._check(lib.pg_amd_ag_linear16(nx, n1, None, 2, BF16))
+    y = lib._check(lib.pg_amd_ag_linear16(h, n2, None, 0, BF16))
+    want = oracle.gemm(F32, _round(oracle, BF16, lib.value(h)), _round(oracle, BF16, w2))
+    assert rel_fro(lib.value(y), want) < 1e-5
+    for n in (y, h, nx, n1, n2):
+        lib.pg_node_free(n)
+
+
+def test_linear16_rejects_bad_input(lib):
+    a = lib.var(np.ones((4, 8), np.float32))
+    w = lib.var(np.ones((8, 6), np.float32))
+    b = lib.var(np.ones(5, np.float32))
+    assert not lib.pg_amd_ag_linear16(a, w, b, 0, BF16)  # bias length
+    assert not lib.pg_amd_ag_linear16(a, w, None, 3, BF16)  # act code
+    assert not lib.pg_amd_ag_linear16(a, w, None, 0, F32)  # dtype
+    for n in (a, w, b):
+        lib.pg_node_free(n)
+
+
 # ---------------------------------------------------------------- MLP step
 
 def _read_params(lib, mlp):
@@ -145,19 +227,21 @@ def test_mlp_f32_matches_reference_golden(lib):
     lib.pg_node_free(t)
 
 
+@pytest.mark.parametrize("fused", [False, True])
 @pytest.mark.parametrize("dt", [BF16, F16])
 @pytest.mark.parametrize("dims,batch", [((96, 128, 128, 128, 10), 64), ((50, 96, 72, 10), 40)])
-def test_mlp_16bit_matches_oracle(lib, oracle, dt, dims, batch):
-    """Two steps of the 16-bit network against orc_mlp_step on the same
-    inputs.  Step 2 reads the weight copies pg_sgd_step wrote in step 1."""
-    print(f"mlp dt={dt} dims={dims} batch={batch}", flush=True)
+def test_mlp_16bit_matches_oracle(lib, oracle, dt, dims, batch, fused):
+    """Two steps of the 16-bit network (matmul16 + add + gelu nodes, or one
+    linear16 node per layer) against orc_mlp_step on the same inputs.
+    Step 2 reads the weight copies pg_sgd_step wrote in step 1."""
+    print(f"mlp dt={dt} dims={dims} batch={batch} fused={fused}", flush=True)
     rng = np.random.default_rng(sum(dims) + batch)
     Ws = [(rng.uniform(-1, 1, (dims[i], dims[i + 1])) / np.sqrt(dims[i])).astype(np.float32)
           for i in range(len(dims) - 1)]
     bs = [(0.1 * rng.standard_normal(dims[i + 1])).astype(np.float32) for i in range(len(dims) - 1)]
     x = rng.standard_normal((batch, dims[0])).astype(np.float32)
     t = rng.standard_normal((batch, dims[-1])).astype(np.float32)
-    mlp = Mlp.from_arrays(lib, Ws, bs, dt)
+    mlp = Mlp.from_arrays(lib, Ws, bs, dt, fused=fused)
     nx, nt = lib.var(x, requires_grad=False), lib.var(t, requires_grad=False)
     rW, rb = [w.copy() for w in Ws], [b.copy() for b in bs]
     rWb, rbb = [np.zeros_like(w) for w in Ws], [np.zeros_like(b) for b in bs]
