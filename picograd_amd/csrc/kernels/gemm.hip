@@ -15,7 +15,7 @@
 //  - K-contiguous tiles sit in LDS as [rows][64] with 16-byte chunks
 //    XOR-swizzled by (r ^ r >> 3) & 7 and reach the MFMA with ds_read_b128;
 //    MN-contiguous tiles sit as [64][rows] with chunks swizzled by
-//    2 (k & 3) and reach it with ds_read_b64_tr_b16, the gfx950 transposing
+//    4 (k & 3) and reach it with ds_read_b64_tr_b16, the gfx950 transposing
 //    LDS read (within each 16-lane group, lane i of the result takes element
 //    i % 4 of the 8 bytes lane 4p + i / 4 addressed, for slot p);
 //  - fragment reads for the next 16-wide k step are issued before the MFMAs
@@ -85,67 +85,88 @@ __device__ __forceinline__ void dma16(const void *src, LDS uint4 *dst)
     __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src) : "memory");
 }
 
-// K-contiguous operand tile: ROWS x 64, rows of eight 16-byte chunks.
-// Load instruction q of wave w fills chunk slots (w NQ + q) 64 .. + 63.
-template <int ROWS, int NT>
+// K-contiguous operand tile: ROWS x KB (KB = 64 or 32), rows of KB / 8
+// 16-byte chunks.  Load instruction q of wave w fills chunk slots
+// (w NQ + q) 64 .. + 63.  Chunks are XOR-swizzled within a row so the 16
+// lanes of each ds_read_b128 pass hit 16 different bank groups: by
+// (r ^ r >> 3) & 7 for 8-chunk rows, by (r >> 2) & 3 for 4-chunk rows (four
+// 64-byte rows share a 256-byte bank window).
+template <int ROWS, int NT, int KB>
 struct TileK {
-    static constexpr int NQ = ROWS * 8 / NT;
-    static_assert(ROWS * 8 % NT == 0, "tile slots must divide by the thread count");
-    __device__ __forceinline__ static int swz(int chunk, int row) { return chunk ^ ((row ^ (row >> 3)) & 7); }
+    static constexpr int CH = KB / 8;
+    static constexpr int NQ = ROWS * CH / NT;
+    static_assert(ROWS * CH % NT == 0, "tile slots must divide by the thread count");
+    static_assert(KB == 64 || KB == 32, "k depth");
+    __device__ __forceinline__ static int swz(int chunk, int row)
+    {
+        return CH == 8 ? chunk ^ ((row ^ (row >> 3)) & 7) : chunk ^ ((row >> 2) & 3);
+    }
 
     // rows past `extent` are clamped to its last row (their results are
     // never stored); 1 <= extent
+    __device__ __forceinline__ static void load_q(int q, const uint16_t *__restrict__ p, size_t ld, int row0,
+                                                  int extent, int k0, LDS uint4 *dst, int tid)
+    {
+        const int lane = tid & 63, wave = tid >> 6;
+        const int base = (wave * NQ + q) * 64;
+        const int slot = base + lane;
+        const int row = slot / CH;
+        const int logical = swz(slot % CH, row);
+        int gr = row0 + row;
+        gr = gr < extent ? gr : extent - 1;
+        dma16(p + (size_t)gr * ld + k0 + logical * 8, dst + base);
+    }
     __device__ __forceinline__ static void load(const uint16_t *__restrict__ p, size_t ld, int row0, int extent,
                                                 int k0, LDS uint4 *dst, int tid)
     {
-        const int lane = tid & 63, wave = tid >> 6;
 #pragma unroll
-        for (int q = 0; q < NQ; ++q) {
-            const int base = (wave * NQ + q) * 64;
-            const int slot = base + lane;
-            const int row = slot >> 3;
-            const int logical = swz(slot & 7, row);
-            int gr = row0 + row;
-            gr = gr < extent ? gr : extent - 1;
-            dma16(p + (size_t)gr * ld + k0 + logical * 8, dst + base);
-        }
+        for (int q = 0; q < NQ; ++q)
+            load_q(q, p, ld, row0, extent, k0, dst, tid);
     }
 
     // MFMA operand fragment: rows r0 + lane % 32, k = 16 s + 8 (lane / 32) .. + 7
     __device__ __forceinline__ static uint4 frag(const LDS uint4 *sm, int r0, int s, int lane)
     {
         const int r = r0 + (lane & 31);
-        const u32x4 v = ((const LDS u32x4 *)sm)[r * 8 + swz(2 * s + (lane >> 5), r)];
+        const u32x4 v = ((const LDS u32x4 *)sm)[r * CH + swz(2 * s + (lane >> 5), r)];
         return __builtin_bit_cast(uint4, v);
     }
 };
 
-// MN-contiguous operand tile: held as [64][ROWS] (k-major rows of ROWS
-// values), 16-byte chunks swizzled by 2 (k & 3) so the four k-rows one
+// MN-contiguous operand tile: held as [KB][ROWS] (k-major rows of ROWS
+// values), 16-byte chunks swizzled by 4 (k & 3) so the k-rows one
 // transposing read touches fall in distinct banks.
-template <int ROWS, int NT>
+template <int ROWS, int NT, int KB>
 struct TileMN {
     static constexpr int CPR = ROWS / 8;
-    static constexpr int NQ = BK * CPR / NT;
-    static_assert(BK * CPR % NT == 0, "tile slots must divide by the thread count");
-    __device__ __forceinline__ static int fk(int k) { return (k & 3) << 1; }
+    static constexpr int NQ = KB * CPR / NT;
+    static_assert(KB * CPR % NT == 0, "tile slots must divide by the thread count");
+    static_assert(CPR >= 16, "the swizzle permutes 16 chunks of a row");
+    // chunk swizzle of row k: the 64-byte windows of rows k = 0..3 (mod 4)
+    // land on four different quarters of the 64 banks, so the 8 rows x 64
+    // bytes one ds_read_b64_tr_b16 touches take the minimum two passes
+    __device__ __forceinline__ static int fk(int k) { return (k & 3) << 2; }
 
     // columns past `extent` are clamped to its last 8 (never stored);
     // extent % 8 == 0, extent >= 8
+    __device__ __forceinline__ static void load_q(int q, const uint16_t *__restrict__ p, size_t ld, int row0,
+                                                  int extent, int k0, LDS uint4 *dst, int tid)
+    {
+        const int lane = tid & 63, wave = tid >> 6;
+        const int base = (wave * NQ + q) * 64;
+        const int slot = base + lane;
+        const int k = slot / CPR;
+        const int logical = (slot % CPR) ^ fk(k);
+        int mn = row0 + logical * 8;
+        mn = mn < extent ? mn : extent - 8;
+        dma16(p + (size_t)(k0 + k) * ld + mn, dst + base);
+    }
     __device__ __forceinline__ static void load(const uint16_t *__restrict__ p, size_t ld, int row0, int extent,
                                                 int k0, LDS uint4 *dst, int tid)
     {
-        const int lane = tid & 63, wave = tid >> 6;
 #pragma unroll
-        for (int q = 0; q < NQ; ++q) {
-            const int base = (wave * NQ + q) * 64;
-            const int slot = base + lane;
-            const int k = slot / CPR;
-            const int logical = (slot % CPR) ^ fk(k);
-            int mn = row0 + logical * 8;
-            mn = mn < extent ? mn : extent - 8;
-            dma16(p + (size_t)(k0 + k) * ld + mn, dst + base);
-        }
+        for (int q = 0; q < NQ; ++q)
+            load_q(q, p, ld, row0, extent, k0, dst, tid);
     }
 
     // MFMA operand fragment from two ds_read_b64_tr_b16: in 16-lane group g
@@ -168,7 +189,7 @@ struct TileMN {
     }
 };
 
-template <int BM, int BN, int WGM, int WGN, bool TA, bool TB, bool F16, bool EPI>
+template <int BM, int BN, int WGM, int WGN, bool TA, bool TB, bool F16, bool EPI, int KB, int S>
 __global__ void __launch_bounds__(64 * WGM * WGN, 1)
     k_gemm16(const uint16_t *__restrict__ A, size_t lda, size_t sA, int a_extent, const uint16_t *__restrict__ B,
              size_t ldb, size_t sB, int b_extent, float *__restrict__ C, size_t ldc, size_t sC, int M, int N, int K,
@@ -177,14 +198,15 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1)
     constexpr int NT = 64 * WGM * WGN;
     constexpr int WM = BM / WGM, WN = BN / WGN;
     constexpr int FM = WM / 32, FN = WN / 32;
-    using OA = typename std::conditional<TA, TileMN<BM, NT>, TileK<BM, NT>>::type;
-    using OB = typename std::conditional<TB, TileMN<BN, NT>, TileK<BN, NT>>::type;
-    // one array per stage, so each stage index below is a compile-time
-    // choice of array
-    __shared__ uint4 smA0[BM * 8], smA1[BM * 8];
-    __shared__ uint4 smB0[BN * 8], smB1[BN * 8];
-    LDS uint4 *const A0 = (LDS uint4 *)smA0, *const A1 = (LDS uint4 *)smA1;
-    LDS uint4 *const B0 = (LDS uint4 *)smB0, *const B1 = (LDS uint4 *)smB1;
+    using OA = typename std::conditional<TA, TileMN<BM, NT, KB>, TileK<BM, NT, KB>>::type;
+    using OB = typename std::conditional<TB, TileMN<BN, NT, KB>, TileK<BN, NT, KB>>::type;
+    // S-stage ring of A and B tiles in one LDS block; the k-loop below is
+    // unrolled by S, so every stage index is a compile-time constant
+    constexpr int SA = BM * KB / 8, SB = BN * KB / 8; // uint4 per stage
+    __shared__ uint4 smem[S * (SA + SB)];
+    LDS uint4 *const lds = (LDS uint4 *)smem;
+    auto stA = [&](int st) { return lds + st * SA; };
+    auto stB = [&](int st) { return lds + S * SA + st * SB; };
 
     // tile order: XCD-aware (block ids dealt round-robin to the 8 XCDs are
     // regrouped so consecutive ids share an XCD), then 8 tile-rows at a time
@@ -215,24 +237,44 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1)
             for (int e = 0; e < 16; ++e)
                 acc[i][j][e] = 0.0f;
 
-    const int KT = K / BK;
-    OA::load(Ab, lda, m0, a_extent, 0, A0, tid);
-    OB::load(Bb, ldb, n0, b_extent, 0, B0, tid);
+    const int KT = K / KB;
+    // DMA instructions per thread per tile: the vmcnt unit of the waits
+    constexpr int LPT = OA::NQ + OB::NQ;
+#pragma unroll
+    for (int t = 0; t < S - 1; ++t) {
+        if (t < KT) {
+            OA::load(Ab, lda, m0, a_extent, t * KB, stA(t), tid);
+            OB::load(Bb, ldb, n0, b_extent, t * KB, stB(t), tid);
+        }
+    }
 
     auto step = [&](int kt, LDS uint4 *cA, LDS uint4 *cB, LDS uint4 *nA, LDS uint4 *nB) {
-        // this wave's loads of tile kt have landed; after the barrier every
-        // wave's have, and every wave is done reading tile kt-1 (the other
-        // stage).  A bare s_barrier: the fence of __syncthreads() would make
-        // the compiler drain outstanding memory operations first.  The
-        // empty asm statements keep LDS accesses from moving across it.
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        // this wave's loads of tile kt have landed (tiles kt+1 .. kt+S-2 may
+        // still be in flight); after the barrier every wave's have, and
+        // every wave is done reading the stage tile kt+S-1 goes to.  A bare
+        // s_barrier: the fence of __syncthreads() would make the compiler
+        // drain outstanding memory operations first.  The empty asm
+        // statements keep LDS accesses from moving across it.
+        if (S > 2 && kt + S - 2 < KT)
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm((S > 2 ? S - 2 : 0) * LPT));
+        else
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
         __asm__ volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
         __asm__ volatile("" ::: "memory");
-        if (kt + 1 < KT) {
-            OA::load(Ab, lda, m0, a_extent, (kt + 1) * BK, nA, tid);
-            OB::load(Bb, ldb, n0, b_extent, (kt + 1) * BK, nB, tid);
-        }
+        // the next tile's loads go out one per MFMA from the first k-step
+        // on, early enough to land before the next barrier, and never as a
+        // burst that holds every wave at the vector-memory queue while the
+        // matrix units idle
+        const bool more = kt + S - 1 < KT;
+        const int knext = (kt + S - 1) * KB;
+        constexpr int NL = OA::NQ + OB::NQ;
+        auto issue = [&](int q) {
+            if (q < OA::NQ)
+                OA::load_q(q, Ab, lda, m0, a_extent, knext, nA, tid);
+            else
+                OB::load_q(q - OA::NQ, Bb, ldb, n0, b_extent, knext, nB, tid);
+        };
         uint4 fa[2][FM], fb[2][FN];
         auto rd = [&](int s, uint4(&xa)[FM], uint4(&xb)[FN]) {
 #pragma unroll
@@ -244,21 +286,35 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1)
         };
         rd(0, fa[0], fb[0]);
 #pragma unroll
-        for (int s = 0; s < BK / 16; ++s) {
+        for (int s = 0; s < KB / 16; ++s) {
             const int cur = s & 1;
-            if (s + 1 < BK / 16)
+            if (s + 1 < KB / 16)
                 rd(s + 1, fa[cur ^ 1], fb[cur ^ 1]);
+            // keep the next step's fragment reads ahead of this step's
+            // MFMAs: left alone, the scheduler sinks each read to just
+            // before its first use and the LDS latency shows at every step
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int i = 0; i < FM; ++i)
 #pragma unroll
-                for (int j = 0; j < FN; ++j)
+                for (int j = 0; j < FN; ++j) {
                     acc[i][j] = mfma32<F16>(fa[cur][i], fb[cur][j], acc[i][j]);
+                    const int g = (s * FM + i) * FN + j;
+                    if (g < NL) {
+                        if (more)
+                            issue(g);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                }
+            __builtin_amdgcn_sched_barrier(0);
         }
     };
-    for (int kt = 0; kt < KT; kt += 2) {
-        step(kt, A0, B0, A1, B1);
-        if (kt + 1 < KT)
-            step(kt + 1, A1, B1, A0, B0);
+    for (int kt = 0; kt < KT; kt += S) {
+#pragma unroll
+        for (int u = 0; u < S; ++u) {
+            if (kt + u < KT)
+                step(kt + u, stA(u), stB(u), stA((u + S - 1) % S), stB((u + S - 1) % S));
+        }
     }
 
     // epilogue: lane holds column lane % 32 of rows (e/4)*8 + (lane/32)*4 + e%4
@@ -272,11 +328,8 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1)
         // (8-byte for 16-bit) stores.  Every index into acc stays static.
         static_assert(WN == 64, "one lane group of 16 x 4 columns per row");
         constexpr int RS = WN + 8;
-        constexpr int RPA = (BM * 8 * 16) / (32 * RS * 4); // regions per stage array
-        static_assert(RPA >= 1 && WGM * WGN <= 4 * RPA && BM == BN, "epilogue regions fit the stages");
-        const int arr = wave / RPA, slot = wave % RPA;
-        LDS char *abase = arr == 0 ? (LDS char *)A0 : arr == 1 ? (LDS char *)A1 : arr == 2 ? (LDS char *)B0 : (LDS char *)B1;
-        LDS float *reg = (LDS float *)(abase + slot * (32 * RS * 4));
+        static_assert(WGM * WGN * 32 * RS * 4 <= S * (SA + SB) * 16, "epilogue regions fit the stages");
+        LDS float *reg = (LDS float *)((LDS char *)lds + wave * (32 * RS * 4));
         const int c4 = (lane & 15) * 4;
         const int gcol = n0 + wn * WN + c4;
         float bias4[4];
@@ -488,11 +541,11 @@ struct gemm_args {
     bool small_tiles; // 128 x 128 tiles whatever the count (split-K runs)
 };
 
-template <int BM, int BN, int WGM, int WGN, bool TA, bool TB, bool F16, bool EPI>
+template <int BM, int BN, int WGM, int WGN, bool TA, bool TB, bool F16, bool EPI, int KB = 64, int S = 2>
 int launch_tile(const gemm_args &g, const pgk_epi &epi, hipStream_t s)
 {
     const int tm = (g.m + BM - 1) / BM, tn = (g.n + BN - 1) / BN;
-    hipLaunchKernelGGL((k_gemm16<BM, BN, WGM, WGN, TA, TB, F16, EPI>), dim3((unsigned)(tm * tn), 1, g.batch),
+    hipLaunchKernelGGL((k_gemm16<BM, BN, WGM, WGN, TA, TB, F16, EPI, KB, S>), dim3((unsigned)(tm * tn), 1, g.batch),
                        dim3(64 * WGM * WGN), 0, s, g.a, g.lda, g.sa, g.a_extent, g.b, g.ldb, g.sb, g.b_extent, g.c,
                        g.ldc, g.sc, g.m, g.n, g.k, g.beta, tm, tn, epi);
     return (int)hipGetLastError();
