@@ -1,6 +1,6 @@
 """Benchmark of the MI355X picograd backward path (one GPU).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only c2,c3,c1,c5]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only c2,c3,c4,c1,c5]
 
 Headline (the JSON `value`): config 2 of BASELINE.json -- the fused
 broadcasting elementwise backward of y = gelu(x + bias) * sigmoid(g),
@@ -9,9 +9,10 @@ pg_backward() over the resident graph: the fused kernel reads x, g and bias
 and writes dx, dg and dbias (the column sum over 16384 rows) in one pass.
 value = algorithmic bytes (16 B/element + 32 KiB) / measured step time.
 
-Also reported in `extra`: config 3 (bf16 dgrad + wgrad, TFLOP/s), config 1
-(the [64, 64] chain, µs per iteration of leaves + forward + backward) and
-config 5 when the MLP step is available.
+Also reported in `extra`: config 3 (bf16 dgrad + wgrad, TFLOP/s), config 4
+(ragged f16 matmul + bmm backward, TFLOP/s), config 1 (the [64, 64] chain,
+µs per iteration of leaves + forward + backward) and config 5 (the MLP
+training step, steps/s).
 
 Timing: HIP events on the library stream around K steps (after W warmup
 steps, with stream synchronisation on both sides); per-kernel durations
@@ -341,6 +342,59 @@ def cpu_c3(M=1024, K=4096, N=4096, budget_s=20.0):
     return {"value": flops / t / 1e12, "unit": "TFLOP/s", "sample": f"M={M} of 8192", "ms": t * 1e3}
 
 
+# ---------------------------------------------------------------- config 4
+
+def bench_c4(L, ev, steps, warmup):
+    """Config 4: the ragged f16 matmul backward (4097 x 1000 x 3000) and the
+    bmm backward (32 x [512,128] . [128,512]) in one step; inputs from the
+    library RNG, seed 45, in the reference's draw order."""
+    from oracle_lib import Oracle
+    from picograd_amd.capi import F16
+    log("[c4] f16 4097x1000x3000 + bmm 32x512x128x512")
+    o = Oracle()
+    o.orc_seed(45)
+    M, K, N = 4097, 1000, 3000
+    a = o.cast16(F16, o.normal(M * K, 0.0, 1.0).reshape(M, K))
+    b = o.cast16(F16, o.normal(K * N, 0.0, 1.0).reshape(K, N))
+    dc = o.normal(M * N, 0.0, 1.0).reshape(M, N)
+    sd = float(1.0 / np.sqrt(128.0))
+    q = o.cast16(F16, o.normal(32 * 512 * 128, 0.0, sd).reshape(32, 512, 128))
+    kt = o.cast16(F16, o.normal(32 * 128 * 512, 0.0, sd).reshape(32, 128, 512))
+    ds = o.normal(32 * 512 * 512, 0.0, 1.0).reshape(32, 512, 512)
+    na, nb, nq, nk = (L.var(x, dtype=F16) for x in (a, b, q, kt))
+    c = L.op("matmul", na, nb)
+    s = L.op("matmul", nq, nk)
+    # upstream grads: f16 values (the cast in the backward is then exact)
+    dc_t = L.tensor(o.cast16(F16, dc).view(np.float16).astype(np.float32))
+    ds_t = L.tensor(o.cast16(F16, ds).view(np.float16).astype(np.float32))
+    L.sync()
+
+    def step():
+        L.pg_amd_backward_from(c, dc_t)
+        L.pg_amd_backward_from(s, ds_t)
+
+    for _ in range(warmup):
+        step()
+    L.sync()
+    L.pg_amd_timer_reset()
+    L.pg_amd_timer_enable(1)
+    ev.time(step, steps)
+    L.pg_amd_timer_enable(0)
+    g_ms, g_n = timer_ms(L, T_GEMM16)
+    L.pg_amd_timer_reset()
+    ms = ev.time(step, steps)
+    for t in (dc_t, ds_t):
+        L.pg_tensor_free(t)
+    for n in (c, s, na, nb, nq, nk):
+        L.pg_node_free(n)
+    L.sync()
+    flops = 2 * 2 * M * N * K + 2 * 2 * 32 * 512 * 512 * 128
+    step_ms = ms / steps
+    return {"step_ms": step_ms, "tflops": flops / (step_ms * 1e-3) / 1e12, "flops": flops,
+            "gemm_ms_per_step": g_ms / steps, "gemm_tflops": flops / (g_ms / steps * 1e-3) / 1e12,
+            "gemm_launches_per_step": g_n / steps, "peak_frac": flops / (step_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS}
+
+
 # ---------------------------------------------------------------- config 5
 
 C5_DIMS = (1024, 4096, 4096, 4096, 10)
@@ -481,7 +535,7 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="c2,c3,c1,c5")
+    ap.add_argument("--only", default="c2,c3,c4,c1,c5")
     ap.add_argument("--calib", action="store_true",
                     help="first run a plain copy kernel of known size (the HBM counter calibration)")
     ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 counter passes")
@@ -512,6 +566,9 @@ def main(argv=None):
     if "c3" in only:
         extra["c3_bf16_dgrad_wgrad"] = bench_c3(L, ev, max(3, a.steps // 2), a.warmup)
         log(f"[c3] {extra['c3_bf16_dgrad_wgrad']}")
+    if "c4" in only:
+        extra["c4_f16_ragged_and_bmm"] = bench_c4(L, ev, max(3, a.steps // 2), a.warmup)
+        log(f"[c4] {extra['c4_f16_ragged_and_bmm']}")
     if "c1" in only:
         extra["c1_chain_64x64"] = bench_c1(L)
         log(f"[c1] {extra['c1_chain_64x64']}")

@@ -22,8 +22,10 @@
 //    of the current one;
 //  - tiles are remapped so the blocks that share operand panels run on one
 //    XCD (and its L2), grouped 8 tile-rows at a time.
-// The k-loop requires K % 64 == 0: the host runs the last K % 64 columns
-// as one more launch over zero-padded copies (beta = 1).
+// A partial last k-tile loads zeros past K: its out-of-range chunks (K % 8
+// == 0 for a K-contiguous operand) or k-rows (MN-contiguous) are DMA'd from
+// a 16-byte zero page.  Otherwise the host runs the last K % 64 columns as
+// one more launch over zero-padded copies (beta = 1).
 //
 // k_gemm_f32: plain LDS-tiled f32 FMA GEMM with either operand transposed,
 // for f32 matmuls (not on the bf16/f16 hot path).
@@ -85,6 +87,10 @@ __device__ __forceinline__ void dma16(const void *src, LDS uint4 *dst)
     __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src) : "memory");
 }
 
+// 16 zero bytes in global memory: the DMA source of every chunk past the
+// end of the reduction dim, so a partial last k-tile lands zero-filled
+__device__ const uint4 g_zero16 = {0u, 0u, 0u, 0u};
+
 // K-contiguous operand tile: ROWS x KB (KB = 64 or 32), rows of KB / 8
 // 16-byte chunks.  Load instruction q of wave w fills chunk slots
 // (w NQ + q) 64 .. + 63.  Chunks are XOR-swizzled within a row so the 16
@@ -104,8 +110,9 @@ struct TileK {
 
     // rows past `extent` are clamped to its last row (their results are
     // never stored); 1 <= extent
+    // chunks at k >= kend read zeros (kend % 8 == 0)
     __device__ __forceinline__ static void load_q(int q, const uint16_t *__restrict__ p, size_t ld, int row0,
-                                                  int extent, int k0, LDS uint4 *dst, int tid)
+                                                  int extent, int k0, int kend, LDS uint4 *dst, int tid)
     {
         const int lane = tid & 63, wave = tid >> 6;
         const int base = (wave * NQ + q) * 64;
@@ -114,14 +121,16 @@ struct TileK {
         const int logical = swz(slot % CH, row);
         int gr = row0 + row;
         gr = gr < extent ? gr : extent - 1;
-        dma16(p + (size_t)gr * ld + k0 + logical * 8, dst + base);
+        const int kc = k0 + logical * 8;
+        const void *src = kc < kend ? (const void *)(p + (size_t)gr * ld + kc) : (const void *)&g_zero16;
+        dma16(src, dst + base);
     }
     __device__ __forceinline__ static void load(const uint16_t *__restrict__ p, size_t ld, int row0, int extent,
-                                                int k0, LDS uint4 *dst, int tid)
+                                                int k0, int kend, LDS uint4 *dst, int tid)
     {
 #pragma unroll
         for (int q = 0; q < NQ; ++q)
-            load_q(q, p, ld, row0, extent, k0, dst, tid);
+            load_q(q, p, ld, row0, extent, k0, kend, dst, tid);
     }
 
     // MFMA operand fragment: rows r0 + lane % 32, k = 16 s + 8 (lane / 32) .. + 7
@@ -149,8 +158,9 @@ struct TileMN {
 
     // columns past `extent` are clamped to its last 8 (never stored);
     // extent % 8 == 0, extent >= 8
+    // k-rows at k >= kend read zeros
     __device__ __forceinline__ static void load_q(int q, const uint16_t *__restrict__ p, size_t ld, int row0,
-                                                  int extent, int k0, LDS uint4 *dst, int tid)
+                                                  int extent, int k0, int kend, LDS uint4 *dst, int tid)
     {
         const int lane = tid & 63, wave = tid >> 6;
         const int base = (wave * NQ + q) * 64;
@@ -159,14 +169,16 @@ struct TileMN {
         const int logical = (slot % CPR) ^ fk(k);
         int mn = row0 + logical * 8;
         mn = mn < extent ? mn : extent - 8;
-        dma16(p + (size_t)(k0 + k) * ld + mn, dst + base);
+        const void *src =
+            k0 + k < kend ? (const void *)(p + (size_t)(k0 + k) * ld + mn) : (const void *)&g_zero16;
+        dma16(src, dst + base);
     }
     __device__ __forceinline__ static void load(const uint16_t *__restrict__ p, size_t ld, int row0, int extent,
-                                                int k0, LDS uint4 *dst, int tid)
+                                                int k0, int kend, LDS uint4 *dst, int tid)
     {
 #pragma unroll
         for (int q = 0; q < NQ; ++q)
-            load_q(q, p, ld, row0, extent, k0, dst, tid);
+            load_q(q, p, ld, row0, extent, k0, kend, dst, tid);
     }
 
     // MFMA operand fragment from two ds_read_b64_tr_b16: in 16-lane group g
@@ -193,7 +205,7 @@ template <int BM, int BN, int WGM, int WGN, bool TA, bool TB, bool F16, bool EPI
 __global__ void __launch_bounds__(64 * WGM * WGN, 1)
     k_gemm16(const uint16_t *__restrict__ A, size_t lda, size_t sA, int a_extent, const uint16_t *__restrict__ B,
              size_t ldb, size_t sB, int b_extent, float *__restrict__ C, size_t ldc, size_t sC, int M, int N, int K,
-             int beta, int tiles_m, int tiles_n, pgk_epi epi)
+             int beta, int tiles_m, int tiles_n, pgk_epi epi, int k_total, int kz_step)
 {
     constexpr int NT = 64 * WGM * WGN;
     constexpr int WM = BM / WGM, WN = BN / WGN;
@@ -237,14 +249,19 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1)
             for (int e = 0; e < 16; ++e)
                 acc[i][j][e] = 0.0f;
 
-    const int KT = K / KB;
+    // valid reduction length of this batch entry: K, or for split-K slice z
+    // the rest of k_total from z * kz_step; the last partial tile reads
+    // zeros past it (kend % 8 == 0)
+    const int krem = k_total - (int)blockIdx.z * kz_step;
+    const int kend = krem < K ? krem : K;
+    const int KT = (kend + KB - 1) / KB;
     // DMA instructions per thread per tile: the vmcnt unit of the waits
     constexpr int LPT = OA::NQ + OB::NQ;
 #pragma unroll
     for (int t = 0; t < S - 1; ++t) {
         if (t < KT) {
-            OA::load(Ab, lda, m0, a_extent, t * KB, stA(t), tid);
-            OB::load(Bb, ldb, n0, b_extent, t * KB, stB(t), tid);
+            OA::load(Ab, lda, m0, a_extent, t * KB, kend, stA(t), tid);
+            OB::load(Bb, ldb, n0, b_extent, t * KB, kend, stB(t), tid);
         }
     }
 
@@ -271,9 +288,9 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1)
         constexpr int NL = OA::NQ + OB::NQ;
         auto issue = [&](int q) {
             if (q < OA::NQ)
-                OA::load_q(q, Ab, lda, m0, a_extent, knext, nA, tid);
+                OA::load_q(q, Ab, lda, m0, a_extent, knext, kend, nA, tid);
             else
-                OB::load_q(q - OA::NQ, Bb, ldb, n0, b_extent, knext, nB, tid);
+                OB::load_q(q - OA::NQ, Bb, ldb, n0, b_extent, knext, kend, nB, tid);
         };
         uint4 fa[2][FM], fb[2][FN];
         auto rd = [&](int s, uint4(&xa)[FM], uint4(&xb)[FN]) {
@@ -539,6 +556,7 @@ struct gemm_args {
     int m, n, k, beta;
     unsigned batch;
     bool small_tiles; // 128 x 128 tiles whatever the count (split-K runs)
+    int k_total, kz_step; // split-K: slice z reduces [z kz_step, min(k_total, (z+1) kz_step))
 };
 
 template <int BM, int BN, int WGM, int WGN, bool TA, bool TB, bool F16, bool EPI, int KB = 64, int S = 2>
@@ -547,7 +565,7 @@ int launch_tile(const gemm_args &g, const pgk_epi &epi, hipStream_t s)
     const int tm = (g.m + BM - 1) / BM, tn = (g.n + BN - 1) / BN;
     hipLaunchKernelGGL((k_gemm16<BM, BN, WGM, WGN, TA, TB, F16, EPI, KB, S>), dim3((unsigned)(tm * tn), 1, g.batch),
                        dim3(64 * WGM * WGN), 0, s, g.a, g.lda, g.sa, g.a_extent, g.b, g.ldb, g.sb, g.b_extent, g.c,
-                       g.ldc, g.sc, g.m, g.n, g.k, g.beta, tm, tn, epi);
+                       g.ldc, g.sc, g.m, g.n, g.k, g.beta, tm, tn, epi, g.k_total ? g.k_total : g.k, g.kz_step);
     return (int)hipGetLastError();
 }
 
@@ -586,25 +604,28 @@ int launch_any(int f16, int ta, int tb, const gemm_args &g, hipStream_t s)
 // (deterministic).  256 x 256 tiles fill the chip at one per CU, so a GEMM
 // with 128 of them is not split; 128 x 128 tiles (four waves, under half a
 // CU's registers) are split towards two per CU.  0 = not split.
-static int splitk_plan(size_t m, size_t n, size_t kmain, size_t batch)
+static int splitk_plan(size_t m, size_t n, size_t kin, size_t batch)
 {
-    if (batch != 1 || kmain < 1024)
+    if (batch != 1 || kin < 1024)
         return 0;
     const size_t big = ((m + 255) / 256) * ((n + 255) / 256);
     const size_t tiles = ((m + 127) / 128) * ((n + 127) / 128);
-    if (big >= 128 || tiles >= 512 || (tiles >= 128 && kmain < 2048))
+    if (big >= 128 || tiles >= 512 || (tiles >= 128 && kin < 2048))
         return 0;
-    const size_t chunks = kmain / BK;
-    size_t want = (512 + tiles - 1) / tiles, most = kmain / 512;
+    size_t want = (512 + tiles - 1) / tiles, most = kin / 512;
     size_t sp = want < most ? want : most;
-    while (sp > 1 && chunks % sp)
-        --sp;
     return sp > 1 ? (int)sp : 0;
 }
 
+// the k the main kernel covers: all of it when both operands are
+// MN-contiguous (a partial last k-tile reads zero rows past k) or k % 8 == 0
+// (zero chunks past k), else the 64-aligned part, the rest going through
+// zero-padded slabs in one more launch
+static size_t k_inkernel(int ta, int tb, size_t k) { return (ta && tb) || k % 8 == 0 ? k : k - k % BK; }
+
 static size_t tail_ws(int ta, int tb, size_t m, size_t n, size_t k, size_t batch)
 {
-    if (k % BK == 0)
+    if (k_inkernel(ta, tb, k) == k)
         return 0;
     const size_t ma = (m + 7) & ~(size_t)7, nb = (n + 7) & ~(size_t)7;
     const size_t a = (ta ? 64 * (ma < 8 ? 8 : ma) : 64 * m) * batch;
@@ -614,7 +635,7 @@ static size_t tail_ws(int ta, int tb, size_t m, size_t n, size_t k, size_t batch
 
 extern "C" size_t pgk_gemm16_workspace(int ta, int tb, size_t m, size_t n, size_t k, size_t batch)
 {
-    const int sp = splitk_plan(m, n, k - k % BK, batch);
+    const int sp = splitk_plan(m, n, k_inkernel(ta, tb, k), batch);
     const size_t part = sp ? (((size_t)sp * m * n * sizeof(float) + 255) & ~(size_t)255) : 0;
     return part + tail_ws(ta, tb, m, n, k, batch);
 }
@@ -640,7 +661,7 @@ extern "C" int pgk_gemm16(int dtype, int ta, int tb, size_t m, size_t n, size_t 
         return (int)hipErrorInvalidValue;
     hipStream_t st = (hipStream_t)s;
     const int f16 = dtype == 1;
-    const size_t kmain = k - k % BK, ktail = k % BK;
+    const size_t kmain = k_inkernel(ta, tb, k), ktail = k - kmain;
     const size_t mn = m * n;
     const unsigned gmn = (unsigned)((mn + 255) / 256 < 2048 ? (mn + 255) / 256 : 2048);
     if (!k) { // empty reduction: C = beta ? C : 0
@@ -665,12 +686,12 @@ extern "C" int pgk_gemm16(int dtype, int ta, int tb, size_t m, size_t n, size_t 
         return (int)hipErrorInvalidValue;
     int rc = 0;
     if (kmain && sp) {
-        // slice z covers k in [z * ks, (z + 1) * ks): operand offsets along
-        // the reduction, dense [m, n] partials
-        const size_t ks = kmain / (size_t)sp;
+        // slice z covers k in [z * ks, min(kmain, (z + 1) * ks)): operand
+        // offsets along the reduction, dense [m, n] partials
+        const size_t ks = ((kmain + sp - 1) / sp + BK - 1) / BK * BK;
         float *part = (float *)ws;
         gemm_args g = {a, lda, ta ? ks * lda : ks, (int)a_extent, b, ldb, tb ? ks * ldb : ks, (int)b_extent, part, n,
-                       m * n, (int)m, (int)n, (int)ks, 0, (unsigned)sp, true};
+                       m * n, (int)m, (int)n, (int)ks, 0, (unsigned)sp, true, (int)kmain, (int)ks};
         rc = launch_any(f16, ta, tb, g, st);
         if (rc)
             return rc;
@@ -686,8 +707,9 @@ extern "C" int pgk_gemm16(int dtype, int ta, int tb, size_t m, size_t n, size_t 
             return rc;
     }
     if (ktail) {
-        // last k-slab of each operand, zero-padded to 64 (and to a multiple
-        // of 8 columns for an MN-contiguous copy), then one more launch
+        // (k % 8 != 0) last k-slab of each operand, zero-padded to 64 (and to
+        // a multiple of 8 columns for an MN-contiguous copy), then one more
+        // launch
         const size_t ma = ta ? (((m + 7) & ~(size_t)7) < 8 ? 8 : ((m + 7) & ~(size_t)7)) : m;
         const size_t nbp = tb ? (((n + 7) & ~(size_t)7) < 8 ? 8 : ((n + 7) & ~(size_t)7)) : n;
         uint16_t *pa = (uint16_t *)((char *)ws + part_bytes);
