@@ -27,6 +27,7 @@ import argparse
 import csv
 import ctypes as C
 import json
+import math
 import os
 import shutil
 import subprocess
@@ -461,7 +462,12 @@ def bench_c5(L, ev, steps, warmup, dims=C5_DIMS, batch=C5_BATCH, fused=True):
             "sgd_ms": sgd_ms, "sgd_gbs": sgd_bytes / (sgd_ms * 1e-3) / 1e9, "sgd_bytes": sgd_bytes,
             "params": params, "fused_bwd_ms_per_step": (j_ms + f_ms) / steps,
             "act_bwd_ms_per_step": a_ms / steps,
-            "loss_first": first, "loss_last": last, "steps_run": 1 + max(0, warmup - 1) + 2 * steps + 1}
+            # the reference's mean_all makes this loss a sum over the batch, so
+            # lr 0.01 diverges within a few steps (as in the reference); a
+            # non-finite loss is reported as null to keep the line strict JSON
+            "loss_first": first if math.isfinite(first) else None,
+            "loss_last": last if math.isfinite(last) else None,
+            "steps_run": 1 + max(0, warmup - 1) + 2 * steps + 1}
 
 
 def cpu_c5(dims=C5_DIMS, batch=C5_BATCH, budget_s=25.0):
@@ -616,7 +622,7 @@ def main(argv=None):
         "cpu_baseline": cpu,
         "extra": extra,
     }
-    print(json.dumps(out), flush=True)
+    print(json.dumps(out, allow_nan=False), flush=True)
     return 0
 
 
