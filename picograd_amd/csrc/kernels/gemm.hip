@@ -255,58 +255,68 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1)
     const int krem = k_total - (int)blockIdx.z * kz_step;
     const int kend = krem < K ? krem : K;
     const int KT = (kend + KB - 1) / KB;
-    // DMA instructions per thread per tile: the vmcnt unit of the waits
-    constexpr int LPT = OA::NQ + OB::NQ;
-#pragma unroll
-    for (int t = 0; t < S - 1; ++t) {
-        if (t < KT) {
-            OA::load(Ab, lda, m0, a_extent, t * KB, kend, stA(t), tid);
-            OB::load(Bb, ldb, n0, b_extent, t * KB, kend, stB(t), tid);
-        }
-    }
-
-    auto step = [&](int kt, LDS uint4 *cA, LDS uint4 *cB, LDS uint4 *nA, LDS uint4 *nB) {
-        // this wave's loads of tile kt have landed (tiles kt+1 .. kt+S-2 may
-        // still be in flight); after the barrier every wave's have, and
-        // every wave is done reading the stage tile kt+S-1 goes to.  A bare
-        // s_barrier: the fence of __syncthreads() would make the compiler
-        // drain outstanding memory operations first.  The empty asm
-        // statements keep LDS accesses from moving across it.
-        if (S > 2 && kt + S - 2 < KT)
-            __builtin_amdgcn_s_waitcnt(vmcnt_imm((S > 2 ? S - 2 : 0) * LPT));
+    // Two-stage ring, tile t in stage t & 1.  Tiles 0 and 1 are in flight
+    // before the loop; tile t+2 is loaded while tile t+1 is computed.  The
+    // one barrier per tile sits between the fragment reads and the MFMAs of
+    // a tile's last k-step: by then every wave has read the whole stage
+    // (its last fragments are in registers), so after it the stage is
+    // refilled with tile t+2 and tile t+1's first fragments are read while
+    // the last MFMAs of tile t still run -- the matrix units do not drain at
+    // the barrier.
+    static_assert(S == 2 && (KB / 16) % 2 == 0, "two stages, an even number of k-steps per tile");
+    constexpr int LPT = OA::NQ + OB::NQ; // DMA instructions per thread per tile
+    constexpr int KS = KB / 16, NM = FM * FN;
+    auto dma = [&](int q, int t, LDS uint4 *dA, LDS uint4 *dB) {
+        if (q < OA::NQ)
+            OA::load_q(q, Ab, lda, m0, a_extent, t * KB, kend, dA, tid);
+        else
+            OB::load_q(q - OA::NQ, Bb, ldb, n0, b_extent, t * KB, kend, dB, tid);
+    };
+    // a bare s_barrier after an explicit wait on this wave's loads: the
+    // fence of __syncthreads() would drain every outstanding memory
+    // operation; the empty asm statements keep LDS accesses from moving
+    // across it
+    auto sync_tile = [&](bool newer_in_flight) {
+        if (newer_in_flight)
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(LPT));
         else
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
         __asm__ volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
         __asm__ volatile("" ::: "memory");
-        // the next tile's loads go out one per MFMA from the first k-step
-        // on, early enough to land before the next barrier, and never as a
-        // burst that holds every wave at the vector-memory queue while the
-        // matrix units idle
-        const bool more = kt + S - 1 < KT;
-        const int knext = (kt + S - 1) * KB;
-        constexpr int NL = OA::NQ + OB::NQ;
-        auto issue = [&](int q) {
-            if (q < OA::NQ)
-                OA::load_q(q, Ab, lda, m0, a_extent, knext, kend, nA, tid);
-            else
-                OB::load_q(q - OA::NQ, Bb, ldb, n0, b_extent, knext, kend, nB, tid);
-        };
-        uint4 fa[2][FM], fb[2][FN];
-        auto rd = [&](int s, uint4(&xa)[FM], uint4(&xb)[FN]) {
+    };
+    uint4 fa[2][FM], fb[2][FN];
+    auto rd = [&](const LDS uint4 *cA, const LDS uint4 *cB, int s, uint4(&xa)[FM], uint4(&xb)[FN]) {
 #pragma unroll
-            for (int i = 0; i < FM; ++i)
-                xa[i] = OA::frag(cA, wm * WM + i * 32, s, lane);
+        for (int i = 0; i < FM; ++i)
+            xa[i] = OA::frag(cA, wm * WM + i * 32, s, lane);
 #pragma unroll
-            for (int j = 0; j < FN; ++j)
-                xb[j] = OB::frag(cB, wn * WN + j * 32, s, lane);
-        };
-        rd(0, fa[0], fb[0]);
+        for (int j = 0; j < FN; ++j)
+            xb[j] = OB::frag(cB, wn * WN + j * 32, s, lane);
+    };
 #pragma unroll
-        for (int s = 0; s < KB / 16; ++s) {
+    for (int q = 0; q < LPT; ++q)
+        if (KT > 0)
+            dma(q, 0, stA(0), stB(0));
+#pragma unroll
+    for (int q = 0; q < LPT; ++q)
+        if (KT > 1)
+            dma(q, 1, stA(1), stB(1));
+    sync_tile(KT > 1);
+    rd(stA(0), stB(0), 0, fa[0], fb[0]);
+
+    // tile kt from stage (cA, cB); the other stage (oA, oB) holds tile kt+1
+    auto tile = [&](int kt, LDS uint4 *cA, LDS uint4 *cB, LDS uint4 *oA, LDS uint4 *oB) {
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
             const int cur = s & 1;
-            if (s + 1 < KB / 16)
-                rd(s + 1, fa[cur ^ 1], fb[cur ^ 1]);
+            const bool last = s == KS - 1;
+            if (!last) {
+                rd(cA, cB, s + 1, fa[cur ^ 1], fb[cur ^ 1]);
+            } else if (kt + 1 < KT) {
+                sync_tile(false);
+                rd(oA, oB, 0, fa[cur ^ 1], fb[cur ^ 1]);
+            }
             // keep the next step's fragment reads ahead of this step's
             // MFMAs: left alone, the scheduler sinks each read to just
             // before its first use and the LDS latency shows at every step
@@ -316,22 +326,25 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1)
 #pragma unroll
                 for (int j = 0; j < FN; ++j) {
                     acc[i][j] = mfma32<F16>(fa[cur][i], fb[cur][j], acc[i][j]);
-                    const int g = (s * FM + i) * FN + j;
-                    if (g < NL) {
-                        if (more)
-                            issue(g);
+                    if (last) {
+                        // tile kt+2 into the stage just freed, a few loads
+                        // per MFMA rather than one burst at the vector-memory
+                        // queue
+                        const int g = i * FN + j;
+#pragma unroll
+                        for (int q = g * LPT / NM; q < (g + 1) * LPT / NM; ++q)
+                            if (kt + 2 < KT)
+                                dma(q, kt + 2, cA, cB);
                         __builtin_amdgcn_sched_barrier(0);
                     }
                 }
             __builtin_amdgcn_sched_barrier(0);
         }
     };
-    for (int kt = 0; kt < KT; kt += S) {
-#pragma unroll
-        for (int u = 0; u < S; ++u) {
-            if (kt + u < KT)
-                step(kt + u, stA(u), stB(u), stA((u + S - 1) % S), stB((u + S - 1) % S));
-        }
+    for (int kt = 0; kt < KT; kt += 2) {
+        tile(kt, stA(0), stB(0), stA(1), stB(1));
+        if (kt + 1 < KT)
+            tile(kt + 1, stA(1), stB(1), stA(0), stB(0));
     }
 
     // epilogue: lane holds column lane % 32 of rows (e/4)*8 + (lane/32)*4 + e%4
