@@ -305,9 +305,15 @@ def bench_c3(L, ev, steps, warmup, M=8192, K=4096, N=4096):
     for n in (c, na, nw):
         L.pg_node_free(n)
     L.sync()
+    # the attainable MFMA rate on this chip: pseudo-random bf16 operands from
+    # registers, and fed from LDS as in the GEMM's inner loop
+    probe_reg, probe_lds = L.pg_amd_mfma_probe(0), L.pg_amd_mfma_probe(1)
+    gemm_tf = (flops / 2) / (kern_ms * 1e-3) / 1e12
     return {"step_ms": step_ms, "tflops": flops / (step_ms * 1e-3) / 1e12,
-            "gemm_ms": kern_ms, "gemm_tflops": (flops / 2) / (kern_ms * 1e-3) / 1e12,
-            "flops": flops, "gemm_launches": g_n}
+            "gemm_ms": kern_ms, "gemm_tflops": gemm_tf, "gemm_frac_of_2p5": gemm_tf / BF16_PEAK_TFLOPS,
+            "flops": flops, "gemm_launches": g_n,
+            "mfma_probe_tflops": {"registers": probe_reg, "lds_fed": probe_lds},
+            "gemm_frac_of_lds_fed_probe": gemm_tf / probe_lds if probe_lds > 0 else None}
 
 
 def cpu_c3(M=1024, K=4096, N=4096, budget_s=20.0):

@@ -78,6 +78,13 @@ pg_node *pg_amd_ag_linear16(pg_node *x, pg_node *w, pg_node *b, int act, pg_dtyp
 size_t pg_amd_jit_compiles(void);
 size_t pg_amd_jit_cache_hits(void);
 
+/* Attainable bf16 MFMA rate of this device in TFLOP/s (a measurement aid
+ * for rooflines): one block of eight waves per CU issues back-to-back
+ * v_mfma_f32_32x32x16_bf16 on pseudo-random bf16 operands, from registers
+ * (lds = 0) or read from LDS one k-step ahead like the GEMM (lds = 1).
+ * Waits for the stream.  Returns a negative value on failure. */
+double pg_amd_mfma_probe(int lds);
+
 /* Kernel timer: while enabled, the fused backward kernel (kind 0), its
  * reduction finisher (1), the MFMA GEMMs (2), the SGD kernel (3) and the
  * GEMM operand staging (4) are bracketed by HIP events on the library

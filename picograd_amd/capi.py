@@ -160,6 +160,7 @@ _AMD_PROTOS = {
     "pg_tensor_copy_from_host": (bo, [vp, vp]),
     "pg_tensor_empty_dtype": (vp, [ip, sz, SZP]),
     "pg_amd_timer_enable": (None, [ip]),
+    "pg_amd_mfma_probe": (C.c_double, [ip]),
     "pg_amd_timer_read": (C.c_double, [ip, C.POINTER(C.c_size_t)]),
     "pg_amd_timer_reset": (None, []),
 }

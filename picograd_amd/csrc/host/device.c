@@ -310,3 +310,36 @@ void pg_amd_timer_reset(void)
     }
     g_ntev = 0;
 }
+
+double pg_amd_mfma_probe(int lds)
+{
+    if (!pgd_ok())
+        return -1.0;
+    int dev = 0, cus = 0;
+    if (!hip_ok(hipGetDevice(&dev), "mfma probe") ||
+        !hip_ok(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev), "mfma probe") || cus < 1)
+        return -1.0;
+    /* one block of eight waves per CU; 8 x 4096 MFMAs per wave (~0.5 ms) */
+    const int blocks = cus, iters = 4096;
+    const size_t n = (size_t)blocks * 512;
+    float *sink = pgd_malloc(n * sizeof(float));
+    if (!sink)
+        return -1.0;
+    hipEvent_t a = NULL, b = NULL;
+    double tflops = -1.0;
+    if (hip_ok(hipEventCreate(&a), "mfma probe") && hip_ok(hipEventCreate(&b), "mfma probe") &&
+        pgd_check(pgk_mfma_probe(lds ? 1 : 0, sink, n, blocks, iters, g_stream), "mfma probe") &&
+        hip_ok(hipEventRecord(a, g_stream), "mfma probe") &&
+        pgd_check(pgk_mfma_probe(lds ? 1 : 0, sink, n, blocks, iters, g_stream), "mfma probe") &&
+        hip_ok(hipEventRecord(b, g_stream), "mfma probe") && hip_ok(hipEventSynchronize(b), "mfma probe")) {
+        float ms = 0.0f;
+        if (hip_ok(hipEventElapsedTime(&ms, a, b), "mfma probe") && ms > 0.0f)
+            tflops = (double)blocks * 8.0 * iters * 8.0 * 32768.0 / (ms * 1e-3) / 1e12;
+    }
+    if (a)
+        hipEventDestroy(a);
+    if (b)
+        hipEventDestroy(b);
+    pgd_free(sink, n * sizeof(float));
+    return tflops;
+}

@@ -608,7 +608,80 @@ int launch_any(int f16, int ta, int tb, const gemm_args &g, hipStream_t s)
     }
 }
 
+// ---------------------------------------------------------------- MFMA probe
+// The attainable MFMA rate of this chip, for the roofline: eight waves per
+// CU run back-to-back v_mfma_f32_32x32x16_bf16 on 4 x 2 fragment tiles,
+// either from registers (lds = 0) or read from LDS one k-step ahead as the
+// GEMM's inner loop does (lds = 1).  The operands are bf16 values of
+// magnitude 0.5 .. 2 with pseudo-random signs and mantissas: the matrix
+// units draw more power, and the chip clocks lower, on such data than on
+// constant patterns.
+__global__ void __launch_bounds__(512, 1) k_mfma_probe(float *sink, int iters, int lds)
+{
+    __shared__ uint4 sm[8192];
+    for (int i = threadIdx.x; i < 8192; i += blockDim.x) {
+        uint32_t v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            uint32_t h = (uint32_t)(i * 4 + q + 1) * 2654435761u;
+            h ^= h >> 15;
+            h *= 2246822519u;
+            h ^= h >> 13;
+            const uint32_t lo = (h & 0x7Fu) | ((h >> 9) & 1u ? 0x3F80u : 0x3F00u) | ((h & 0x100u) << 7);
+            const uint32_t hi = ((h >> 16) & 0x7Fu) | ((h >> 25) & 1u ? 0x3F80u : 0x3F00u) | ((h >> 9) & 0x8000u);
+            v[q] = lo | (hi << 16);
+        }
+        sm[i] = make_uint4(v[0], v[1], v[2], v[3]);
+    }
+    __syncthreads();
+    f32x16 acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+                acc[i][j][e] = 0.0f;
+    const int l = threadIdx.x & 63, w = threadIdx.x >> 6;
+    uint4 fa[2][4], fb[2][2];
+    auto rd = [&](int it, uint4(&xa)[4], uint4(&xb)[2]) {
+        const int base = lds ? (it & 7) * 512 : 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            xa[i] = sm[((w * 8 + i) * 64 + l + base) & 8191];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            xb[j] = sm[((w * 8 + 4 + j) * 64 + l + base) & 8191];
+    };
+    rd(0, fa[0], fb[0]);
+    rd(1, fa[1], fb[1]);
+    for (int it = 0; it < iters; it += 2) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            if (lds)
+                rd(it + u + 2, fa[u ^ 1], fb[u ^ 1]);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = mfma32<false>(fa[u][i], fb[u][j], acc[i][j]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+                sum += acc[i][j][e];
+    sink[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = sum;
+}
+
 } // namespace
+
 
 // Split-K for GEMMs with few output tiles and a long reduction (the N = 10
 // layer of an MLP and its weight grad, a weight grad with a short output
@@ -763,5 +836,13 @@ extern "C" int pgk_gemm_f32(int ta, int tb, size_t m, size_t n, size_t k, const 
     dim3 grid((unsigned)((n + FT - 1) / FT), (unsigned)((m + FT - 1) / FT), (unsigned)batch);
     hipLaunchKernelGGL(k_gemm_f32, grid, dim3(256), 0, (hipStream_t)s, ta, tb, (int)m, (int)n, (int)k, a, lda,
                        stride_a, b, ldb, stride_b, c, ldc, stride_c, beta);
+    return (int)hipGetLastError();
+}
+
+extern "C" int pgk_mfma_probe(int lds, float *sink, size_t sink_floats, int blocks, int iters, pgk_stream s)
+{
+    if (blocks < 1 || iters < 2 || (iters & 1) || sink_floats < (size_t)blocks * 512)
+        return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_mfma_probe, dim3((unsigned)blocks), dim3(512), 0, (hipStream_t)s, sink, iters, lds);
     return (int)hipGetLastError();
 }

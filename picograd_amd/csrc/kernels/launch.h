@@ -114,6 +114,11 @@ int pgk_gemm16(int dtype, int ta, int tb, size_t m, size_t n, size_t k, const ui
                float *c, size_t ldc, size_t stride_c, size_t batch, int beta, const pgk_epi *epi, void *ws,
                pgk_stream s);
 
+/* MFMA rate probe: `blocks` x 512 threads, each wave 8 x iters bf16
+ * 32x32x16 MFMAs, operands from registers (lds 0) or LDS (lds 1); sink
+ * receives blocks * 512 floats.  FLOP = blocks * 8 * iters * 8 * 32768. */
+int pgk_mfma_probe(int lds, float *sink, size_t sink_floats, int blocks, int iters, pgk_stream s);
+
 /* f32 GEMM, C (beta ? += : =) op(A) op(B); ta/tb select A^T / B^T
  * (A(i,p) = ta ? a[p*lda+i] : a[i*lda+p], same for B(p,j)). */
 int pgk_gemm_f32(int ta, int tb, size_t m, size_t n, size_t k, const float *a, size_t lda,
