@@ -32,6 +32,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <math.h>
+
 #include <type_traits>
 
 #include "convert16.h"
@@ -568,7 +570,7 @@ struct gemm_args {
     size_t ldc, sc;
     int m, n, k, beta;
     unsigned batch;
-    bool small_tiles; // 128 x 128 tiles whatever the count (split-K runs)
+    int tile;         // 2: 256 x 256 tiles, 1: 128 x 128, 0: by tile count
     int k_total, kz_step; // split-K: slice z reduces [z kz_step, min(k_total, (z+1) kz_step))
 };
 
@@ -588,7 +590,7 @@ int launch_layout(const gemm_args &g, hipStream_t s, const pgk_epi &epi = pgk_ep
     // 256 x 256 tiles (eight waves, each 128 x 64) whenever they still give
     // most CUs a tile; else 128 x 128 (four waves, each 64 x 64)
     const size_t big = (size_t)((g.m + 255) / 256) * ((g.n + 255) / 256) * g.batch;
-    if (big >= 128 && !g.small_tiles)
+    if (g.tile == 2 || (g.tile == 0 && big >= 128))
         return launch_tile<256, 256, 2, 4, TA, TB, F16, EPI>(g, epi, s);
     return launch_tile<128, 128, 2, 2, TA, TB, F16, EPI>(g, epi, s);
 }
@@ -683,24 +685,46 @@ __global__ void __launch_bounds__(512, 1) k_mfma_probe(float *sink, int iters, i
 } // namespace
 
 
-// Split-K for GEMMs with few output tiles and a long reduction (the N = 10
-// layer of an MLP and its weight grad, a weight grad with a short output
-// dim): `splits` slices of the 64-aligned part of k run as a batch into
-// dense partials, then k_splitk_sum adds them in slice order into C
-// (deterministic).  256 x 256 tiles fill the chip at one per CU, so a GEMM
-// with 128 of them is not split; 128 x 128 tiles (four waves, under half a
-// CU's registers) are split towards two per CU.  0 = not split.
-static int splitk_plan(size_t m, size_t n, size_t kin, size_t batch)
+// Launch plan of one GEMM: the tile (256 x 256 with eight waves, or
+// 128 x 128 with four) and a split-K factor, from a small cost model of
+// this chip.  A launch takes ceil(blocks / 256 CUs) rounds of one block's
+// time, that block running at the per-CU rate measured for its tile
+// (~4.4 and ~2.6 TFLOP/s); split-K (slices of the reduction run as a
+// batch into dense partials that k_splitk_sum adds in slice order, so the
+// result is deterministic) adds a pass over sp + 1 copies of C at ~5 TB/s.
+// Ragged shapes such as M = 4097 (33 rows of 128-tiles) and weight grads
+// with a short output dim are where it matters.
+typedef struct {
+    int tile; // 2 = 256 x 256, 1 = 128 x 128
+    int sp;   // split-K factor, 1 = none
+} gemm_plan;
+
+static gemm_plan plan_gemm(size_t m, size_t n, size_t kin, size_t batch)
 {
-    if (batch != 1 || kin < 1024)
-        return 0;
-    const size_t big = ((m + 255) / 256) * ((n + 255) / 256);
-    const size_t tiles = ((m + 127) / 128) * ((n + 127) / 128);
-    if (big >= 128 || tiles >= 512 || (tiles >= 128 && kin < 2048))
-        return 0;
-    size_t want = (512 + tiles - 1) / tiles, most = kin / 512;
-    size_t sp = want < most ? want : most;
-    return sp > 1 ? (int)sp : 0;
+    const double cus = 256.0, rate[3] = {0.0, 2.6e12, 4.4e12}, bw = 5.0e12;
+    gemm_plan best = {2, 1};
+    double best_t = 1e300;
+    for (int tile = 2; tile >= 1; --tile) {
+        const size_t bm = tile == 2 ? 256 : 128;
+        const size_t tiles = ((m + bm - 1) / bm) * ((n + bm - 1) / bm) * batch;
+        const int max_sp = batch == 1 && kin >= 1024 ? 8 : 1;
+        for (int sp = 1; sp <= max_sp; ++sp) {
+            const size_t ks = ((kin + sp - 1) / sp + BK - 1) / BK * BK;
+            if (sp > 1 && ks * (size_t)(sp - 1) >= kin)
+                break; // the last slice would be empty
+            const double rounds = ceil((double)(tiles * sp) / cus);
+            double t = rounds * 2.0 * (double)bm * (double)bm * (double)(sp > 1 ? ks : kin) / rate[tile];
+            if (sp > 1)
+                t += (double)(sp + 1) * (double)m * (double)n * 4.0 / bw;
+            // a split must win clearly: its partials also cost HBM capacity
+            if (t < best_t * (sp > 1 ? 0.92 : 1.0)) {
+                best_t = t;
+                best.tile = tile;
+                best.sp = sp;
+            }
+        }
+    }
+    return best;
 }
 
 // the k the main kernel covers: all of it when both operands are
@@ -721,8 +745,8 @@ static size_t tail_ws(int ta, int tb, size_t m, size_t n, size_t k, size_t batch
 
 extern "C" size_t pgk_gemm16_workspace(int ta, int tb, size_t m, size_t n, size_t k, size_t batch)
 {
-    const int sp = splitk_plan(m, n, k_inkernel(ta, tb, k), batch);
-    const size_t part = sp ? (((size_t)sp * m * n * sizeof(float) + 255) & ~(size_t)255) : 0;
+    const gemm_plan pl = plan_gemm(m, n, k_inkernel(ta, tb, k), batch);
+    const size_t part = pl.sp > 1 ? (((size_t)pl.sp * m * n * sizeof(float) + 255) & ~(size_t)255) : 0;
     return part + tail_ws(ta, tb, m, n, k, batch);
 }
 
@@ -758,12 +782,13 @@ extern "C" int pgk_gemm16(int dtype, int ta, int tb, size_t m, size_t n, size_t 
             hipLaunchKernelGGL(k_bias_act, dim3(gmn), dim3(256), 0, st, c, ldc, (int)m, (int)n, *epi);
         return (int)hipGetLastError();
     }
-    const int sp = splitk_plan(m, n, kmain, batch);
+    const gemm_plan pl = plan_gemm(m, n, kmain, batch);
+    const int sp = pl.sp > 1 ? pl.sp : 0;
     // the epilogue rides on the GEMM when one launch of the forward layout
     // finishes C; otherwise it is a pass over C afterwards
     if (has_epi && !sp && !ktail && !ta && tb) {
         gemm_args g = {a, lda, stride_a, (int)a_extent, b, ldb, stride_b, (int)b_extent, c, ldc, stride_c,
-                       (int)m, (int)n, (int)kmain, 0, 1u};
+                       (int)m, (int)n, (int)kmain, 0, 1u, pl.tile};
         return f16 ? launch_layout<false, true, true, true>(g, st, *epi)
                    : launch_layout<false, true, false, true>(g, st, *epi);
     }
@@ -777,7 +802,7 @@ extern "C" int pgk_gemm16(int dtype, int ta, int tb, size_t m, size_t n, size_t 
         const size_t ks = ((kmain + sp - 1) / sp + BK - 1) / BK * BK;
         float *part = (float *)ws;
         gemm_args g = {a, lda, ta ? ks * lda : ks, (int)a_extent, b, ldb, tb ? ks * ldb : ks, (int)b_extent, part, n,
-                       m * n, (int)m, (int)n, (int)ks, 0, (unsigned)sp, true, (int)kmain, (int)ks};
+                       m * n, (int)m, (int)n, (int)ks, 0, (unsigned)sp, pl.tile, (int)kmain, (int)ks};
         rc = launch_any(f16, ta, tb, g, st);
         if (rc)
             return rc;
@@ -787,7 +812,7 @@ extern "C" int pgk_gemm16(int dtype, int ta, int tb, size_t m, size_t n, size_t 
             return rc;
     } else if (kmain) {
         gemm_args g = {a, lda, stride_a, (int)a_extent, b, ldb, stride_b, (int)b_extent, c, ldc, stride_c,
-                       (int)m, (int)n, (int)kmain, beta, (unsigned)batch};
+                       (int)m, (int)n, (int)kmain, beta, (unsigned)batch, pl.tile};
         rc = launch_any(f16, ta, tb, g, st);
         if (rc)
             return rc;
