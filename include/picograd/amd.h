@@ -51,6 +51,13 @@ void pg_amd_backward_from(pg_node *root, const pg_tensor *seed);
  * (ops/matmul.c:191) and has no cast op, so it has no counterpart. */
 pg_node *pg_amd_ag_matmul16(pg_node *a, pg_node *b, pg_dtype dtype);
 
+/* Tells the library that t's device elements were written behind its back
+ * (through t->dev by pg_gemm/pg_gemm_ex or the caller's own kernels), so a
+ * kept 16-bit copy is remade before its next use.  Writes through the
+ * library's own calls (ops, pg_tensor_fill/copy_from/copy_from_host/
+ * sync_device, pg_jit_run outputs, pg_sgd_step) are tracked already. */
+void pg_amd_tensor_modified(pg_tensor *t);
+
 /* Activation codes of pg_amd_ag_linear16: the reference's PG_ACT_* values
  * (backend/cpu/gemm.h:37-39). */
 #ifndef PG_ACT_NONE

@@ -152,6 +152,7 @@ _AMD_PROTOS = {
     "pg_amd_backward_from": (None, [vp, vp]),
     "pg_amd_ag_matmul16": (vp, [vp, vp, ip]),
     "pg_amd_ag_linear16": (vp, [vp, vp, vp, ip, ip]),
+    "pg_amd_tensor_modified": (None, [vp]),
     "pg_amd_jit_compiles": (sz, []),
     "pg_amd_jit_cache_hits": (sz, []),
     "pg_tensor_sync_host": (bo, [vp]),

@@ -256,6 +256,8 @@ void pgt_touch(pg_tensor *t)
         t->data_ref->shadow_stale = true;
 }
 
+void pg_amd_tensor_modified(pg_tensor *t) { pgt_touch(t); }
+
 const uint16_t *pgt_shadow16(pg_tensor *t, pg_dtype dt)
 {
     if (!t || !t->data_ref || t->dtype != PG_DTYPE_F32 || (dt != PG_DTYPE_F16 && dt != PG_DTYPE_BF16)) {

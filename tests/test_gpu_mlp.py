@@ -73,7 +73,8 @@ def test_matmul16_rejects_bad_input(lib):
 
 def test_matmul16_kept_copy_follows_writes(lib, oracle):
     """The 16-bit copy of an operand is remade after writes to its tensor
-    (fill, copy from host) and rewritten by pg_sgd_step: with A = I the
+    (fill, copy from host, a JIT output, a raw write reported with
+    pg_amd_tensor_modified) and rewritten by pg_sgd_step: with A = I the
     product returns q(B) exactly."""
     from picograd_amd.capi import SgdCfg
     K = 64
@@ -107,6 +108,32 @@ def test_matmul16_kept_copy_follows_writes(lib, oracle):
     w2 = lib.value(w)
     assert not np.array_equal(w2, w1)
     assert np.array_equal(qw(), _round(oracle, BF16, w2))
+    # a fused-JIT kernel writing the tensor as an output
+    g = lib.pg_jit_graph_new()
+    shp = (C.c_size_t * 2)(K, K)
+    xin = lib.pg_jit_add_input(g, 2, shp)
+    y = lib.pg_jit_mul(g, xin, lib.pg_jit_add_const(g, 2.0))
+    lib.pg_jit_mark_output(g, y)
+    exe = lib.pg_jit_compile(g)
+    assert exe, lib.pg_jit_last_error()
+    src = lib.tensor(w0)
+    ins = (C.c_void_p * 1)(src)
+    outs = (C.c_void_p * 1)(wt)
+    assert lib.pg_jit_run(exe, ins, 1, outs, 1), lib.pg_jit_last_error()
+    assert np.array_equal(qw(), _round(oracle, BF16, 2 * w0))
+    lib.pg_jit_exe_free(exe)
+    lib.pg_jit_graph_free(g)
+    lib.pg_tensor_free(src)
+    # a raw-pointer write (pg_gemm_ex into the tensor's storage), reported
+    # with pg_amd_tensor_modified
+    a16 = oracle.cast16(BF16, np.eye(K, dtype=np.float32))
+    b16 = oracle.cast16(BF16, w1)
+    ta, tb = lib.tensor(a16, BF16), lib.tensor(b16, BF16)
+    lib.pg_gemm_ex(BF16, K, K, K, lib.tinfo(ta).dev, K, lib.tinfo(tb).dev, K, lib.tinfo(wt).dev, K)
+    lib.pg_amd_tensor_modified(wt)
+    assert np.array_equal(qw(), _round(oracle, BF16, w1))
+    lib.pg_tensor_free(ta)
+    lib.pg_tensor_free(tb)
     lib.pg_sgd_free(opt)
     lib.pg_node_free(w)
     lib.pg_node_free(eye)
