@@ -199,12 +199,62 @@ void *pgd_scratch(int slot, size_t nbytes)
     return g_scratch[slot];
 }
 
+/* Small host-to-device copies go through a ring of pinned staging slots so
+ * that they queue without a stream sync: the source is copied into the next
+ * slot (waiting, if ever, only for that slot's previous copy), and the
+ * DMA from the slot is queued on the stream.  Larger copies go straight from
+ * pageable memory, which stages them before the call returns. */
+#define PGD_STAGE_SLOTS 64
+#define PGD_STAGE_BYTES ((size_t)256 << 10)
+static unsigned char *g_stage;
+static hipEvent_t g_stage_ev[PGD_STAGE_SLOTS];
+static bool g_stage_used[PGD_STAGE_SLOTS];
+static int g_stage_next, g_stage_state; /* 0 = not tried, 1 = ok, -1 = unavailable */
+
+static bool stage_ready(void)
+{
+    if (g_stage_state)
+        return g_stage_state > 0;
+    g_stage_state = -1;
+    if (hipHostMalloc((void **)&g_stage, PGD_STAGE_SLOTS * PGD_STAGE_BYTES, hipHostMallocDefault) != hipSuccess) {
+        (void)hipGetLastError();
+        g_stage = NULL;
+        return false;
+    }
+    for (int i = 0; i < PGD_STAGE_SLOTS; i++) {
+        if (hipEventCreateWithFlags(&g_stage_ev[i], hipEventDisableTiming) != hipSuccess) {
+            (void)hipGetLastError();
+            while (i-- > 0)
+                hipEventDestroy(g_stage_ev[i]);
+            hipHostFree(g_stage);
+            g_stage = NULL;
+            return false;
+        }
+    }
+    g_stage_state = 1;
+    return true;
+}
+
 bool pgd_h2d(void *dst, const void *src, size_t nbytes)
 {
     if (!nbytes)
         return true;
     if (!pgd_ok())
         return false;
+    if (nbytes <= PGD_STAGE_BYTES && stage_ready()) {
+        const int s = g_stage_next;
+        g_stage_next = (s + 1) % PGD_STAGE_SLOTS;
+        if (g_stage_used[s] && !hip_ok(hipEventSynchronize(g_stage_ev[s]), "hipEventSynchronize"))
+            return false;
+        unsigned char *slot = g_stage + (size_t)s * PGD_STAGE_BYTES;
+        memcpy(slot, src, nbytes);
+        if (!hip_ok(hipMemcpyAsync(dst, slot, nbytes, hipMemcpyHostToDevice, g_stream), "hipMemcpyAsync H2D"))
+            return false;
+        g_stage_used[s] = hip_ok(hipEventRecord(g_stage_ev[s], g_stream), "hipEventRecord");
+        if (!g_stage_used[s])
+            return pgd_sync(); /* no event to wait on later: finish the copy now */
+        return true;
+    }
     /* pageable source: the copy is staged before the call returns */
     return hip_ok(hipMemcpyAsync(dst, src, nbytes, hipMemcpyHostToDevice, g_stream),
                   "hipMemcpyAsync H2D") &&
