@@ -93,9 +93,10 @@ size_t pg_amd_jit_cache_hits(void);
 double pg_amd_mfma_probe(int lds);
 
 /* Kernel timer: while enabled, the fused backward kernel (kind 0), its
- * reduction finisher (1), the MFMA GEMMs (2), the SGD kernel (3) and the
- * GEMM operand staging (4) are bracketed by HIP events on the library
- * stream.  pg_amd_timer_read waits for the stream and returns the summed
+ * reduction finisher (1), the MFMA GEMMs (2), the SGD kernel (3), the
+ * GEMM operand staging (4), the Adam kernel (5) and the gradient-clipping
+ * passes (6) are bracketed by HIP events on the library stream.
+ * pg_amd_timer_read waits for the stream and returns the summed
  * milliseconds of one kind (and the number of launches). */
 void pg_amd_timer_enable(int on);
 double pg_amd_timer_read(int kind, size_t *count);

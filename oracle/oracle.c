@@ -195,6 +195,111 @@ void orc_sgd_step(float *p, const float *g, float *buf, size_t n, float lr,
     }
 }
 
+/* ---------------- Adam / AdamW and gradient clipping ---------------- */
+
+float orc_adam_bias_correction(float beta, unsigned long long step)
+{
+    /* adam.c:121-125: 1 - beta^t in f32 through powf, floored at 1e-12 */
+    float bc = 1.0f - powf(beta, (float)step);
+    return bc < 1e-12f ? 1e-12f : bc;
+}
+
+void orc_adam_step(float *p, const float *g, float *m, float *v, float *vmax,
+                   size_t n, float lr, float beta1, float beta2, float eps,
+                   float weight_decay, bool amsgrad, bool decoupled,
+                   unsigned long long step)
+{
+    /* adam.c:157-177 in the order the reference's -O3 -ffast-math build
+     * evaluates it (its scalar remainder loop, with IEEE sqrt and divide):
+     * the moments reassociated to g + b1*(m - g) and g^2 + b2*(v - g^2),
+     * v_hat = v * (1/bc2), and lr*m_hat/(sqrt(v_hat) + eps) folded to
+     * (m*lr) / ((sqrt(v_hat) + eps) * bc1).  Its 8-wide loop replaces the
+     * square root and the quotient by x86 reciprocal estimates plus one
+     * Newton step, which this restatement does not follow. */
+    const float bc1 = orc_adam_bias_correction(beta1, step);
+    const float bc2 = orc_adam_bias_correction(beta2, step);
+    const float inv_bc2 = 1.0f / bc2;
+    for (size_t j = 0; j < n; j++) {
+        float pj = p[j];
+        float gj = g[j];
+        if (weight_decay != 0.0f) {
+            if (decoupled)
+                pj -= lr * weight_decay * pj; /* AdamW shrink first (:157-160) */
+            else
+                gj += weight_decay * pj; /* L2 joins the grad (:164-166) */
+        }
+        m[j] = gj + beta1 * (m[j] - gj);
+        float g2 = gj * gj;
+        v[j] = g2 + beta2 * (v[j] - g2);
+        float vh = v[j];
+        if (amsgrad) {
+            if (v[j] > vmax[j])
+                vmax[j] = v[j];
+            vh = vmax[j];
+        }
+        float denom = (sqrtf(vh * inv_bc2) + eps) * bc1;
+        p[j] = pj - (m[j] * lr) / denom;
+    }
+}
+
+float orc_grad_norm(float *const *g, const size_t *n, size_t count)
+{
+    /* clip.c:5-18: squares summed in f64, tensor by tensor in element
+     * order; NULL grads skipped */
+    double sum = 0.0;
+    for (size_t i = 0; i < count; i++) {
+        if (!g[i])
+            continue;
+        for (size_t j = 0; j < n[i]; j++) {
+            double x = (double)g[i][j];
+            sum += x * x;
+        }
+    }
+    return (float)sqrt(sum);
+}
+
+float orc_clip_grad_norm(float *const *g, const size_t *n, size_t count,
+                         float max_norm, float eps)
+{
+    /* clip.c:27-40 */
+    if (!g || max_norm <= 0.0f)
+        return -1.0f;
+    if (eps < 0.0f)
+        eps = 1e-6f;
+    float total = orc_grad_norm(g, n, count);
+    if (total <= max_norm)
+        return total;
+    /* clip.c:33-39 as the reference's build evaluates it: g*max_norm
+     * times the reciprocal of (total + eps) */
+    float inv = 1.0f / (total + eps);
+    for (size_t i = 0; i < count; i++) {
+        if (!g[i])
+            continue;
+        for (size_t j = 0; j < n[i]; j++)
+            g[i][j] = (g[i][j] * max_norm) * inv;
+    }
+    return total;
+}
+
+void orc_clip_grad_value(float *const *g, const size_t *n, size_t count,
+                         float clip_value)
+{
+    /* clip.c:49-61 */
+    if (!g || clip_value <= 0.0f)
+        return;
+    for (size_t i = 0; i < count; i++) {
+        if (!g[i])
+            continue;
+        for (size_t j = 0; j < n[i]; j++) {
+            float x = g[i][j];
+            if (x > clip_value)
+                g[i][j] = clip_value;
+            else if (x < -clip_value)
+                g[i][j] = -clip_value;
+        }
+    }
+}
+
 /* ---------------- GEMM with f32 accumulation ---------------- */
 
 typedef struct {

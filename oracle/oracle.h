@@ -20,6 +20,15 @@
  *   orc_chain1_backward               golden C1 grads (JIT on and off)
  *   orc_chain2_backward               golden C2 grads at a reduced shape
  *   orc_mse_grad_scale                golden mse/mean_all graphs
+ *   orc_adam_step                     golden six-step trajectories of the
+ *                                     reference (five configurations): bit
+ *                                     for bit on the elements its build
+ *                                     computes with IEEE sqrt/divide, within
+ *                                     2^-21 of the update elsewhere (its x86
+ *                                     reciprocal estimates); closed forms
+ *                                     (test_training.c:237-268)
+ *   orc_grad_norm, orc_clip_*         golden clip fixtures bit for bit;
+ *                                     closed forms
  *   orc_mlp_step                      golden two-step f32 MLP training run
  *                                     of the reference (ORC_F32); the 16-bit
  *                                     modes differ only by orc_round_f32 on
@@ -56,6 +65,31 @@ void orc_round_f32(int dtype, float *x, size_t n); /* x = f32(dtype(x)) */
 void orc_sgd_step(float *p, const float *g, float *buf, size_t n, float lr,
                   float momentum, float dampening, float weight_decay,
                   bool nesterov);
+
+/*
+ * Adam / AdamW (adam.c:113-181): one step over one parameter tensor.  `step`
+ * is the optimiser's counter after its increment (1 on the first step); m, v
+ * (and vmax when amsgrad) start at zero.  lr and weight_decay are the values
+ * in force for this tensor (the per-parameter overrides of :136-138 already
+ * resolved by the caller).  Evaluated in the order the reference's
+ * -ffast-math build uses: m = g + b1*(m - g), v = g^2 + b2*(v - g^2),
+ * p -= (m*lr) / ((sqrt(v * (1/bc2)) + eps) * bc1), IEEE sqrt and divide.
+ */
+float orc_adam_bias_correction(float beta, unsigned long long step);
+void orc_adam_step(float *p, const float *g, float *m, float *v, float *vmax,
+                   size_t n, float lr, float beta1, float beta2, float eps,
+                   float weight_decay, bool amsgrad, bool decoupled,
+                   unsigned long long step);
+
+/* Gradient clipping over `count` grads g[i] of n[i] elements (NULL skipped):
+ * global L2 norm (clip.c:5-18), clip by norm (:27-40, returns the norm
+ * before clipping, -1 on bad arguments; scaled as (g*max_norm) *
+ * (1/(norm + eps)), the reference build's order), clip by value (:49-61). */
+float orc_grad_norm(float *const *g, const size_t *n, size_t count);
+float orc_clip_grad_norm(float *const *g, const size_t *n, size_t count,
+                         float max_norm, float eps);
+void orc_clip_grad_value(float *const *g, const size_t *n, size_t count,
+                         float clip_value);
 
 /*
  * C[i,j] (+)= sum_p A(i,p) * B(p,j), every product formed from f32 values

@@ -57,6 +57,11 @@ class SgdCfg(C.Structure):
                 ("weight_decay", C.c_float), ("nesterov", C.c_bool)]
 
 
+class AdamCfg(C.Structure):
+    _fields_ = [("lr", C.c_float), ("beta1", C.c_float), ("beta2", C.c_float), ("eps", C.c_float),
+                ("weight_decay", C.c_float), ("amsgrad", C.c_bool), ("decoupled_wd", C.c_bool)]
+
+
 vp, sz, fl, bo, ip = C.c_void_p, C.c_size_t, C.c_float, C.c_bool, C.c_int
 SZP = C.POINTER(C.c_size_t)
 
@@ -107,6 +112,25 @@ _PROTOS = {
     "pg_sgd_num_params": (sz, [vp]),
     "pg_sgd_zero_grad": (None, [vp]),
     "pg_sgd_step": (None, [vp]),
+    # adam.h
+    "pg_adam_cfg_default": (AdamCfg, []),
+    "pg_adam_new": (vp, [C.POINTER(AdamCfg)]),
+    "pg_adam_free": (None, [vp]),
+    "pg_adam_add_param": (ip, [vp, vp]),
+    "pg_adam_add_param_lr": (ip, [vp, vp, fl, fl]),
+    "pg_adam_num_params": (sz, [vp]),
+    "pg_adam_set_lr": (None, [vp, fl]),
+    "pg_adam_get_lr": (fl, [vp]),
+    "pg_adam_set_param_lr": (None, [vp, sz, fl]),
+    "pg_adam_set_param_wd": (None, [vp, sz, fl]),
+    "pg_adam_zero_grad": (None, [vp]),
+    "pg_adam_step": (None, [vp]),
+    "pg_adam_set_step": (None, [vp, C.c_ulonglong]),
+    "pg_adam_get_step": (C.c_ulonglong, [vp]),
+    # clip.h
+    "pg_clip_grad_norm": (fl, [C.POINTER(vp), sz, fl, fl]),
+    "pg_clip_grad_value": (None, [C.POINTER(vp), sz, fl]),
+    "pg_grad_norm": (fl, [C.POINTER(vp), sz]),
     # backend.h
     "pg_gemm": (None, [sz, sz, sz, vp, sz, vp, sz, vp, sz]),
     "pg_gemm_ex": (None, [ip, sz, sz, sz, vp, sz, vp, sz, vp, sz]),

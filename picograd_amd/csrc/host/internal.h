@@ -34,9 +34,12 @@ bool pgd_check(int status, const char *what);
 /* a scratch device buffer of at least nbytes, reused across calls on the
  * stream (grows, never shrinks) */
 void *pgd_scratch(int slot, size_t nbytes);
-#define PGD_SCRATCH_SLOTS 4
+#define PGD_SCRATCH_SLOTS 5
 /* kernel timer (pg_amd_timer_*): kinds and bracket calls */
-enum { PGD_T_JIT_MAIN = 0, PGD_T_JIT_FIN = 1, PGD_T_GEMM16 = 2, PGD_T_SGD = 3, PGD_T_STAGE = 4 };
+enum {
+    PGD_T_JIT_MAIN = 0, PGD_T_JIT_FIN = 1, PGD_T_GEMM16 = 2, PGD_T_SGD = 3, PGD_T_STAGE = 4,
+    PGD_T_ADAM = 5, PGD_T_CLIP = 6
+};
 int pgd_tbegin(int kind);
 void pgd_tend(int slot);
 

@@ -146,6 +146,46 @@ typedef struct {
 int pgk_sgd_multi(const pgk_sgd_seg *segs, int nseg, float lr, float momentum, float dampening,
                   float weight_decay, int nesterov, pgk_stream s);
 
+/* multi-tensor Adam / AdamW (optim.hip) */
+typedef struct {
+    float *p;
+    const float *g;
+    float *m, *v;
+    float *vmax;      /* amsgrad only, else NULL */
+    uint16_t *shadow; /* optional 16-bit copy of p written after the update */
+    int shadow_dtype; /* 1 = f16, 2 = bf16 (RNE) */
+    float lr, wd;     /* this tensor's learning rate and weight decay */
+    size_t n;
+} pgk_adam_seg;
+typedef struct {
+    float beta1, beta2, eps;
+    float bc1;     /* 1 - beta1^t, floored at 1e-12 */
+    float inv_bc2; /* 1 / (1 - beta2^t), the floor applied before the division */
+    int amsgrad, decoupled;
+} pgk_adam_hyper;
+int pgk_adam_multi(const pgk_adam_seg *segs, int nseg, const pgk_adam_hyper *h, pgk_stream s);
+
+/* gradient clipping over a list of f32 grads (optim.hip) */
+typedef struct {
+    float *g;
+    size_t n;
+} pgk_grad_seg;
+/* bytes of workspace pgk_grad_norm needs for these grads */
+size_t pgk_grad_norm_workspace(const pgk_grad_seg *segs, int nseg);
+/* res[0] = (float)sqrt(sum of squares in f64), the grads added in list
+ * order and each in a fixed block order.  With clip set, also
+ * res[1] = 1 / (res[0] + eps), res[2] = 1 unless res[0] <= max_norm (else 0)
+ * and res[3] = max_norm.  res is 4 floats of device memory. */
+int pgk_grad_norm(const pgk_grad_seg *segs, int nseg, int clip, float max_norm, float eps, float *res,
+                  void *ws, pgk_stream s);
+/* g = (g * res[3]) * res[1] for every grad when res[2] is 1 (the
+ * device-side decision pgk_grad_norm took); a tensor must not appear twice
+ * in one call */
+int pgk_grad_scale(const pgk_grad_seg *segs, int nseg, const float *res, pgk_stream s);
+/* g = min(max(g, -c), c) elementwise (NaN kept); a tensor must not
+ * appear twice in one call */
+int pgk_clip_value(const pgk_grad_seg *segs, int nseg, float c, pgk_stream s);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,427 @@
+// Multi-tensor optimizer and gradient-clipping kernels for gfx950.
+//
+// One launch covers up to a table's worth of tensors.  Every tensor is cut
+// into fixed chunks (one block each) and `first[i]` is the first block of
+// tensor i, so the grid is the sum of the chunk counts: a 10-element bias
+// costs one block, not a whole row of idle ones, and the large weights keep
+// every CU busy.  A block finds its tensor by a scan of `first` (uniform,
+// scalar) and moves 16 bytes per lane per access.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "launch.h"
+#include "convert16.h"
+
+namespace {
+
+constexpr int kBlock = 256;
+
+inline int status() { return (int)hipGetLastError(); }
+
+// tensor index of block b: first[0] = 0 <= b < first[cnt]
+__device__ __forceinline__ int seg_of(const unsigned *first, int cnt, unsigned b)
+{
+    int s = 0;
+    for (int i = 1; i < cnt; ++i)
+        s += b >= first[i] ? 1 : 0;
+    return s;
+}
+
+// ---------------------------------------------------------------- Adam
+// adam.c:157-177 per element, in the order the reference's -O3 -ffast-math
+// build evaluates it: decay (AdamW shrink or L2 grad term), moments
+// reassociated to g + b1*(m - g) and g^2 + b2*(v - g^2), amsgrad's running
+// max of v, then p -= (m*lr) / ((sqrt(v * (1/bc2)) + eps) * bc1).  Every
+// product and sum is rounded on its own (no FMA, as in that x86 build);
+// sqrtf and / are IEEE (correctly rounded), as in its remainder loop.
+constexpr int kAdamVec = 2; // float4 per lane per block
+constexpr size_t kAdamChunk = (size_t)kBlock * 4 * kAdamVec;
+#define PGK_ADAM_MAX_SEG 32
+
+struct adam_table {
+    pgk_adam_seg seg[PGK_ADAM_MAX_SEG];
+    unsigned first[PGK_ADAM_MAX_SEG + 1];
+    int cnt;
+};
+
+__device__ __forceinline__ void adam_elem(float &p, float g, float &m, float &v, float &vm, bool ams,
+                                          const pgk_adam_hyper &h, float lr, float wd)
+{
+#pragma clang fp contract(off)
+    float pj = p, gj = g;
+    if (wd != 0.0f) {
+        if (h.decoupled)
+            pj = pj - lr * wd * pj;
+        else
+            gj = gj + wd * pj;
+    }
+    m = gj + h.beta1 * (m - gj);
+    const float g2 = gj * gj;
+    v = g2 + h.beta2 * (v - g2);
+    float vh = v;
+    if (ams) {
+        if (v > vm)
+            vm = v;
+        vh = vm;
+    }
+    const float denom = (sqrtf(vh * h.inv_bc2) + h.eps) * h.bc1;
+    p = pj - (m * lr) / denom;
+}
+
+__global__ void __launch_bounds__(kBlock) k_adam(adam_table tab, pgk_adam_hyper h)
+{
+    const unsigned b = blockIdx.x;
+    const int si = seg_of(tab.first, tab.cnt, b);
+    const pgk_adam_seg sg = tab.seg[si];
+    const size_t base = (size_t)(b - tab.first[si]) * kAdamChunk;
+    const size_t n = sg.n;
+    const bool ams = sg.vmax != nullptr;
+    float *__restrict__ P = sg.p;
+    const float *__restrict__ G = sg.g;
+    float *__restrict__ M = sg.m;
+    float *__restrict__ V = sg.v;
+    float *__restrict__ VM = sg.vmax;
+    const bool vec = ((((uintptr_t)P) | ((uintptr_t)G) | ((uintptr_t)M) | ((uintptr_t)V) | ((uintptr_t)VM)) & 15) == 0 &&
+                     (((uintptr_t)sg.shadow) & 7) == 0;
+    if (vec) {
+        float4 p[kAdamVec], g[kAdamVec], m[kAdamVec], v[kAdamVec], vm[kAdamVec];
+        size_t e[kAdamVec];
+#pragma unroll
+        for (int k = 0; k < kAdamVec; ++k) {
+            e[k] = base + 4 * ((size_t)threadIdx.x + (size_t)k * kBlock);
+            if (e[k] + 4 <= n) {
+                p[k] = *reinterpret_cast<const float4 *>(P + e[k]);
+                g[k] = *reinterpret_cast<const float4 *>(G + e[k]);
+                m[k] = *reinterpret_cast<const float4 *>(M + e[k]);
+                v[k] = *reinterpret_cast<const float4 *>(V + e[k]);
+                vm[k] = ams ? *reinterpret_cast<const float4 *>(VM + e[k]) : make_float4(0, 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < kAdamVec; ++k) {
+            if (e[k] + 4 <= n) {
+                adam_elem(p[k].x, g[k].x, m[k].x, v[k].x, vm[k].x, ams, h, sg.lr, sg.wd);
+                adam_elem(p[k].y, g[k].y, m[k].y, v[k].y, vm[k].y, ams, h, sg.lr, sg.wd);
+                adam_elem(p[k].z, g[k].z, m[k].z, v[k].z, vm[k].z, ams, h, sg.lr, sg.wd);
+                adam_elem(p[k].w, g[k].w, m[k].w, v[k].w, vm[k].w, ams, h, sg.lr, sg.wd);
+                *reinterpret_cast<float4 *>(P + e[k]) = p[k];
+                *reinterpret_cast<float4 *>(M + e[k]) = m[k];
+                *reinterpret_cast<float4 *>(V + e[k]) = v[k];
+                if (ams)
+                    *reinterpret_cast<float4 *>(VM + e[k]) = vm[k];
+                if (sg.shadow) {
+                    ushort4 o;
+                    o.x = to16(sg.shadow_dtype, p[k].x);
+                    o.y = to16(sg.shadow_dtype, p[k].y);
+                    o.z = to16(sg.shadow_dtype, p[k].z);
+                    o.w = to16(sg.shadow_dtype, p[k].w);
+                    *reinterpret_cast<ushort4 *>(sg.shadow + e[k]) = o;
+                }
+            } else {
+                for (size_t j = e[k]; j < n; ++j) { // the last 1-3 elements
+                    float pj = P[j], mj = M[j], vj = V[j], vmj = ams ? VM[j] : 0.0f;
+                    adam_elem(pj, G[j], mj, vj, vmj, ams, h, sg.lr, sg.wd);
+                    P[j] = pj, M[j] = mj, V[j] = vj;
+                    if (ams)
+                        VM[j] = vmj;
+                    if (sg.shadow)
+                        sg.shadow[j] = to16(sg.shadow_dtype, pj);
+                }
+            }
+        }
+    } else {
+        const size_t end = base + kAdamChunk < n ? base + kAdamChunk : n;
+        for (size_t j = base + threadIdx.x; j < end; j += kBlock) {
+            float pj = P[j], mj = M[j], vj = V[j], vmj = ams ? VM[j] : 0.0f;
+            adam_elem(pj, G[j], mj, vj, vmj, ams, h, sg.lr, sg.wd);
+            P[j] = pj, M[j] = mj, V[j] = vj;
+            if (ams)
+                VM[j] = vmj;
+            if (sg.shadow)
+                sg.shadow[j] = to16(sg.shadow_dtype, pj);
+        }
+    }
+}
+
+// ---------------------------------------------------------------- grad norm
+// clip.c:5-18 sums the squares in f64.  Each block adds the squares of its
+// chunk in f64 (lanes in a fixed order) into part[block]; k_norm_fin adds
+// the parts in block order, so the result does not depend on timing.
+constexpr int kNormVec = 4;
+constexpr size_t kNormChunk = (size_t)kBlock * 4 * kNormVec;
+#define PGK_GRAD_MAX_SEG 64
+
+struct grad_table {
+    pgk_grad_seg seg[PGK_GRAD_MAX_SEG];
+    unsigned first[PGK_GRAD_MAX_SEG + 1];
+    int cnt;
+};
+
+__device__ __forceinline__ double block_sum_f64(double x, double *sh)
+{
+    for (int o = 32; o > 0; o >>= 1)
+        x += __shfl_xor(x, o);
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (lane == 0)
+        sh[w] = x;
+    __syncthreads();
+    double t = 0.0;
+    if (threadIdx.x == 0)
+        for (int i = 0; i < kBlock / 64; ++i)
+            t += sh[i];
+    return t;
+}
+
+__global__ void __launch_bounds__(kBlock) k_sumsq(grad_table tab, double *__restrict__ part)
+{
+    __shared__ double sh[kBlock / 64];
+    const unsigned b = blockIdx.x;
+    const int si = seg_of(tab.first, tab.cnt, b);
+    const pgk_grad_seg sg = tab.seg[si];
+    const size_t base = (size_t)(b - tab.first[si]) * kNormChunk;
+    const size_t n = sg.n;
+    const float *__restrict__ G = sg.g;
+    double acc = 0.0;
+    if ((((uintptr_t)G) & 15) == 0) {
+        float4 g[kNormVec];
+        size_t e[kNormVec];
+#pragma unroll
+        for (int k = 0; k < kNormVec; ++k) {
+            e[k] = base + 4 * ((size_t)threadIdx.x + (size_t)k * kBlock);
+            g[k] = e[k] + 4 <= n ? *reinterpret_cast<const float4 *>(G + e[k]) : make_float4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int k = 0; k < kNormVec; ++k) {
+            if (e[k] + 4 > n)
+                for (size_t j = e[k]; j < n; ++j) {
+                    const double x = G[j];
+                    acc += x * x;
+                }
+            const double x0 = g[k].x, x1 = g[k].y, x2 = g[k].z, x3 = g[k].w;
+            acc += x0 * x0;
+            acc += x1 * x1;
+            acc += x2 * x2;
+            acc += x3 * x3;
+        }
+    } else {
+        const size_t end = base + kNormChunk < n ? base + kNormChunk : n;
+        for (size_t j = base + threadIdx.x; j < end; j += kBlock) {
+            const double x = G[j];
+            acc += x * x;
+        }
+    }
+    const double t = block_sum_f64(acc, sh);
+    if (threadIdx.x == 0)
+        part[b] = t;
+}
+
+__global__ void __launch_bounds__(kBlock) k_norm_fin(const double *__restrict__ part, unsigned nparts, int clip,
+                                                     float max_norm, float eps, float *__restrict__ res)
+{
+    __shared__ double sh[kBlock];
+    double x = 0.0;
+    for (unsigned i = threadIdx.x; i < nparts; i += kBlock)
+        x += part[i];
+    sh[threadIdx.x] = x;
+    __syncthreads();
+    for (int s = kBlock / 2; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s)
+            sh[threadIdx.x] += sh[threadIdx.x + s];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        const float total = (float)sqrt(sh[0]);
+        res[0] = total;
+        if (clip) {
+            // clip.c:32-33: nothing happens when total <= max_norm; the
+            // scale is applied as (g * max_norm) * (1 / (total + eps)), the
+            // order the reference's build uses
+            res[1] = 1.0f / (total + eps);
+            res[2] = total <= max_norm ? 0.0f : 1.0f;
+            res[3] = max_norm;
+        }
+    }
+}
+
+// g = (g * res[3]) * res[1] when res[2] is set (clip.c:34-39); every block
+// reads the flag the finisher wrote, so no host round trip sits between the
+// two passes.
+__device__ __forceinline__ float scale_elem(float g, float mx, float inv)
+{
+    return (g * mx) * inv;
+}
+
+__global__ void __launch_bounds__(kBlock) k_grad_scale(grad_table tab, const float *__restrict__ res)
+{
+    if (res[2] == 0.0f)
+        return;
+    const float inv = res[1], mx = res[3];
+    const unsigned b = blockIdx.x;
+    const int si = seg_of(tab.first, tab.cnt, b);
+    const pgk_grad_seg sg = tab.seg[si];
+    const size_t base = (size_t)(b - tab.first[si]) * kNormChunk;
+    const size_t n = sg.n;
+    float *__restrict__ G = sg.g;
+    if ((((uintptr_t)G) & 15) == 0) {
+#pragma unroll
+        for (int k = 0; k < kNormVec; ++k) {
+            const size_t e = base + 4 * ((size_t)threadIdx.x + (size_t)k * kBlock);
+            if (e + 4 <= n) {
+                float4 g = *reinterpret_cast<const float4 *>(G + e);
+                g.x = scale_elem(g.x, mx, inv), g.y = scale_elem(g.y, mx, inv);
+                g.z = scale_elem(g.z, mx, inv), g.w = scale_elem(g.w, mx, inv);
+                *reinterpret_cast<float4 *>(G + e) = g;
+            } else {
+                for (size_t j = e; j < n; ++j)
+                    G[j] = scale_elem(G[j], mx, inv);
+            }
+        }
+    } else {
+        const size_t end = base + kNormChunk < n ? base + kNormChunk : n;
+        for (size_t j = base + threadIdx.x; j < end; j += kBlock)
+            G[j] = scale_elem(G[j], mx, inv);
+    }
+}
+
+// clip.c:49-61: values above c become c, below -c become -c
+__device__ __forceinline__ float clamp_c(float x, float c)
+{
+    return x > c ? c : (x < -c ? -c : x);
+}
+
+__global__ void __launch_bounds__(kBlock) k_grad_clamp(grad_table tab, float c)
+{
+    const unsigned b = blockIdx.x;
+    const int si = seg_of(tab.first, tab.cnt, b);
+    const pgk_grad_seg sg = tab.seg[si];
+    const size_t base = (size_t)(b - tab.first[si]) * kNormChunk;
+    const size_t n = sg.n;
+    float *__restrict__ G = sg.g;
+    if ((((uintptr_t)G) & 15) == 0) {
+#pragma unroll
+        for (int k = 0; k < kNormVec; ++k) {
+            const size_t e = base + 4 * ((size_t)threadIdx.x + (size_t)k * kBlock);
+            if (e + 4 <= n) {
+                float4 g = *reinterpret_cast<const float4 *>(G + e);
+                g.x = clamp_c(g.x, c), g.y = clamp_c(g.y, c), g.z = clamp_c(g.z, c), g.w = clamp_c(g.w, c);
+                *reinterpret_cast<float4 *>(G + e) = g;
+            } else {
+                for (size_t j = e; j < n; ++j)
+                    G[j] = clamp_c(G[j], c);
+            }
+        }
+    } else {
+        const size_t end = base + kNormChunk < n ? base + kNormChunk : n;
+        for (size_t j = base + threadIdx.x; j < end; j += kBlock)
+            G[j] = clamp_c(G[j], c);
+    }
+}
+
+// fills a grad table with segs[0..cnt) and their block prefix; returns the
+// block count (0 when every tensor is empty)
+unsigned grad_table_fill(grad_table &tab, const pgk_grad_seg *segs, int cnt)
+{
+    tab = {};
+    unsigned blocks = 0;
+    for (int q = 0; q < cnt; ++q) {
+        tab.seg[q] = segs[q];
+        tab.first[q] = blocks;
+        blocks += (unsigned)((segs[q].n + kNormChunk - 1) / kNormChunk);
+    }
+    tab.first[cnt] = blocks;
+    tab.cnt = cnt;
+    return blocks;
+}
+
+size_t grad_blocks(const pgk_grad_seg *segs, int nseg)
+{
+    size_t blocks = 0;
+    for (int q = 0; q < nseg; ++q)
+        blocks += (segs[q].n + kNormChunk - 1) / kNormChunk;
+    return blocks;
+}
+
+} // namespace
+
+extern "C" int pgk_adam_multi(const pgk_adam_seg *segs, int nseg, const pgk_adam_hyper *h, pgk_stream s)
+{
+    for (int base = 0; base < nseg; base += PGK_ADAM_MAX_SEG) {
+        const int cnt = nseg - base < PGK_ADAM_MAX_SEG ? nseg - base : PGK_ADAM_MAX_SEG;
+        adam_table tab = {};
+        unsigned blocks = 0;
+        for (int q = 0; q < cnt; ++q) {
+            tab.seg[q] = segs[base + q];
+            tab.first[q] = blocks;
+            blocks += (unsigned)((segs[base + q].n + kAdamChunk - 1) / kAdamChunk);
+        }
+        tab.first[cnt] = blocks;
+        tab.cnt = cnt;
+        if (!blocks)
+            continue;
+        hipLaunchKernelGGL(k_adam, dim3(blocks), dim3(kBlock), 0, (hipStream_t)s, tab, *h);
+        const int st = status();
+        if (st)
+            return st;
+    }
+    return 0;
+}
+
+extern "C" size_t pgk_grad_norm_workspace(const pgk_grad_seg *segs, int nseg)
+{
+    const size_t b = grad_blocks(segs, nseg);
+    return (b ? b : 1) * sizeof(double);
+}
+
+extern "C" int pgk_grad_norm(const pgk_grad_seg *segs, int nseg, int clip, float max_norm, float eps, float *res,
+                             void *ws, pgk_stream s)
+{
+    double *part = (double *)ws;
+    unsigned off = 0;
+    for (int base = 0; base < nseg; base += PGK_GRAD_MAX_SEG) {
+        const int cnt = nseg - base < PGK_GRAD_MAX_SEG ? nseg - base : PGK_GRAD_MAX_SEG;
+        grad_table tab;
+        const unsigned blocks = grad_table_fill(tab, segs + base, cnt);
+        if (!blocks)
+            continue;
+        hipLaunchKernelGGL(k_sumsq, dim3(blocks), dim3(kBlock), 0, (hipStream_t)s, tab, part + off);
+        off += blocks;
+        const int st = status();
+        if (st)
+            return st;
+    }
+    hipLaunchKernelGGL(k_norm_fin, dim3(1), dim3(kBlock), 0, (hipStream_t)s, (const double *)part, off, clip,
+                       max_norm, eps, res);
+    return status();
+}
+
+extern "C" int pgk_grad_scale(const pgk_grad_seg *segs, int nseg, const float *res, pgk_stream s)
+{
+    for (int base = 0; base < nseg; base += PGK_GRAD_MAX_SEG) {
+        const int cnt = nseg - base < PGK_GRAD_MAX_SEG ? nseg - base : PGK_GRAD_MAX_SEG;
+        grad_table tab;
+        const unsigned blocks = grad_table_fill(tab, segs + base, cnt);
+        if (!blocks)
+            continue;
+        hipLaunchKernelGGL(k_grad_scale, dim3(blocks), dim3(kBlock), 0, (hipStream_t)s, tab, res);
+        const int st = status();
+        if (st)
+            return st;
+    }
+    return 0;
+}
+
+extern "C" int pgk_clip_value(const pgk_grad_seg *segs, int nseg, float c, pgk_stream s)
+{
+    for (int base = 0; base < nseg; base += PGK_GRAD_MAX_SEG) {
+        const int cnt = nseg - base < PGK_GRAD_MAX_SEG ? nseg - base : PGK_GRAD_MAX_SEG;
+        grad_table tab;
+        const unsigned blocks = grad_table_fill(tab, segs + base, cnt);
+        if (!blocks)
+            continue;
+        hipLaunchKernelGGL(k_grad_clamp, dim3(blocks), dim3(kBlock), 0, (hipStream_t)s, tab, c);
+        const int st = status();
+        if (st)
+            return st;
+    }
+    return 0;
+}

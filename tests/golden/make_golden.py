@@ -27,7 +27,7 @@ sys.path.insert(0, str(ROOT))
 sys.path.insert(0, str(ROOT / "tests"))
 
 from oracle_lib import REF_CONVERT_SO, REF_SO  # noqa: E402
-from picograd_amd.capi import BF16, F16, F32, PgLib, SgdCfg, shape_arg  # noqa: E402
+from picograd_amd.capi import BF16, F16, F32, AdamCfg, PgLib, SgdCfg, shape_arg  # noqa: E402
 
 
 def ref_lib() -> PgLib:
@@ -352,6 +352,142 @@ def mlp(R: PgLib) -> dict:
     return out
 
 
+# (lr, beta1, beta2, eps, weight_decay, amsgrad, decoupled_wd), the second
+# parameter's (lr, wd) override for pg_adam_add_param_lr, and the step
+# counter set before the first step (pg_adam_set_step; 0 = untouched)
+ADAM_CFGS = [
+    ((1e-3, 0.9, 0.999, 1e-8, 0.0, False, True), (0.0, -1.0), 0),
+    ((0.01, 0.9, 0.999, 1e-8, 0.01, False, True), (0.003, 0.0), 0),
+    ((0.02, 0.85, 0.99, 1e-6, 0.05, False, False), (0.0, 0.2), 100),
+    ((0.005, 0.9, 0.99, 1e-8, 0.01, True, True), (0.02, -1.0), 0),
+    ((0.01, 0.5, 0.9, 1e-3, 0.1, True, False), (0.0, -1.0), 0),
+]
+ADAM_STEPS = 6
+ADAM_SKIP = 3  # the step at which the second parameter has no grad
+
+
+def adam_trajectories(R: PgLib) -> dict:
+    """pg_adam_step (opt/adam.c:113-181): two parameters per configuration,
+    one registered with per-parameter overrides (adam.c:136-138), six steps
+    with grads set exactly through loss = sum_all(p0 * G0) + sum_all(p1 * G1);
+    at step ADAM_SKIP the second parameter is left out of the loss, so it has
+    no grad and is skipped while the step counter still advances.  Grads mix
+    normal values, exact zeros and a few large entries."""
+    rng = np.random.default_rng(17)
+    out = {"cfgs": np.array([c + o + (s,) for c, o, s in ADAM_CFGS], np.float64)}
+    for ci, (cfg, (lr1, wd1), step0) in enumerate(ADAM_CFGS):
+        p0 = rng.standard_normal(257).astype(np.float32)
+        p1 = rng.standard_normal((5, 7)).astype(np.float32)
+        g0 = rng.standard_normal((ADAM_STEPS, 257)).astype(np.float32)
+        g1 = rng.standard_normal((ADAM_STEPS, 5, 7)).astype(np.float32)
+        g0[:, ::13] = 0.0
+        g0[:, 5::37] *= 100.0
+        g1[:, 0, :] *= 0.01
+        n0, n1 = R.var(p0), R.var(p1)
+        opt = R.pg_adam_new(C.byref(AdamCfg(*cfg)))
+        R.pg_adam_add_param(opt, n0)
+        R.pg_adam_add_param_lr(opt, n1, lr1, wd1)
+        if step0:
+            R.pg_adam_set_step(opt, step0)
+        t0, t1 = [], []
+        for s in range(ADAM_STEPS):
+            R.pg_adam_zero_grad(opt)
+            a = R.var(g0[s], requires_grad=False)
+            pa = R.op("mul", n0, a)
+            la = R.op("sum_all", pa)
+            made = [la, pa, a]
+            loss = la
+            if s != ADAM_SKIP:
+                b = R.var(g1[s], requires_grad=False)
+                pb = R.op("mul", n1, b)
+                lb = R.op("sum_all", pb)
+                loss = R.op("add", la, lb)
+                made = [loss, lb, pb, b] + made
+            R.pg_backward(loss)
+            _free(R, *made)
+            R.pg_adam_step(opt)
+            t0.append(R.value(n0))
+            t1.append(R.value(n1))
+        out[f"final_step_{ci}"] = np.array(R.pg_adam_get_step(opt), np.int64)
+        R.pg_adam_free(opt)
+        _free(R, n0, n1)
+        out.update({f"p0_{ci}": p0, f"p1_{ci}": p1, f"g0_{ci}": g0, f"g1_{ci}": g1,
+                    f"traj0_{ci}": np.stack(t0), f"traj1_{ci}": np.stack(t1)})
+    return out
+
+
+def _params(nodes):
+    return (C.c_void_p * len(nodes))(*[n if n else None for n in nodes])
+
+
+def clip(R: PgLib) -> dict:
+    """pg_grad_norm / pg_clip_grad_norm / pg_clip_grad_value (opt/clip.c):
+    three grads (set exactly through sum_all(p * G)), a NULL entry and a node
+    without a grad in the list; the norm, clipping below and above the norm,
+    the default eps (eps < 0), a grad listed twice, value clipping, and the
+    norm of one large grad (f64 accumulation)."""
+    rng = np.random.default_rng(23)
+    shapes = [(100,), (6, 7), (1,)]
+    out = {}
+
+    def setup(gs, scale=1.0):
+        ps = [R.var(rng.standard_normal(sh).astype(np.float32)) for sh in shapes]
+        terms, made = [], []
+        for p, g in zip(ps, gs):
+            gn = R.var(g, requires_grad=False)
+            pr = R.op("mul", p, gn)
+            sm = R.op("sum_all", pr)
+            made += [sm, pr, gn]
+            terms.append(sm)
+        loss = terms[0]
+        for t in terms[1:]:
+            loss = R.op("add", loss, t)
+            made.insert(0, loss)
+        R.pg_backward(loss)
+        _free(R, *made)
+        return ps
+
+    for case in range(5):
+        gs = [(rng.standard_normal(sh) * (1 + 3 * case)).astype(np.float32) for sh in shapes]
+        for i, g in enumerate(gs):
+            out[f"g{i}_{case}"] = g
+        ps = setup(gs)
+        nograd = R.var(np.ones(3, np.float32))
+        lst = [ps[0], None, ps[1], nograd, ps[2]]
+        if case == 0:
+            out["norm_0"] = np.float32(R.pg_grad_norm(_params(lst), len(lst)))
+        elif case == 1:  # clip below the norm
+            n = R.pg_grad_norm(_params(lst), len(lst))
+            out["max_norm_1"] = np.float32(0.5 * n)
+            out["ret_1"] = np.float32(R.pg_clip_grad_norm(_params(lst), len(lst), out["max_norm_1"], 1e-6))
+        elif case == 2:  # above the norm: untouched; then default eps
+            n = R.pg_grad_norm(_params(lst), len(lst))
+            out["max_norm_2a"] = np.float32(2.0 * n)
+            out["ret_2a"] = np.float32(R.pg_clip_grad_norm(_params(lst), len(lst), out["max_norm_2a"], 1e-6))
+            out["max_norm_2b"] = np.float32(0.25 * n)
+            out["ret_2b"] = np.float32(R.pg_clip_grad_norm(_params(lst), len(lst), out["max_norm_2b"], -1.0))
+        elif case == 3:  # a grad listed twice
+            lst = [ps[0], ps[0], ps[1]]
+            out["max_norm_3"] = np.float32(1.0)
+            out["ret_3"] = np.float32(R.pg_clip_grad_norm(_params(lst), len(lst), 1.0, 1e-6))
+        else:  # value clipping
+            out["clip_value_4"] = np.float32(2.5)
+            R.pg_clip_grad_value(_params(lst), len(lst), 2.5)
+        for i, p in enumerate(ps):
+            out[f"after{i}_{case}"] = R.grad(p)
+        _free(R, nograd, *ps)
+    big = (10.0 * rng.standard_normal(30011)).astype(np.float32)
+    out["big_g"] = big
+    (pb,) = [R.var(np.zeros_like(big))]
+    gn = R.var(big, requires_grad=False)
+    pr = R.op("mul", pb, gn)
+    sm = R.op("sum_all", pr)
+    R.pg_backward(sm)
+    out["big_norm"] = np.float32(R.pg_grad_norm(_params([pb]), 1))
+    _free(R, sm, pr, gn, pb)
+    return out
+
+
 CASES = {
     "rng": rng_streams,
     "convert": lambda R: conversions(),
@@ -362,6 +498,8 @@ CASES = {
     "matmul_bwd": matmul_backward,
     "mse": mse,
     "mlp": mlp,
+    "adam": adam_trajectories,
+    "clip": clip,
 }
 
 

@@ -34,6 +34,12 @@ class Oracle:
             "orc_cast_f32": (None, [_ip, _vp, _vp, _sz]),
             "orc_round_f32": (None, [_ip, _vp, _sz]),
             "orc_sgd_step": (None, [_vp, _vp, _vp, _sz, _fl, _fl, _fl, _fl, C.c_bool]),
+            "orc_adam_bias_correction": (_fl, [_fl, C.c_ulonglong]),
+            "orc_adam_step": (None, [_vp, _vp, _vp, _vp, _vp, _sz, _fl, _fl, _fl, _fl, _fl, C.c_bool, C.c_bool,
+                                     C.c_ulonglong]),
+            "orc_grad_norm": (_fl, [C.POINTER(_vp), C.POINTER(_sz), _sz]),
+            "orc_clip_grad_norm": (_fl, [C.POINTER(_vp), C.POINTER(_sz), _sz, _fl, _fl]),
+            "orc_clip_grad_value": (None, [C.POINTER(_vp), C.POINTER(_sz), _sz, _fl]),
             "orc_gemm_acc32": (None, [_ip, _ip, _ip, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _ip, _ip]),
             "orc_gemm_acc64": (None, [_ip, _ip, _ip, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _ip]),
             "orc_chain1_backward": (None, [_vp, _vp, _vp, _sz, _vp, _vp, _vp]),
@@ -88,6 +94,35 @@ class Oracle:
     def sgd_step(self, p, g, buf, lr, mu, damp, wd, nesterov) -> None:
         self.orc_sgd_step(p.ctypes.data, g.ctypes.data, buf.ctypes.data if buf is not None else None,
                           p.size, lr, mu, damp, wd, nesterov)
+
+    def adam_step(self, p, g, m, v, vmax, lr, beta1, beta2, eps, wd, amsgrad, decoupled, step) -> None:
+        """One orc_adam_step over f32 arrays, in place (vmax may be None unless amsgrad)."""
+        for a in (p, g, m, v) + ((vmax,) if vmax is not None else ()):
+            assert a.dtype == np.float32 and a.flags.c_contiguous and a.size == p.size
+        self.orc_adam_step(p.ctypes.data, g.ctypes.data, m.ctypes.data, v.ctypes.data,
+                           vmax.ctypes.data if vmax is not None else None, p.size, lr, beta1, beta2, eps, wd,
+                           bool(amsgrad), bool(decoupled), int(step))
+
+    @staticmethod
+    def _grad_list(gs):
+        for g in gs:
+            assert g is None or (g.dtype == np.float32 and g.flags.c_contiguous)
+        ptrs = (C.c_void_p * len(gs))(*[g.ctypes.data if g is not None else None for g in gs])
+        ns = (C.c_size_t * len(gs))(*[g.size if g is not None else 0 for g in gs])
+        return ptrs, ns
+
+    def grad_norm(self, gs) -> float:
+        ptrs, ns = self._grad_list(gs)
+        return self.orc_grad_norm(ptrs, ns, len(gs))
+
+    def clip_grad_norm(self, gs, max_norm, eps) -> float:
+        """In place over the arrays of gs (None entries skipped); returns the norm."""
+        ptrs, ns = self._grad_list(gs)
+        return self.orc_clip_grad_norm(ptrs, ns, len(gs), max_norm, eps)
+
+    def clip_grad_value(self, gs, c) -> None:
+        ptrs, ns = self._grad_list(gs)
+        self.orc_clip_grad_value(ptrs, ns, len(gs), c)
 
     def chain1(self, a, b, c):
         da, db, dc = (np.empty_like(a) for _ in range(3))

@@ -148,6 +148,219 @@ def test_sgd_planted_mistake_is_caught():
     assert np.abs(wrong - g["traj_0"][0]).max() > 1e-5
 
 
+# ---------------------------------------------------------------- Adam
+
+# The reference's 8-wide loop takes sqrt and the quotient through x86
+# reciprocal estimates plus one Newton step; its remainder loop (the last
+# n % 8 elements of a tensor) uses IEEE sqrt and division, as the oracle does.
+ADAM_UPDATE_TOL = 2.0 ** -21  # relative to the update, beyond one ulp of the weight
+ADAM_SKIP = 3  # tests/golden/make_golden.py: the second parameter has no grad at this step
+
+
+def _adam_cfg(g, ci):
+    lr, b1, b2, eps, wd, ams, dec, lr1, wd1, step0 = (float(x) for x in g["cfgs"][ci])
+    lrs = [lr, lr1 if lr1 > 0 else lr]  # adam.c:136-138
+    wds = [wd, wd1 if wd1 >= 0 else wd]
+    return lrs, wds, b1, b2, eps, bool(ams), bool(dec), int(step0)
+
+
+def _adam_stepwise(oracle, g, ci, step_fn=None):
+    """Runs configuration ci, each step starting from the reference's
+    weights of the previous step (the moments are the run's own).  Returns
+    the worst update error beyond one ulp of the weight, relative to the
+    reference's update, and whether every remainder-loop element matched
+    bit for bit."""
+    lrs, wds, b1, b2, eps, ams, dec, step = _adam_cfg(g, ci)
+    prev = [g[f"p0_{ci}"].reshape(-1).copy(), g[f"p1_{ci}"].reshape(-1).copy()]
+    mom = [[np.zeros(p.size, np.float32) for _ in range(3)] for p in prev]
+    worst, tails = 0.0, True
+    for s in range(6):
+        step += 1
+        for k in range(2):
+            ref = g[f"traj{k}_{ci}"][s].reshape(-1)
+            if k == 1 and s == ADAM_SKIP:
+                assert np.array_equal(ref, prev[k]), "a parameter without a grad must not move"
+                continue
+            p = prev[k].copy()
+            gr = g[f"g{k}_{ci}"][s].reshape(-1).astype(np.float32)
+            m, v, vm = mom[k]
+            (step_fn or oracle.adam_step)(p, gr, m, v, vm if ams else None, lrs[k], b1, b2, eps, wds[k], ams,
+                                          dec, step)
+            r = ref.astype(np.float64)
+            u = np.abs(prev[k].astype(np.float64) - r)
+            beyond = np.maximum(np.abs(p.astype(np.float64) - r) - np.spacing(np.abs(ref)), 0.0)
+            worst = max(worst, float((beyond / np.maximum(u, 1e-30)).max()))
+            t = ref.size - ref.size % 8
+            tails &= bool(np.array_equal(p[t:].view(np.uint32), ref[t:].view(np.uint32)))
+            prev[k] = ref.copy()
+    assert step == int(g[f"final_step_{ci}"])
+    return worst, tails
+
+
+@pytest.mark.parametrize("ci", range(5))
+def test_adam_matches_reference(oracle, ci):
+    """Six steps of pg_adam_step (adam.c:113-181) per configuration: Adam
+    with L2 decay, AdamW, amsgrad, per-parameter lr / wd overrides, a
+    parameter without a grad (skipped while the step counter advances) and
+    a counter set by pg_adam_set_step.  Step by step from the reference's
+    weights, the elements its build computes with IEEE arithmetic match bit
+    for bit and the rest within one ulp plus 2^-21 of the update; run freely
+    for six steps the weights stay within 2^-23 * max(1, |p|) * 2."""
+    g = golden("adam")
+    worst, tails = _adam_stepwise(oracle, g, ci)
+    assert tails and worst <= ADAM_UPDATE_TOL, (tails, worst)
+    lrs, wds, b1, b2, eps, ams, dec, step = _adam_cfg(g, ci)
+    ps = [g[f"p0_{ci}"].reshape(-1).copy(), g[f"p1_{ci}"].reshape(-1).copy()]
+    mom = [[np.zeros(p.size, np.float32) for _ in range(3)] for p in ps]
+    for s in range(6):
+        step += 1
+        for k in range(2):
+            if k == 1 and s == ADAM_SKIP:
+                continue
+            m, v, vm = mom[k]
+            oracle.adam_step(ps[k], g[f"g{k}_{ci}"][s].reshape(-1).astype(np.float32), m, v,
+                             vm if ams else None, lrs[k], b1, b2, eps, wds[k], ams, dec, step)
+    for k in range(2):
+        ref = g[f"traj{k}_{ci}"][5].reshape(-1)
+        assert np.all(np.abs(ps[k] - ref) <= 2.0 ** -22 * np.maximum(1.0, np.abs(ref))), k
+
+
+def test_adam_source_order_misses_reference(oracle):
+    """Why the oracle follows the build's evaluation order: adam.c:167-176
+    evaluated as written (b2*v + (1 - b2)*g*g, m / bc1, v / bc2) leaves the
+    reference's weights by up to ~4e-5 of the update at beta2 = 0.999 (the
+    reassociated v = g^2 + b2*(v - g^2) cancels), far outside the band."""
+    f = np.float32
+    g = golden("adam")
+
+    def as_written(p, gr, m, v, vm, lr, b1, b2, eps, wd, ams, dec, step):
+        bc1 = max(f(1) - np.power(f(b1), f(step)), f(1e-12))
+        bc2 = max(f(1) - np.power(f(b2), f(step)), f(1e-12))
+        if wd != 0 and dec:
+            p[:] = p - f(lr) * f(wd) * p
+        if wd != 0 and not dec:
+            gr = gr + f(wd) * p
+        m[:] = f(b1) * m + (f(1) - f(b1)) * gr
+        v[:] = f(b2) * v + (f(1) - f(b2)) * gr * gr
+        vv = v
+        if ams:
+            vm[:] = np.maximum(vm, v)
+            vv = vm
+        p[:] = p - f(lr) * (m / bc1) / (np.sqrt(vv / bc2) + f(eps))
+
+    worst, _ = _adam_stepwise(oracle, g, 1, as_written)
+    assert worst > 20 * ADAM_UPDATE_TOL
+
+
+def test_adam_known_answers(oracle):
+    """Closed forms.  Step 1 moves every weight with g != 0 by lr * sign(g)
+    (the bias corrections cancel the moment scales), leaves g == 0 weights
+    alone, and AdamW first shrinks by lr*wd.  test_training.c:237-268: with
+    grads of 1, a parameter with lr 0.1 moves 0.1 and one with 0.01 moves
+    0.01."""
+    p0 = np.array([1.0, -2.0, 0.5, 3.0], np.float32)
+    gr = np.array([0.3, -5.0, 0.0, 1e-3], np.float32)
+    p = p0.copy()
+    z = [np.zeros(4, np.float32) for _ in range(3)]
+    oracle.adam_step(p, gr, z[0], z[1], None, 0.01, 0.9, 0.999, 1e-8, 0.0, False, True, 1)
+    want = p0 - 0.01 * np.sign(gr)
+    assert np.allclose(p, want, rtol=0, atol=2e-6) and p[2] == p0[2]
+    p = p0.copy()
+    z = [np.zeros(4, np.float32) for _ in range(3)]
+    oracle.adam_step(p, np.zeros(4, np.float32), z[0], z[1], None, 0.1, 0.9, 0.999, 1e-8, 0.5, False, True, 1)
+    assert np.array_equal(p, p0 - np.float32(0.1 * 0.5) * p0)
+    for lr in (0.1, 0.01):
+        x = np.ones(1, np.float32)
+        z = [np.zeros(1, np.float32) for _ in range(3)]
+        oracle.adam_step(x, np.ones(1, np.float32), z[0], z[1], None, lr, 0.9, 0.999, 1e-8, 0.0, False, True, 1)
+        assert abs((1.0 - x[0]) - lr) < 1e-6
+    # amsgrad keeps the running maximum of v: a smaller second grad moves
+    # the weight less than plain Adam does
+    outs = []
+    for ams in (False, True):
+        x = np.zeros(1, np.float32)
+        m, v, vm = (np.zeros(1, np.float32) for _ in range(3))
+        for t, gv in enumerate((10.0, 0.1), start=1):
+            oracle.adam_step(x, np.array([gv], np.float32), m, v, vm, 0.01, 0.9, 0.999, 1e-8, 0.0, ams, True, t)
+        outs.append(float(x[0]))
+        if ams:
+            assert vm[0] >= v[0] > 0
+    assert abs(outs[1]) < abs(outs[0])
+
+
+def test_adam_planted_mistakes_are_caught(oracle):
+    """A bias correction one step off, L2 decay applied as AdamW, or the
+    betas swapped each leave the tolerance band."""
+    g = golden("adam")
+
+    def off_by_one(p, gr, m, v, vm, lr, b1, b2, eps, wd, ams, dec, step):
+        oracle.adam_step(p, gr, m, v, vm, lr, b1, b2, eps, wd, ams, dec, step + 1)
+
+    def decay_kind(p, gr, m, v, vm, lr, b1, b2, eps, wd, ams, dec, step):
+        oracle.adam_step(p, gr, m, v, vm, lr, b1, b2, eps, wd, ams, not dec, step)
+
+    def swapped(p, gr, m, v, vm, lr, b1, b2, eps, wd, ams, dec, step):
+        oracle.adam_step(p, gr, m, v, vm, lr, b2, b1, eps, wd, ams, dec, step)
+
+    for fn, ci in ((off_by_one, 0), (decay_kind, 2), (swapped, 3)):
+        worst, _ = _adam_stepwise(oracle, g, ci, fn)
+        assert worst > 100 * ADAM_UPDATE_TOL, fn.__name__
+
+
+# ---------------------------------------------------------------- gradient clipping
+
+def test_clip_matches_reference(oracle):
+    """pg_grad_norm / pg_clip_grad_norm / pg_clip_grad_value (clip.c:5-61):
+    the norm (f64 sum, f32 result) and every clipped grad bit for bit, with
+    NULL entries and grad-less nodes skipped, no change when the norm is
+    within max_norm, eps < 0 taken as 1e-6, and a grad listed twice counted
+    and scaled twice."""
+    g = golden("clip")
+    gs = lambda c: [g[f"g{i}_{c}"].copy() for i in range(3)]
+    with_gaps = lambda a: [a[0], None, a[1], None, a[2]]
+    bits = lambda x: np.asarray(x, np.float32).view(np.uint32)
+
+    a = gs(0)
+    assert bits(oracle.grad_norm(with_gaps(a))) == bits(g["norm_0"])
+    a = gs(1)
+    assert bits(oracle.clip_grad_norm(with_gaps(a), float(g["max_norm_1"]), 1e-6)) == bits(g["ret_1"])
+    for i in range(3):
+        assert np.array_equal(bits(a[i]), bits(g[f"after{i}_1"])), i
+    a = gs(2)
+    assert bits(oracle.clip_grad_norm(with_gaps(a), float(g["max_norm_2a"]), 1e-6)) == bits(g["ret_2a"])
+    assert bits(oracle.clip_grad_norm(with_gaps(a), float(g["max_norm_2b"]), -1.0)) == bits(g["ret_2b"])
+    for i in range(3):
+        assert np.array_equal(bits(a[i]), bits(g[f"after{i}_2"])), i
+    a = gs(3)
+    assert bits(oracle.clip_grad_norm([a[0], a[0], a[1]], 1.0, 1e-6)) == bits(g["ret_3"])
+    for i in range(3):
+        assert np.array_equal(bits(a[i]), bits(g[f"after{i}_3"])), i
+    a = gs(4)
+    oracle.clip_grad_value(with_gaps(a), float(g["clip_value_4"]))
+    for i in range(3):
+        assert np.array_equal(bits(a[i]), bits(g[f"after{i}_4"])), i
+    assert bits(oracle.grad_norm([g["big_g"].copy()])) == bits(g["big_norm"])
+    assert oracle.clip_grad_norm([a[0]], 0.0, 1e-6) == -1.0
+
+
+def test_clip_closed_forms_and_planted_mistake(oracle):
+    """The norm of a 3-4-12 vector is 13; clipping to 6.5 halves it up to
+    eps; a norm summed in f32 instead of f64 misses the reference on the
+    large fixture."""
+    v = np.array([3.0, 4.0, 12.0], np.float32)
+    assert oracle.grad_norm([v.copy()]) == 13.0
+    w = v.copy()
+    assert oracle.clip_grad_norm([w], 6.5, 0.0) == 13.0
+    assert np.array_equal(w, v * np.float32(0.5))
+    g = golden("clip")
+    big = g["big_g"]
+    f32_sum = np.float32(0)
+    for x in big:  # serial f32 accumulation
+        f32_sum = np.float32(f32_sum + x * x)
+    assert np.float32(np.sqrt(f32_sum)) != g["big_norm"]
+    assert abs(float(np.sqrt(np.sum(big.astype(np.float64) ** 2))) - float(g["big_norm"])) <= np.spacing(g["big_norm"])
+
+
 # ---------------------------------------------------------------- elementwise chains
 
 def test_chain1_matches_reference(oracle):
