@@ -1,6 +1,6 @@
 """Benchmark of the MI355X picograd backward path (one GPU).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only c2,c3,c4,c1,c5]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only c2,c3,c4,c1,c5,opt]
 
 Headline (the JSON `value`): config 2 of BASELINE.json -- the fused
 broadcasting elementwise backward of y = gelu(x + bias) * sigmoid(g),
@@ -11,8 +11,9 @@ value = algorithmic bytes (16 B/element + 32 KiB) / measured step time.
 
 Also reported in `extra`: config 3 (bf16 dgrad + wgrad, TFLOP/s), config 4
 (ragged f16 matmul + bmm backward, TFLOP/s), config 1 (the [64, 64] chain,
-µs per iteration of leaves + forward + backward) and config 5 (the MLP
-training step, steps/s).
+µs per iteration of leaves + forward + backward), config 5 (the MLP
+training step, steps/s) and the optimiser leg (AdamW + clipping by the
+global grad norm over config 5's 37.8M parameters, GB/s).
 
 Timing: HIP events on the library stream around K steps (after W warmup
 steps, with stream synchronisation on both sides); per-kernel durations
@@ -44,7 +45,7 @@ sys.path.insert(0, str(ROOT / "tests"))
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0  # dense MFMA, MI355X
-T_JIT_MAIN, T_JIT_FIN, T_GEMM16, T_SGD, T_STAGE = 0, 1, 2, 3, 4
+T_JIT_MAIN, T_JIT_FIN, T_GEMM16, T_SGD, T_STAGE, T_ADAM, T_CLIP = 0, 1, 2, 3, 4, 5, 6
 
 
 class HipEvents:
@@ -508,6 +509,107 @@ def cpu_c5(dims=C5_DIMS, batch=C5_BATCH, budget_s=25.0):
             "ms": sec * 1e3}
 
 
+# ---------------------------------------------------------------- optimiser leg
+
+ADAM_CFG = (1e-3, 0.9, 0.999, 1e-8, 0.01, False, True)  # AdamW, weight decay 0.01
+
+
+def c5_param_shapes(dims=C5_DIMS):
+    """Config 5's parameters in registration order: W [in, out], b [out]."""
+    out = []
+    for i in range(len(dims) - 1):
+        out += [(dims[i], dims[i + 1]), (dims[i + 1],)]
+    return out
+
+
+def _opt_setup(X, seed, dims):
+    """Leaves of config 5's parameter shapes with N(0, 1) grads attached
+    (node->grad assigned, as the reference's tests do), and the AdamW
+    optimiser over them."""
+    from picograd_amd.capi import AdamCfg, shape_arg
+    X.pg_seed(seed)
+    params = []
+    for shp in c5_param_shapes(dims):
+        nd, sh = shape_arg(shp)
+        p = X._check(X.pg_var_normal(nd, sh, 0.0, 0.02, True))
+        X.node(p).grad = X.pg_tensor_normal(nd, sh, 0.0, 1.0)
+        params.append(p)
+    opt = X.pg_adam_new(C.byref(AdamCfg(*ADAM_CFG)))
+    for p in params:
+        X.pg_adam_add_param(opt, p)
+    arr = (C.c_void_p * len(params))(*params)
+    return params, opt, arr
+
+
+def bench_opt(L, ev, steps, warmup, dims=C5_DIMS):
+    """One optimiser step = pg_clip_grad_norm (f64 norm pass, finisher,
+    scaling pass, one host read of the norm) + pg_adam_step (one fused
+    multi-tensor launch) over config 5's 8 parameter tensors, grads
+    resident.  max_norm is 0.9 x the norm the previous step left, so every
+    step scales.
+    Algorithmic bytes per parameter: Adam 28 (read p, g, m, v; write p, m,
+    v), clipping 12 (read g for the norm; read and write g to scale)."""
+    params, opt, arr = _opt_setup(L, 48, dims)
+    n = sum(int(np.prod(s)) for s in c5_param_shapes(dims))
+    state = {"norm": float("inf")}
+
+    def step():
+        # 0.9 x the norm the grads were left with, so every call scales
+        mx = 0.9 * state["norm"] if math.isfinite(state["norm"]) else 1e30
+        state["norm"] = min(L.pg_clip_grad_norm(arr, len(params), mx, 1e-6), mx)
+        L.pg_adam_step(opt)
+
+    first = None
+    for i in range(max(1, warmup)):
+        step()
+        first = state["norm"] if first is None else first
+    L.sync()
+    L.pg_amd_timer_reset()
+    L.pg_amd_timer_enable(1)
+    ev.time(step, steps)
+    L.pg_amd_timer_enable(0)
+    a_ms, a_n = timer_ms(L, T_ADAM)
+    c_ms, c_n = timer_ms(L, T_CLIP)
+    L.pg_amd_timer_reset()
+    ms = ev.time(step, steps)
+    L.pg_adam_free(opt)
+    for p in params:
+        L.pg_node_free(p)
+    L.sync()
+    adam_ms, clip_ms, step_ms = a_ms / max(a_n, 1), c_ms / max(c_n, 1), ms / steps
+    return {"params": n, "step_ms": step_ms, "steps_per_s": 1e3 / step_ms,
+            "step_gbs": 40 * n / (step_ms * 1e-3) / 1e9,
+            "adam_ms": adam_ms, "adam_bytes": 28 * n, "adam_gbs": 28 * n / (adam_ms * 1e-3) / 1e9,
+            "clip_ms": clip_ms, "clip_bytes": 12 * n, "clip_gbs": 12 * n / (clip_ms * 1e-3) / 1e9,
+            "norm_first": first, "norm_last": state["norm"], "optimizer": "AdamW lr 1e-3 wd 0.01 + clip"}
+
+
+def cpu_opt(dims=C5_DIMS, budget_s=15.0):
+    """The reference's CPU pg_clip_grad_norm + pg_adam_step over the same
+    parameter set (its loops are single-threaded)."""
+    from oracle_lib import REF_SO
+    from picograd_amd.capi import PgLib
+    if not REF_SO.exists():
+        return None
+    R = PgLib(REF_SO, device=False)
+    params, opt, arr = _opt_setup(R, 48, dims)
+    n = sum(int(np.prod(s)) for s in c5_param_shapes(dims))
+    norm, times = float("inf"), []
+    t0 = time.perf_counter()
+    while len(times) < 6 and time.perf_counter() - t0 < budget_s:
+        s = time.perf_counter()
+        mx = 0.9 * norm if math.isfinite(norm) else 1e30
+        norm = min(R.pg_clip_grad_norm(arr, len(params), mx, 1e-6), mx)
+        R.pg_adam_step(opt)
+        times.append(time.perf_counter() - s)
+    R.pg_adam_free(opt)
+    for p in params:
+        R.pg_node_free(p)
+    sec = float(np.median(times))
+    return {"value": 40 * n / sec / 1e9, "unit": "GB/s", "cores": 1, "kind": "reference",
+            "sample": f"{len(times)} clip + AdamW steps over config 5's {n} parameters", "ms": sec * 1e3}
+
+
 # ---------------------------------------------------------------- config 1
 
 def bench_c1(L, iters=2000):
@@ -547,7 +649,7 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="c2,c3,c4,c1,c5")
+    ap.add_argument("--only", default="c2,c3,c4,c1,c5,opt")
     ap.add_argument("--calib", action="store_true",
                     help="first run a plain copy kernel of known size (the HBM counter calibration)")
     ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 counter passes")
@@ -589,6 +691,9 @@ def main(argv=None):
         c5["unfused_graph"] = bench_c5(L, ev, max(3, a.steps // 2), a.warmup, fused=False)
         extra["c5_mlp_train_step"] = c5
         log(f"[c5] {extra['c5_mlp_train_step']}")
+    if "opt" in only:
+        extra["opt_adamw_clip_c5_params"] = bench_opt(L, ev, max(3, a.steps), a.warmup)
+        log(f"[opt] {extra['opt_adamw_clip_c5_params']}")
     cpu = None
     if not a.no_cpu:
         log("[cpu] reference CPU path, config 2 sample")
@@ -603,6 +708,11 @@ def main(argv=None):
             c5cpu = cpu_c5()
             if c5cpu:
                 extra.setdefault("c5_mlp_train_step", {})["cpu_reference"] = c5cpu
+        if "opt" in only and cpu is not None:
+            log("[cpu] reference CPU path, clip + AdamW over config 5's parameters")
+            ocpu = cpu_opt()
+            if ocpu:
+                extra.setdefault("opt_adamw_clip_c5_params", {})["cpu_reference"] = ocpu
     out = {
         "metric": "fused-bwd HBM GB/s",
         "value": round(c2["gbs"], 2),

@@ -146,9 +146,12 @@ __global__ void __launch_bounds__(kBlock) k_adam(adam_table tab, pgk_adam_hyper 
 // ---------------------------------------------------------------- grad norm
 // clip.c:5-18 sums the squares in f64.  Each block adds the squares of its
 // chunk in f64 (lanes in a fixed order) into part[block]; k_norm_fin adds
-// the parts in block order, so the result does not depend on timing.
-constexpr int kNormVec = 4;
-constexpr size_t kNormChunk = (size_t)kBlock * 4 * kNormVec;
+// the parts in a fixed order, so the result does not depend on timing.
+// The scaling and clamping passes map chunks of kMapChunk elements.
+constexpr int kSumVec = 8;
+constexpr size_t kSumChunk = (size_t)kBlock * 4 * kSumVec;
+constexpr int kMapVec = 4;
+constexpr size_t kMapChunk = (size_t)kBlock * 4 * kMapVec;
 #define PGK_GRAD_MAX_SEG 64
 
 struct grad_table {
@@ -178,22 +181,23 @@ __global__ void __launch_bounds__(kBlock) k_sumsq(grad_table tab, double *__rest
     const unsigned b = blockIdx.x;
     const int si = seg_of(tab.first, tab.cnt, b);
     const pgk_grad_seg sg = tab.seg[si];
-    const size_t base = (size_t)(b - tab.first[si]) * kNormChunk;
+    const size_t base = (size_t)(b - tab.first[si]) * kSumChunk;
     const size_t n = sg.n;
     const float *__restrict__ G = sg.g;
     double acc = 0.0;
     if ((((uintptr_t)G) & 15) == 0) {
-        float4 g[kNormVec];
-        size_t e[kNormVec];
+        const size_t e0 = base + 4 * (size_t)threadIdx.x;
+        float4 g[kSumVec];
 #pragma unroll
-        for (int k = 0; k < kNormVec; ++k) {
-            e[k] = base + 4 * ((size_t)threadIdx.x + (size_t)k * kBlock);
-            g[k] = e[k] + 4 <= n ? *reinterpret_cast<const float4 *>(G + e[k]) : make_float4(0, 0, 0, 0);
+        for (int k = 0; k < kSumVec; ++k) {
+            const size_t e = e0 + (size_t)k * 4 * kBlock;
+            g[k] = e + 4 <= n ? *reinterpret_cast<const float4 *>(G + e) : make_float4(0, 0, 0, 0);
         }
 #pragma unroll
-        for (int k = 0; k < kNormVec; ++k) {
-            if (e[k] + 4 > n)
-                for (size_t j = e[k]; j < n; ++j) {
+        for (int k = 0; k < kSumVec; ++k) {
+            const size_t e = e0 + (size_t)k * 4 * kBlock;
+            if (e + 4 > n)
+                for (size_t j = e; j < n; ++j) {
                     const double x = G[j];
                     acc += x * x;
                 }
@@ -204,7 +208,7 @@ __global__ void __launch_bounds__(kBlock) k_sumsq(grad_table tab, double *__rest
             acc += x3 * x3;
         }
     } else {
-        const size_t end = base + kNormChunk < n ? base + kNormChunk : n;
+        const size_t end = base + kSumChunk < n ? base + kSumChunk : n;
         for (size_t j = base + threadIdx.x; j < end; j += kBlock) {
             const double x = G[j];
             acc += x * x;
@@ -215,16 +219,30 @@ __global__ void __launch_bounds__(kBlock) k_sumsq(grad_table tab, double *__rest
         part[b] = t;
 }
 
-__global__ void __launch_bounds__(kBlock) k_norm_fin(const double *__restrict__ part, unsigned nparts, int clip,
-                                                     float max_norm, float eps, float *__restrict__ res)
+constexpr int kFinBlock = 1024;
+
+__global__ void __launch_bounds__(kFinBlock) k_norm_fin(const double *__restrict__ part, unsigned nparts, int clip,
+                                                        float max_norm, float eps, float *__restrict__ res)
 {
-    __shared__ double sh[kBlock];
+    // thread t adds parts t, t + 1024, ... (eight loads in flight), then a
+    // fixed tree over the threads: the same order on every call
+    __shared__ double sh[kFinBlock];
     double x = 0.0;
-    for (unsigned i = threadIdx.x; i < nparts; i += kBlock)
+    unsigned i = threadIdx.x;
+    for (; i + 7 * kFinBlock < nparts; i += 8 * kFinBlock) {
+        double v[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+            v[q] = part[i + q * kFinBlock];
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+            x += v[q];
+    }
+    for (; i < nparts; i += kFinBlock)
         x += part[i];
     sh[threadIdx.x] = x;
     __syncthreads();
-    for (int s = kBlock / 2; s > 0; s >>= 1) {
+    for (int s = kFinBlock / 2; s > 0; s >>= 1) {
         if ((int)threadIdx.x < s)
             sh[threadIdx.x] += sh[threadIdx.x + s];
         __syncthreads();
@@ -246,98 +264,79 @@ __global__ void __launch_bounds__(kBlock) k_norm_fin(const double *__restrict__ 
 // g = (g * res[3]) * res[1] when res[2] is set (clip.c:34-39); every block
 // reads the flag the finisher wrote, so no host round trip sits between the
 // two passes.
-__device__ __forceinline__ float scale_elem(float g, float mx, float inv)
+struct scale_op {
+    float mx, inv;
+    __device__ float operator()(float g) const { return (g * mx) * inv; }
+};
+
+// clip.c:49-61: values above c become c, below -c become -c
+struct clamp_op {
+    float c;
+    __device__ float operator()(float x) const { return x > c ? c : (x < -c ? -c : x); }
+};
+
+// g = op(g) over block b's chunk: every load of the chunk issued before the
+// first store
+template <typename Op>
+__device__ __forceinline__ void grad_map(const grad_table &tab, unsigned b, Op op)
 {
-    return (g * mx) * inv;
+    const int si = seg_of(tab.first, tab.cnt, b);
+    const pgk_grad_seg sg = tab.seg[si];
+    const size_t base = (size_t)(b - tab.first[si]) * kMapChunk;
+    const size_t n = sg.n;
+    float *__restrict__ G = sg.g;
+    if ((((uintptr_t)G) & 15) == 0) {
+        float4 g[kMapVec];
+        size_t e[kMapVec];
+#pragma unroll
+        for (int k = 0; k < kMapVec; ++k) {
+            e[k] = base + 4 * ((size_t)threadIdx.x + (size_t)k * kBlock);
+            if (e[k] + 4 <= n)
+                g[k] = *reinterpret_cast<const float4 *>(G + e[k]);
+        }
+#pragma unroll
+        for (int k = 0; k < kMapVec; ++k) {
+            if (e[k] + 4 <= n) {
+                float4 r;
+                r.x = op(g[k].x), r.y = op(g[k].y), r.z = op(g[k].z), r.w = op(g[k].w);
+                *reinterpret_cast<float4 *>(G + e[k]) = r;
+            } else {
+                for (size_t j = e[k]; j < n; ++j)
+                    G[j] = op(G[j]);
+            }
+        }
+    } else {
+        const size_t end = base + kMapChunk < n ? base + kMapChunk : n;
+        for (size_t j = base + threadIdx.x; j < end; j += kBlock)
+            G[j] = op(G[j]);
+    }
 }
 
 __global__ void __launch_bounds__(kBlock) k_grad_scale(grad_table tab, const float *__restrict__ res)
 {
     if (res[2] == 0.0f)
         return;
-    const float inv = res[1], mx = res[3];
-    const unsigned b = blockIdx.x;
-    const int si = seg_of(tab.first, tab.cnt, b);
-    const pgk_grad_seg sg = tab.seg[si];
-    const size_t base = (size_t)(b - tab.first[si]) * kNormChunk;
-    const size_t n = sg.n;
-    float *__restrict__ G = sg.g;
-    if ((((uintptr_t)G) & 15) == 0) {
-#pragma unroll
-        for (int k = 0; k < kNormVec; ++k) {
-            const size_t e = base + 4 * ((size_t)threadIdx.x + (size_t)k * kBlock);
-            if (e + 4 <= n) {
-                float4 g = *reinterpret_cast<const float4 *>(G + e);
-                g.x = scale_elem(g.x, mx, inv), g.y = scale_elem(g.y, mx, inv);
-                g.z = scale_elem(g.z, mx, inv), g.w = scale_elem(g.w, mx, inv);
-                *reinterpret_cast<float4 *>(G + e) = g;
-            } else {
-                for (size_t j = e; j < n; ++j)
-                    G[j] = scale_elem(G[j], mx, inv);
-            }
-        }
-    } else {
-        const size_t end = base + kNormChunk < n ? base + kNormChunk : n;
-        for (size_t j = base + threadIdx.x; j < end; j += kBlock)
-            G[j] = scale_elem(G[j], mx, inv);
-    }
-}
-
-// clip.c:49-61: values above c become c, below -c become -c
-__device__ __forceinline__ float clamp_c(float x, float c)
-{
-    return x > c ? c : (x < -c ? -c : x);
+    grad_map(tab, blockIdx.x, scale_op{res[3], res[1]});
 }
 
 __global__ void __launch_bounds__(kBlock) k_grad_clamp(grad_table tab, float c)
 {
-    const unsigned b = blockIdx.x;
-    const int si = seg_of(tab.first, tab.cnt, b);
-    const pgk_grad_seg sg = tab.seg[si];
-    const size_t base = (size_t)(b - tab.first[si]) * kNormChunk;
-    const size_t n = sg.n;
-    float *__restrict__ G = sg.g;
-    if ((((uintptr_t)G) & 15) == 0) {
-#pragma unroll
-        for (int k = 0; k < kNormVec; ++k) {
-            const size_t e = base + 4 * ((size_t)threadIdx.x + (size_t)k * kBlock);
-            if (e + 4 <= n) {
-                float4 g = *reinterpret_cast<const float4 *>(G + e);
-                g.x = clamp_c(g.x, c), g.y = clamp_c(g.y, c), g.z = clamp_c(g.z, c), g.w = clamp_c(g.w, c);
-                *reinterpret_cast<float4 *>(G + e) = g;
-            } else {
-                for (size_t j = e; j < n; ++j)
-                    G[j] = clamp_c(G[j], c);
-            }
-        }
-    } else {
-        const size_t end = base + kNormChunk < n ? base + kNormChunk : n;
-        for (size_t j = base + threadIdx.x; j < end; j += kBlock)
-            G[j] = clamp_c(G[j], c);
-    }
+    grad_map(tab, blockIdx.x, clamp_op{c});
 }
 
-// fills a grad table with segs[0..cnt) and their block prefix; returns the
-// block count (0 when every tensor is empty)
-unsigned grad_table_fill(grad_table &tab, const pgk_grad_seg *segs, int cnt)
+// fills a grad table with segs[0..cnt) and their block prefix for chunks
+// of `chunk` elements; returns the block count (0 when every tensor is empty)
+unsigned grad_table_fill(grad_table &tab, const pgk_grad_seg *segs, int cnt, size_t chunk)
 {
     tab = {};
     unsigned blocks = 0;
     for (int q = 0; q < cnt; ++q) {
         tab.seg[q] = segs[q];
         tab.first[q] = blocks;
-        blocks += (unsigned)((segs[q].n + kNormChunk - 1) / kNormChunk);
+        blocks += (unsigned)((segs[q].n + chunk - 1) / chunk);
     }
     tab.first[cnt] = blocks;
     tab.cnt = cnt;
-    return blocks;
-}
-
-size_t grad_blocks(const pgk_grad_seg *segs, int nseg)
-{
-    size_t blocks = 0;
-    for (int q = 0; q < nseg; ++q)
-        blocks += (segs[q].n + kNormChunk - 1) / kNormChunk;
     return blocks;
 }
 
@@ -368,7 +367,9 @@ extern "C" int pgk_adam_multi(const pgk_adam_seg *segs, int nseg, const pgk_adam
 
 extern "C" size_t pgk_grad_norm_workspace(const pgk_grad_seg *segs, int nseg)
 {
-    const size_t b = grad_blocks(segs, nseg);
+    size_t b = 0;
+    for (int q = 0; q < nseg; ++q)
+        b += (segs[q].n + kSumChunk - 1) / kSumChunk;
     return (b ? b : 1) * sizeof(double);
 }
 
@@ -380,7 +381,7 @@ extern "C" int pgk_grad_norm(const pgk_grad_seg *segs, int nseg, int clip, float
     for (int base = 0; base < nseg; base += PGK_GRAD_MAX_SEG) {
         const int cnt = nseg - base < PGK_GRAD_MAX_SEG ? nseg - base : PGK_GRAD_MAX_SEG;
         grad_table tab;
-        const unsigned blocks = grad_table_fill(tab, segs + base, cnt);
+        const unsigned blocks = grad_table_fill(tab, segs + base, cnt, kSumChunk);
         if (!blocks)
             continue;
         hipLaunchKernelGGL(k_sumsq, dim3(blocks), dim3(kBlock), 0, (hipStream_t)s, tab, part + off);
@@ -389,7 +390,7 @@ extern "C" int pgk_grad_norm(const pgk_grad_seg *segs, int nseg, int clip, float
         if (st)
             return st;
     }
-    hipLaunchKernelGGL(k_norm_fin, dim3(1), dim3(kBlock), 0, (hipStream_t)s, (const double *)part, off, clip,
+    hipLaunchKernelGGL(k_norm_fin, dim3(1), dim3(kFinBlock), 0, (hipStream_t)s, (const double *)part, off, clip,
                        max_norm, eps, res);
     return status();
 }
@@ -399,7 +400,7 @@ extern "C" int pgk_grad_scale(const pgk_grad_seg *segs, int nseg, const float *r
     for (int base = 0; base < nseg; base += PGK_GRAD_MAX_SEG) {
         const int cnt = nseg - base < PGK_GRAD_MAX_SEG ? nseg - base : PGK_GRAD_MAX_SEG;
         grad_table tab;
-        const unsigned blocks = grad_table_fill(tab, segs + base, cnt);
+        const unsigned blocks = grad_table_fill(tab, segs + base, cnt, kMapChunk);
         if (!blocks)
             continue;
         hipLaunchKernelGGL(k_grad_scale, dim3(blocks), dim3(kBlock), 0, (hipStream_t)s, tab, res);
@@ -415,7 +416,7 @@ extern "C" int pgk_clip_value(const pgk_grad_seg *segs, int nseg, float c, pgk_s
     for (int base = 0; base < nseg; base += PGK_GRAD_MAX_SEG) {
         const int cnt = nseg - base < PGK_GRAD_MAX_SEG ? nseg - base : PGK_GRAD_MAX_SEG;
         grad_table tab;
-        const unsigned blocks = grad_table_fill(tab, segs + base, cnt);
+        const unsigned blocks = grad_table_fill(tab, segs + base, cnt, kMapChunk);
         if (!blocks)
             continue;
         hipLaunchKernelGGL(k_grad_clamp, dim3(blocks), dim3(kBlock), 0, (hipStream_t)s, tab, c);
