@@ -9,8 +9,11 @@
 
 #include <stdbool.h>
 #include <stddef.h>
+#include <stdio.h>
 
+#include "adam.h"
 #include "autograd.h"
+#include "sgd.h"
 
 #ifdef __cplusplus
 extern "C" {
@@ -91,6 +94,42 @@ size_t pg_amd_jit_cache_hits(void);
  * (lds = 0) or read from LDS one k-step ahead like the GEMM (lds = 1).
  * Waits for the stream.  Returns a negative value on failure. */
 double pg_amd_mfma_probe(int lds);
+
+/* ---- checkpoints of device parameters and optimiser state ----
+ * Parameter lists in the reference's module checkpoint format (PGMD,
+ * nn/module.c:88-185: "PGMD", u32 version 1, u64 count, then one PGT1
+ * record per parameter value), so a file saved here loads with the
+ * reference's pg_module_load / pg_module_load_into and the reverse: the
+ * reference's pg_module has no device counterpart here, so the list is
+ * passed as nodes (pg_module_params order).  load_into copies each record
+ * into the matching node's value on the device; a count, dtype or shape
+ * mismatch returns false (records before it are already loaded, as in the
+ * reference). */
+bool pg_amd_params_save(pg_node *const *params, size_t n, const char *path);
+bool pg_amd_params_save_fp(pg_node *const *params, size_t n, FILE *fp);
+bool pg_amd_params_load_into(pg_node *const *params, size_t n, const char *path);
+bool pg_amd_params_load_into_fp(pg_node *const *params, size_t n, FILE *fp);
+
+/* Optimiser state, which the reference cannot checkpoint (its SGD momentum
+ * and Adam moments live only in memory; adam.h:42-44 lets a caller restore
+ * the step counter alone).  Formats, built from PGT1 records:
+ *   SGD   "PGSG", u32 version 1, u64 nparams, per parameter u32 has_buf (0
+ *         or 1) then the momentum buffer's PGT1 record when has_buf;
+ *   Adam  "PGAD", u32 version 1, u64 step, u64 nparams, per parameter u32
+ *         flags (bit 0: m and v follow, bit 1: the amsgrad maximum follows)
+ *         then those PGT1 records.
+ * load_into restores the state of an optimiser built with the same
+ * parameters (count and shapes checked, false on a mismatch); a parameter
+ * saved without state gets none, so its next step starts from zero as a
+ * fresh optimiser's does.  The hyper-parameters stay the caller's. */
+bool pg_amd_sgd_save(const pg_sgd *opt, const char *path);
+bool pg_amd_sgd_save_fp(const pg_sgd *opt, FILE *fp);
+bool pg_amd_sgd_load_into(pg_sgd *opt, const char *path);
+bool pg_amd_sgd_load_into_fp(pg_sgd *opt, FILE *fp);
+bool pg_amd_adam_save(const pg_adam *opt, const char *path);
+bool pg_amd_adam_save_fp(const pg_adam *opt, FILE *fp);
+bool pg_amd_adam_load_into(pg_adam *opt, const char *path);
+bool pg_amd_adam_load_into_fp(pg_adam *opt, FILE *fp);
 
 /* Kernel timer: while enabled, the fused backward kernel (kind 0), its
  * reduction finisher (1), the MFMA GEMMs (2), the SGD kernel (3), the

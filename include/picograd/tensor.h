@@ -96,6 +96,19 @@ bool pg_shape_equal(size_t ndim_a, const size_t *shape_a, size_t ndim_b, const s
 pg_tensor *pg_tensor_view(const pg_tensor *src);
 pg_tensor *pg_tensor_reshape_view(const pg_tensor *src, size_t ndim, const size_t *shape);
 
+/* serialization, tensor.h:86-91 of the reference: the PGT1 format ("PGT1",
+ * u32 version 1, u32 dtype, u32 ndim, u64 shape[ndim], u64 numel, u64
+ * elem_size, then the elements row-major).  Saves read the elements from
+ * device memory after all queued work; loads return a device tensor.  The
+ * files are byte-identical to the reference's, and each reads the other's.
+ * Loads reject what the reference rejects (bad magic or version, dtype out
+ * of range, ndim 0 or above 8, a dimension of 0 or above 10,000,000, numel
+ * or element size disagreeing with the header). */
+bool pg_tensor_save(const pg_tensor *t, const char *path);
+pg_tensor *pg_tensor_load(const char *path);
+bool pg_tensor_save_fp(const pg_tensor *t, FILE *fp);
+pg_tensor *pg_tensor_load_fp(FILE *fp);
+
 /* ---- appended: host/device synchronisation ---- */
 /* Waits for queued device work, then copies the elements into the host
  * mirror t->data (allocated on first use).  Returns false on failure. */

@@ -300,6 +300,81 @@ void orc_clip_grad_value(float *const *g, const size_t *n, size_t count,
     }
 }
 
+/* ---------------- PGT1 / PGMD checkpoint bytes ---------------- */
+
+static size_t orc_put(unsigned char *out, size_t pos, size_t cap, const void *p, size_t n)
+{
+    if (out && pos + n <= cap)
+        memcpy(out + pos, p, n);
+    return pos + n;
+}
+
+size_t orc_pgt1_write(int dtype, size_t ndim, const size_t *shape, const void *data,
+                      unsigned char *out, size_t cap)
+{
+    /* tensor.c:607-650 for a contiguous tensor: "PGT1", u32 version 1, u32
+     * dtype, u32 ndim, u64 shape[ndim], u64 numel, u64 elem_size, then the
+     * elements; little-endian (x86) */
+    const uint32_t ver = 1, dt = (uint32_t)dtype, nd = (uint32_t)ndim;
+    uint64_t numel = 1;
+    for (size_t i = 0; i < ndim; i++)
+        numel *= (uint64_t)shape[i];
+    const uint64_t elem = dtype == ORC_F32 ? 4 : 2;
+    size_t pos = orc_put(out, 0, cap, "PGT1", 4);
+    pos = orc_put(out, pos, cap, &ver, 4);
+    pos = orc_put(out, pos, cap, &dt, 4);
+    pos = orc_put(out, pos, cap, &nd, 4);
+    for (size_t i = 0; i < ndim; i++) {
+        const uint64_t d = (uint64_t)shape[i];
+        pos = orc_put(out, pos, cap, &d, 8);
+    }
+    pos = orc_put(out, pos, cap, &numel, 8);
+    pos = orc_put(out, pos, cap, &elem, 8);
+    return orc_put(out, pos, cap, data, (size_t)(numel * elem));
+}
+
+size_t orc_pgt1_check(const unsigned char *buf, size_t len)
+{
+    /* the checks of tensor.c:655-702 in their order; returns the record's
+     * length when a load would succeed, 0 when it would return NULL */
+    size_t pos = 0;
+    uint32_t ver, dt, nd;
+    uint64_t d, numel, elem, want = 1;
+    if (len < 16 || memcmp(buf, "PGT1", 4) != 0)
+        return 0;
+    memcpy(&ver, buf + 4, 4);
+    if (ver != 1)
+        return 0;
+    memcpy(&dt, buf + 8, 4);
+    memcpy(&nd, buf + 12, 4);
+    pos = 16;
+    if (nd == 0 || nd > 8)
+        return 0;
+    if (dt >= 3)
+        return 0;
+    for (uint32_t i = 0; i < nd; i++) {
+        if (pos + 8 > len)
+            return 0;
+        memcpy(&d, buf + pos, 8);
+        pos += 8;
+        if (d == 0 || d > 10000000)
+            return 0;
+        want *= d;
+    }
+    if (pos + 16 > len)
+        return 0;
+    memcpy(&numel, buf + pos, 8);
+    memcpy(&elem, buf + pos + 8, 8);
+    pos += 16;
+    if (numel != want)
+        return 0;
+    if (elem != (dt == (uint32_t)ORC_F32 ? 4u : 2u))
+        return 0;
+    if (len - pos < numel * elem)
+        return 0;
+    return pos + (size_t)(numel * elem);
+}
+
 /* ---------------- GEMM with f32 accumulation ---------------- */
 
 typedef struct {

@@ -29,6 +29,10 @@
  *                                     (test_training.c:237-268)
  *   orc_grad_norm, orc_clip_*         golden clip fixtures bit for bit;
  *                                     closed forms
+ *   orc_pgt1_write, orc_pgt1_check    files written by the reference's
+ *                                     pg_tensor_save / pg_module_save byte
+ *                                     for byte; its loader's verdict on 14
+ *                                     crafted headers
  *   orc_mlp_step                      golden two-step f32 MLP training run
  *                                     of the reference (ORC_F32); the 16-bit
  *                                     modes differ only by orc_round_f32 on
@@ -90,6 +94,18 @@ float orc_clip_grad_norm(float *const *g, const size_t *n, size_t count,
                          float max_norm, float eps);
 void orc_clip_grad_value(float *const *g, const size_t *n, size_t count,
                          float clip_value);
+
+/*
+ * Checkpoint bytes.  orc_pgt1_write lays out one tensor as the reference's
+ * pg_tensor_save_fp does (tensor.c:607-650) into out (when cap allows) and
+ * returns the record's size.  orc_pgt1_check applies pg_tensor_load_fp's
+ * checks (tensor.c:655-702) and returns the record's size if a load would
+ * succeed, else 0.  dtype: ORC_F32 / ORC_F16 / ORC_BF16 (the reference's
+ * pg_dtype values 0 / 1 / 2).
+ */
+size_t orc_pgt1_write(int dtype, size_t ndim, const size_t *shape, const void *data,
+                      unsigned char *out, size_t cap);
+size_t orc_pgt1_check(const unsigned char *buf, size_t len);
 
 /*
  * C[i,j] (+)= sum_p A(i,p) * B(p,j), every product formed from f32 values

@@ -76,6 +76,8 @@ _PROTOS = {
     "pg_tensor_normal": (vp, [sz, SZP, fl, fl]),
     "pg_tensor_free": (None, [vp]),
     "pg_tensor_fill": (None, [vp, fl]),
+    "pg_tensor_save": (bo, [vp, C.c_char_p]),
+    "pg_tensor_load": (vp, [C.c_char_p]),
     # autograd.h
     "pg_var_from_data": (vp, [sz, SZP, vp, bo]),
     "pg_var_from_tensor": (vp, [vp, bo]),
@@ -188,6 +190,12 @@ _AMD_PROTOS = {
     "pg_amd_mfma_probe": (C.c_double, [ip]),
     "pg_amd_timer_read": (C.c_double, [ip, C.POINTER(C.c_size_t)]),
     "pg_amd_timer_reset": (None, []),
+    "pg_amd_params_save": (bo, [C.POINTER(vp), sz, C.c_char_p]),
+    "pg_amd_params_load_into": (bo, [C.POINTER(vp), sz, C.c_char_p]),
+    "pg_amd_sgd_save": (bo, [vp, C.c_char_p]),
+    "pg_amd_sgd_load_into": (bo, [vp, C.c_char_p]),
+    "pg_amd_adam_save": (bo, [vp, C.c_char_p]),
+    "pg_amd_adam_load_into": (bo, [vp, C.c_char_p]),
 }
 
 

@@ -16,6 +16,7 @@
 #include <assert.h>
 #include <math.h>
 #include <stdlib.h>
+#include <string.h>
 
 typedef struct {
     pg_node *param;
@@ -221,4 +222,106 @@ void pg_adam_step(pg_adam *opt)
         pgd_check(pgk_adam_multi(segs, ns, &h, pgd_stream()), "pg_adam_step");
     pgd_tend(tk);
     free(segs);
+}
+
+/* ---------------- moment checkpoint ("PGAD") ---------------- */
+
+bool pg_amd_adam_save_fp(const pg_adam *opt, FILE *fp)
+{
+    if (!opt || !fp)
+        return false;
+    const uint32_t ver = 1;
+    const uint64_t step = (uint64_t)opt->step, n = (uint64_t)opt->n;
+    if (fwrite("PGAD", 1, 4, fp) != 4 || fwrite(&ver, 4, 1, fp) != 1 || fwrite(&step, 8, 1, fp) != 1 ||
+        fwrite(&n, 8, 1, fp) != 1)
+        return false;
+    for (size_t i = 0; i < opt->n; i++) {
+        const adam_state *s = &opt->st[i];
+        const uint32_t flags = (s->m ? 1u : 0u) | (s->m && s->vmax ? 2u : 0u);
+        if (fwrite(&flags, 4, 1, fp) != 1)
+            return false;
+        if ((flags & 1u) && (!pg_tensor_save_fp(s->m, fp) || !pg_tensor_save_fp(s->v, fp)))
+            return false;
+        if ((flags & 2u) && !pg_tensor_save_fp(s->vmax, fp))
+            return false;
+    }
+    return true;
+}
+
+bool pg_amd_adam_save(const pg_adam *opt, const char *path)
+{
+    if (!path)
+        return false;
+    FILE *fp = fopen(path, "wb");
+    if (!fp)
+        return false;
+    bool ok = pg_amd_adam_save_fp(opt, fp);
+    return fclose(fp) == 0 && ok;
+}
+
+/* loads one moment record into *slot, creating it shaped like the
+ * parameter when absent */
+static bool load_moment(pg_tensor **slot, const pg_tensor *like, FILE *fp)
+{
+    if (!*slot) {
+        *slot = pg_tensor_empty_dtype(PG_DTYPE_F32, like->ndim, like->shape);
+        if (!*slot)
+            return false;
+    }
+    return pgc_load_into(*slot, fp);
+}
+
+bool pg_amd_adam_load_into_fp(pg_adam *opt, FILE *fp)
+{
+    if (!opt || !fp)
+        return false;
+    char magic[4];
+    uint32_t ver = 0;
+    uint64_t step = 0, n = 0;
+    if (fread(magic, 1, 4, fp) != 4 || memcmp(magic, "PGAD", 4) != 0)
+        return false;
+    if (fread(&ver, 4, 1, fp) != 1 || ver != 1)
+        return false;
+    if (fread(&step, 8, 1, fp) != 1 || fread(&n, 8, 1, fp) != 1 || n != (uint64_t)opt->n)
+        return false;
+    for (size_t i = 0; i < opt->n; i++) {
+        uint32_t flags = 0;
+        if (fread(&flags, 4, 1, fp) != 1 || flags > 3u || flags == 2u)
+            return false;
+        adam_state *s = &opt->st[i];
+        const pg_tensor *like = s->param->value;
+        if (!(flags & 1u)) {
+            free_moments(s);
+            continue;
+        }
+        if (!load_moment(&s->m, like, fp) || !load_moment(&s->v, like, fp))
+            return false;
+        if (flags & 2u) {
+            if (!load_moment(&s->vmax, like, fp))
+                return false;
+        } else if (opt->cfg.amsgrad) {
+            /* state saved without amsgrad: its running maximum starts at zero */
+            pg_tensor_free(s->vmax);
+            s->vmax = pg_tensor_zeros(like->ndim, like->shape);
+            if (!s->vmax)
+                return false;
+        } else {
+            pg_tensor_free(s->vmax);
+            s->vmax = NULL;
+        }
+    }
+    opt->step = (unsigned long long)step;
+    return true;
+}
+
+bool pg_amd_adam_load_into(pg_adam *opt, const char *path)
+{
+    if (!path)
+        return false;
+    FILE *fp = fopen(path, "rb");
+    if (!fp)
+        return false;
+    bool ok = pg_amd_adam_load_into_fp(opt, fp);
+    fclose(fp);
+    return ok;
 }

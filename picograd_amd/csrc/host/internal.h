@@ -57,6 +57,18 @@ const uint16_t *pgt_shadow16(pg_tensor *t, pg_dtype dt);
 /* records an in-place write of t's elements: its shadow is stale */
 void pgt_touch(pg_tensor *t);
 
+/* ---- checkpoint I/O (checkpoint.c) ---- */
+#include <stdio.h>
+/* nbytes of device memory to / from a file through pinned double buffers
+ * on the library stream (the save is ordered after queued work; the load
+ * has finished when it returns).  false on a short read / write or a
+ * device error. */
+bool pgc_dev_to_file(const void *dev, size_t nbytes, FILE *fp);
+bool pgc_file_to_dev(void *dev, size_t nbytes, FILE *fp);
+/* reads one PGT1 record into dst's storage if dtype and shape match;
+ * dst is left unchanged otherwise */
+bool pgc_load_into(pg_tensor *dst, FILE *fp);
+
 /* ---- RNG (tensor.c) ---- */
 void pg_rng_uniform_host(float *out, size_t n, float low, float high);
 void pg_rng_normal_host(float *out, size_t n, float mean, float stddev);

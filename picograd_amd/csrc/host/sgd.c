@@ -11,6 +11,7 @@
 
 #include <assert.h>
 #include <stdlib.h>
+#include <string.h>
 
 typedef struct {
     pg_node *param;
@@ -139,4 +140,82 @@ void pg_sgd_step(pg_sgd *opt)
                   "pg_sgd_step");
     pgd_tend(tk);
     free(segs);
+}
+
+/* ---------------- momentum checkpoint ("PGSG") ---------------- */
+
+bool pg_amd_sgd_save_fp(const pg_sgd *opt, FILE *fp)
+{
+    if (!opt || !fp)
+        return false;
+    const uint32_t ver = 1;
+    const uint64_t n = (uint64_t)opt->n;
+    if (fwrite("PGSG", 1, 4, fp) != 4 || fwrite(&ver, 4, 1, fp) != 1 || fwrite(&n, 8, 1, fp) != 1)
+        return false;
+    for (size_t i = 0; i < opt->n; i++) {
+        const uint32_t has = opt->st[i].buf ? 1u : 0u;
+        if (fwrite(&has, 4, 1, fp) != 1)
+            return false;
+        if (has && !pg_tensor_save_fp(opt->st[i].buf, fp))
+            return false;
+    }
+    return true;
+}
+
+bool pg_amd_sgd_save(const pg_sgd *opt, const char *path)
+{
+    if (!path)
+        return false;
+    FILE *fp = fopen(path, "wb");
+    if (!fp)
+        return false;
+    bool ok = pg_amd_sgd_save_fp(opt, fp);
+    return fclose(fp) == 0 && ok;
+}
+
+bool pg_amd_sgd_load_into_fp(pg_sgd *opt, FILE *fp)
+{
+    if (!opt || !fp)
+        return false;
+    char magic[4];
+    uint32_t ver = 0;
+    uint64_t n = 0;
+    if (fread(magic, 1, 4, fp) != 4 || memcmp(magic, "PGSG", 4) != 0)
+        return false;
+    if (fread(&ver, 4, 1, fp) != 1 || ver != 1)
+        return false;
+    if (fread(&n, 8, 1, fp) != 1 || n != (uint64_t)opt->n)
+        return false;
+    for (size_t i = 0; i < opt->n; i++) {
+        uint32_t has = 0;
+        if (fread(&has, 4, 1, fp) != 1 || has > 1)
+            return false;
+        sgd_state *s = &opt->st[i];
+        if (!has) {
+            pg_tensor_free(s->buf);
+            s->buf = NULL;
+            continue;
+        }
+        const pg_tensor *v = s->param->value;
+        if (!s->buf) {
+            s->buf = pg_tensor_empty_dtype(PG_DTYPE_F32, v->ndim, v->shape);
+            if (!s->buf)
+                return false;
+        }
+        if (!pgc_load_into(s->buf, fp))
+            return false;
+    }
+    return true;
+}
+
+bool pg_amd_sgd_load_into(pg_sgd *opt, const char *path)
+{
+    if (!path)
+        return false;
+    FILE *fp = fopen(path, "rb");
+    if (!fp)
+        return false;
+    bool ok = pg_amd_sgd_load_into_fp(opt, fp);
+    fclose(fp);
+    return ok;
 }

@@ -488,6 +488,92 @@ def clip(R: PgLib) -> dict:
     return out
 
 
+def _pgt1_header(dtype, shape, numel=None, elem=None, magic=b"PGT1", ver=1, ndim=None):
+    import struct
+    nd = len(shape) if ndim is None else ndim
+    h = magic + struct.pack("<III", ver, dtype, nd) + b"".join(struct.pack("<Q", d) for d in shape)
+    n = int(np.prod(shape)) if numel is None else numel
+    es = (4 if dtype == F32 else 2) if elem is None else elem
+    return h + struct.pack("<QQ", n, es)
+
+
+# crafted PGT1 byte strings and whether the reference's pg_tensor_load takes
+# them (tensor.c:655-702); the data after each header is zeros
+CKPT_CRAFTED = [
+    ("ok_f32", _pgt1_header(F32, (2, 3)) + bytes(24)),
+    ("ok_bf16", _pgt1_header(BF16, (5,)) + bytes(10)),
+    ("bad_magic", _pgt1_header(F32, (2,), magic=b"PGT2") + bytes(8)),
+    ("bad_version", _pgt1_header(F32, (2,), ver=2) + bytes(8)),
+    ("bad_dtype", _pgt1_header(3, (2,), elem=4) + bytes(8)),
+    ("ndim_zero", _pgt1_header(F32, (), ndim=0) + bytes(4)),
+    ("ndim_nine", _pgt1_header(F32, (1,) * 9) + bytes(4)),
+    ("dim_zero", _pgt1_header(F32, (3, 0), numel=0) + bytes(0)),
+    ("dim_too_big", _pgt1_header(F32, (10000001,)) + bytes(16)),
+    ("dim_at_bound", _pgt1_header(F16, (10000000,)) + bytes(20000000)),
+    ("numel_mismatch", _pgt1_header(F32, (2, 3), numel=5) + bytes(24)),
+    ("elem_mismatch", _pgt1_header(F32, (2, 3), elem=2) + bytes(24)),
+    ("truncated_data", _pgt1_header(F32, (2, 3)) + bytes(20)),
+    ("truncated_header", _pgt1_header(F32, (2, 3))[:20]),
+]
+
+
+def checkpoint_files(R: PgLib) -> dict:
+    """pg_tensor_save / pg_tensor_load (core/tensor.c:604-711) and
+    pg_module_save (nn/module.c:91-104): the bytes the reference writes for
+    f32, f16 and bf16 tensors of several ranks and for a three-parameter
+    module, and its loader's verdict on crafted headers."""
+    import os
+    import tempfile
+    rng = np.random.default_rng(31)
+    out = {}
+    arrays = {
+        "t0": (F32, rng.standard_normal((3, 5)).astype(np.float32)),
+        "t1": (F16, rng.standard_normal((2, 3, 4)).astype(np.float16).view(np.uint16)),
+        "t2": (BF16, (rng.standard_normal(7).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)),
+        "t3": (F32, np.array([42.5], np.float32)),
+        "t4": (F32, rng.standard_normal((2, 1, 3, 1, 2, 1, 1, 2)).astype(np.float32)),
+    }
+    with tempfile.TemporaryDirectory() as d:
+        for name, (dt, arr) in arrays.items():
+            t = R.tensor(arr, dt)
+            path = os.path.join(d, name + ".pgt")
+            assert R.lib.pg_tensor_save(C.c_void_p(t), path.encode())
+            R.pg_tensor_free(t)
+            out[f"{name}_dtype"] = np.array(dt, np.int64)
+            out[f"{name}_data"] = arr
+            out[f"{name}_bytes"] = np.frombuffer(open(path, "rb").read(), np.uint8)
+        L = R.lib
+        L.pg_module_new.restype = C.c_void_p
+        L.pg_module_register.argtypes = [C.c_void_p, C.c_void_p]
+        L.pg_module_save.argtypes = [C.c_void_p, C.c_char_p]
+        L.pg_module_free.argtypes = [C.c_void_p]
+        L.pg_tensor_load.restype = C.c_void_p
+        L.pg_tensor_load.argtypes = [C.c_char_p]
+        m = L.pg_module_new()
+        nodes = [R.var(rng.standard_normal(sh).astype(np.float32)) for sh in ((4, 6), (6,), (6, 2))]
+        for i, n in enumerate(nodes):
+            L.pg_module_register(C.c_void_p(m), C.c_void_p(n))
+            out[f"mod_p{i}"] = R.value(n)
+        path = os.path.join(d, "mod.pgmd")
+        assert L.pg_module_save(C.c_void_p(m), path.encode())
+        out["mod_bytes"] = np.frombuffer(open(path, "rb").read(), np.uint8)
+        L.pg_module_free(C.c_void_p(m))
+        _free(R, *nodes)
+        names, verdicts = [], []
+        for i, (name, blob) in enumerate(CKPT_CRAFTED):
+            out[f"crafted_{i}"] = np.frombuffer(blob, np.uint8)
+            path = os.path.join(d, name + ".pgt")
+            open(path, "wb").write(blob)
+            t = L.pg_tensor_load(path.encode())
+            verdicts.append(bool(t))
+            if t:
+                R.pg_tensor_free(t)
+            names.append(name)
+        out["crafted_names"] = np.array(names)
+        out["crafted_loads"] = np.array(verdicts)
+    return out
+
+
 CASES = {
     "rng": rng_streams,
     "convert": lambda R: conversions(),
@@ -500,6 +586,7 @@ CASES = {
     "mlp": mlp,
     "adam": adam_trajectories,
     "clip": clip,
+    "ckpt": checkpoint_files,
 }
 
 

@@ -40,6 +40,8 @@ class Oracle:
             "orc_grad_norm": (_fl, [C.POINTER(_vp), C.POINTER(_sz), _sz]),
             "orc_clip_grad_norm": (_fl, [C.POINTER(_vp), C.POINTER(_sz), _sz, _fl, _fl]),
             "orc_clip_grad_value": (None, [C.POINTER(_vp), C.POINTER(_sz), _sz, _fl]),
+            "orc_pgt1_write": (_sz, [_ip, _sz, C.POINTER(_sz), _vp, _vp, _sz]),
+            "orc_pgt1_check": (_sz, [_vp, _sz]),
             "orc_gemm_acc32": (None, [_ip, _ip, _ip, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _ip, _ip]),
             "orc_gemm_acc64": (None, [_ip, _ip, _ip, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _ip]),
             "orc_chain1_backward": (None, [_vp, _vp, _vp, _sz, _vp, _vp, _vp]),
@@ -123,6 +125,19 @@ class Oracle:
     def clip_grad_value(self, gs, c) -> None:
         ptrs, ns = self._grad_list(gs)
         self.orc_clip_grad_value(ptrs, ns, len(gs), c)
+
+    def pgt1_bytes(self, dtype: int, arr: np.ndarray) -> bytes:
+        """The PGT1 record of arr (f32, or uint16 bits for f16/bf16)."""
+        arr = np.ascontiguousarray(arr)
+        shape = (C.c_size_t * max(1, arr.ndim))(*arr.shape)
+        n = self.orc_pgt1_write(dtype, arr.ndim, shape, arr.ctypes.data, None, 0)
+        out = (C.c_ubyte * n)()
+        self.orc_pgt1_write(dtype, arr.ndim, shape, arr.ctypes.data, out, n)
+        return bytes(out)
+
+    def pgt1_check(self, blob: bytes) -> int:
+        buf = (C.c_ubyte * max(1, len(blob))).from_buffer_copy(blob + b"\0" * (len(blob) == 0))
+        return self.orc_pgt1_check(buf, len(blob))
 
     def chain1(self, a, b, c):
         da, db, dc = (np.empty_like(a) for _ in range(3))

@@ -361,6 +361,47 @@ def test_clip_closed_forms_and_planted_mistake(oracle):
     assert abs(float(np.sqrt(np.sum(big.astype(np.float64) ** 2))) - float(g["big_norm"])) <= np.spacing(g["big_norm"])
 
 
+# ---------------------------------------------------------------- checkpoint bytes
+
+def test_pgt1_bytes_match_reference(oracle):
+    """pg_tensor_save (tensor.c:607-650) and pg_module_save (module.c:91-104):
+    the oracle's records equal the files the reference wrote, for f32, f16
+    and bf16 tensors of ranks 1 to 8 and a three-parameter module."""
+    import struct
+    g = golden("ckpt")
+    for i in range(5):
+        dt, arr = int(g[f"t{i}_dtype"]), g[f"t{i}_data"]
+        assert oracle.pgt1_bytes(dt, arr) == g[f"t{i}_bytes"].tobytes(), i
+        assert oracle.pgt1_check(g[f"t{i}_bytes"].tobytes()) == g[f"t{i}_bytes"].size
+    mod = b"PGMD" + struct.pack("<IQ", 1, 3) + b"".join(oracle.pgt1_bytes(0, g[f"mod_p{i}"]) for i in range(3))
+    assert mod == g["mod_bytes"].tobytes()
+
+
+def test_pgt1_loader_checks_match_reference(oracle):
+    """pg_tensor_load's verdict (tensor.c:655-702) on crafted records: bad
+    magic, version, dtype, ndim 0 or 9, a zero or oversized dimension (the
+    10,000,000 bound is inclusive), numel or element size disagreeing, and
+    truncation."""
+    g = golden("ckpt")
+    for i, (name, ok) in enumerate(zip(g["crafted_names"], g["crafted_loads"])):
+        assert bool(oracle.pgt1_check(g[f"crafted_{i}"].tobytes())) == bool(ok), name
+
+
+def test_pgt1_planted_mistakes_are_caught(oracle):
+    """A shape written as u32 or a big-endian header would not be the
+    reference's file."""
+    import struct
+    g = golden("ckpt")
+    arr = g["t0_data"]
+    ref = g["t0_bytes"].tobytes()
+    as_u32 = b"PGT1" + struct.pack("<III", 1, 0, 2) + struct.pack("<II", *arr.shape) + struct.pack(
+        "<QQ", arr.size, 4) + arr.tobytes()
+    big = b"PGT1" + struct.pack(">III", 1, 0, 2) + struct.pack(">QQ", *arr.shape) + struct.pack(
+        ">QQ", arr.size, 4) + arr.tobytes()
+    assert as_u32 != ref and big != ref
+    assert oracle.pgt1_check(as_u32) == 0 and oracle.pgt1_check(big) == 0
+
+
 # ---------------------------------------------------------------- elementwise chains
 
 def test_chain1_matches_reference(oracle):
