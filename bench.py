@@ -1,6 +1,6 @@
 """Benchmark of the MI355X picograd backward path (one GPU).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only c2,c3,c4,c1,c5,opt]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only c2,c3,c4,c1,c5,opt,ckpt,jit]
 
 Headline (the JSON `value`): config 2 of BASELINE.json -- the fused
 broadcasting elementwise backward of y = gelu(x + bias) * sigmoid(g),
@@ -12,8 +12,11 @@ value = algorithmic bytes (16 B/element + 32 KiB) / measured step time.
 Also reported in `extra`: config 3 (bf16 dgrad + wgrad, TFLOP/s), config 4
 (ragged f16 matmul + bmm backward, TFLOP/s), config 1 (the [64, 64] chain,
 µs per iteration of leaves + forward + backward), config 5 (the MLP
-training step, steps/s) and the optimiser leg (AdamW + clipping by the
-global grad norm over config 5's 37.8M parameters, GB/s).
+training step, steps/s), the optimiser leg (AdamW + clipping by the
+global grad norm over config 5's 37.8M parameters, GB/s) and the
+checkpoint leg (config 5's parameters and SGD momentum saved and loaded in
+the reference's PGT1/PGMD formats, GB/s) and jit_demo.c's workloads
+(µs per iteration, beside the reference's published figures).
 
 Timing: HIP events on the library stream around K steps (after W warmup
 steps, with stream synchronisation on both sides); per-kernel durations
@@ -610,6 +613,216 @@ def cpu_opt(dims=C5_DIMS, budget_s=15.0):
             "sample": f"{len(times)} clip + AdamW steps over config 5's {n} parameters", "ms": sec * 1e3}
 
 
+# ---------------------------------------------------------------- checkpoint leg
+
+def _ckpt_dir() -> str:
+    """A memory-backed directory when there is one, so the file system's
+    disk speed is not what is measured."""
+    import tempfile
+    return "/dev/shm" if os.access("/dev/shm", os.W_OK) else tempfile.gettempdir()
+
+
+def bench_ckpt(L, reps=3, dims=C5_DIMS):
+    """pg_amd_params_save (PGMD, the reference's module format) +
+    pg_amd_sgd_save (momentum) of config 5's parameters after one SGD step,
+    then pg_amd_params_load_into + pg_amd_sgd_load_into back; best of
+    `reps`.  Bytes = both files."""
+    from picograd_amd.capi import SgdCfg, shape_arg
+    L.pg_seed(49)
+    params = []
+    for shp in c5_param_shapes(dims):
+        nd, sh = shape_arg(shp)
+        p = L._check(L.pg_var_normal(nd, sh, 0.0, 0.02, True))
+        L.node(p).grad = L.pg_tensor_normal(nd, sh, 0.0, 1.0)
+        params.append(p)
+    opt = L.pg_sgd_new(C.byref(SgdCfg(0.01, 0.9, 0.0, 1e-4, True)))
+    for p in params:
+        L.pg_sgd_add_param(opt, p)
+    L.pg_sgd_step(opt)
+    arr = (C.c_void_p * len(params))(*params)
+    d = _ckpt_dir()
+    pf, sf = os.path.join(d, f"pg_bench_{os.getpid()}.pgmd"), os.path.join(d, f"pg_bench_{os.getpid()}.pgsg")
+    save, load = [], []
+    try:
+        for _ in range(reps):
+            L.sync()
+            t0 = time.perf_counter()
+            ok = L.pg_amd_params_save(arr, len(params), pf.encode()) and L.pg_amd_sgd_save(opt, sf.encode())
+            save.append(time.perf_counter() - t0)
+            assert ok, L.pg_amd_last_error()
+            t0 = time.perf_counter()
+            ok = L.pg_amd_params_load_into(arr, len(params), pf.encode()) and L.pg_amd_sgd_load_into(opt, sf.encode())
+            L.sync()
+            load.append(time.perf_counter() - t0)
+            assert ok, L.pg_amd_last_error()
+        nbytes = os.path.getsize(pf) + os.path.getsize(sf)
+    finally:
+        for f in (pf, sf):
+            if os.path.exists(f):
+                os.remove(f)
+        L.pg_sgd_free(opt)
+        for p in params:
+            L.pg_node_free(p)
+    return {"bytes": nbytes, "dir": d, "save_ms": min(save) * 1e3, "load_ms": min(load) * 1e3,
+            "save_gbs": nbytes / min(save) / 1e9, "load_gbs": nbytes / min(load) / 1e9}
+
+
+def cpu_ckpt(reps=3, dims=C5_DIMS):
+    """The reference's pg_module_save of the same parameter list from host
+    memory (it has no optimiser-state format), and pg_module_load_into."""
+    from oracle_lib import REF_SO
+    from picograd_amd.capi import PgLib, shape_arg
+    if not REF_SO.exists():
+        return None
+    R = PgLib(REF_SO, device=False)
+    lib = R.lib
+    lib.pg_module_new.restype = C.c_void_p
+    lib.pg_module_register.argtypes = [C.c_void_p, C.c_void_p]
+    lib.pg_module_save.argtypes = [C.c_void_p, C.c_char_p]
+    lib.pg_module_load_into.argtypes = [C.c_void_p, C.c_char_p]
+    lib.pg_module_free.argtypes = [C.c_void_p]
+    R.pg_seed(49)
+    m = lib.pg_module_new()
+    nodes = []
+    for shp in c5_param_shapes(dims):
+        nd, sh = shape_arg(shp)
+        n = R._check(R.pg_var_normal(nd, sh, 0.0, 0.02, True))
+        lib.pg_module_register(C.c_void_p(m), C.c_void_p(n))
+        nodes.append(n)
+    f = os.path.join(_ckpt_dir(), f"pg_bench_ref_{os.getpid()}.pgmd")
+    save, load = [], []
+    try:
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            assert lib.pg_module_save(C.c_void_p(m), f.encode())
+            save.append(time.perf_counter() - t0)
+            t0 = time.perf_counter()
+            assert lib.pg_module_load_into(C.c_void_p(m), f.encode())
+            load.append(time.perf_counter() - t0)
+        nbytes = os.path.getsize(f)
+    finally:
+        if os.path.exists(f):
+            os.remove(f)
+        lib.pg_module_free(C.c_void_p(m))
+        for n in nodes:
+            R.pg_node_free(n)
+    return {"value": nbytes / min(save) / 1e9, "unit": "GB/s", "cores": 1, "kind": "reference",
+            "sample": f"pg_module_save of config 5's parameters ({nbytes} B) from host memory",
+            "load_gbs": nbytes / min(load) / 1e9}
+
+
+# ---------------------------------------------------------------- forward JIT leg
+
+def _demo_graph(X, shape):
+    """jit_demo.c's graph: (a + b) * c -> relu -> tanh over `shape`."""
+    from picograd_amd.capi import shape_arg
+    g = X.pg_jit_graph_new()
+    ids = []
+    for _ in range(3):
+        nd, sh = shape_arg(shape)
+        ids.append(X.pg_jit_add_input(g, nd, sh))
+    t = X.pg_jit_add(g, ids[0], ids[1])
+    t = X.pg_jit_mul(g, t, ids[2])
+    t = X.pg_jit_add_op(g, 11, (C.c_int * 1)(t), 1)  # PG_JIT_RELU
+    t = X.pg_jit_add_op(g, 13, (C.c_int * 1)(t), 1)  # PG_JIT_TANH
+    X.pg_jit_mark_output(g, t)
+    exe = X.pg_jit_compile(g)
+    assert exe, X.pg_jit_last_error()
+    return g, exe
+
+
+def _demo_inputs(X, shape):
+    from picograd_amd.capi import shape_arg
+    X.pg_seed(42)
+    nd, sh = shape_arg(shape)
+    return [X.pg_tensor_uniform(nd, sh, -1.0, 1.0) for _ in range(3)]
+
+
+def jit_forward_loop(X, shape, iters):
+    """jit_demo.c's timed loop: y = pg_jit_run_single(exe, ins, 3);
+    pg_tensor_free(y), `iters` times; microseconds per iteration (the
+    device library's result waited for at the end)."""
+    g, exe = _demo_graph(X, shape)
+    ts = _demo_inputs(X, shape)
+    ins = (C.c_void_p * 3)(*ts)
+    for _ in range(min(iters, 50)):
+        X.pg_tensor_free(X.pg_jit_run_single(exe, ins, 3))
+    if X.device:
+        X.sync()
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        X.pg_tensor_free(X.pg_jit_run_single(exe, ins, 3))
+    if X.device:
+        X.sync()
+    us = (time.perf_counter() - t0) / iters * 1e6
+    for t in ts:
+        X.pg_tensor_free(t)
+    X.pg_jit_exe_free(exe)
+    X.pg_jit_graph_free(g)
+    return us
+
+
+def chain_backward_loop(X, shape, iters):
+    """The config-1 loop (leaves, add, mul, relu, tanh, sum_all,
+    pg_backward) at `shape`: the README's "large [512,512]" backward case."""
+    from oracle_lib import Oracle
+    o = Oracle()
+    o.orc_seed(42)
+    n = shape[0] * shape[1]
+    a, b, c = (o.uniform(n, -1.0, 1.0).reshape(shape) for _ in range(3))
+    shp = (C.c_size_t * 2)(*shape)
+
+    def one():
+        na = X.pg_var_from_data(2, shp, a.ctypes.data, True)
+        nb = X.pg_var_from_data(2, shp, b.ctypes.data, True)
+        nc = X.pg_var_from_data(2, shp, c.ctypes.data, True)
+        t0 = X.pg_ag_add(na, nb)
+        t1 = X.pg_ag_mul(t0, nc)
+        t2 = X.pg_ag_relu(t1)
+        t3 = X.pg_ag_tanh(t2)
+        loss = X.pg_ag_sum_all(t3)
+        X.pg_backward(loss)
+        for nn in (loss, t3, t2, t1, t0, na, nb, nc):
+            X.pg_node_free(nn)
+
+    for _ in range(min(iters, 10)):
+        one()
+    if X.device:
+        X.sync()
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        one()
+    if X.device:
+        X.sync()
+    return (time.perf_counter() - t0) / iters * 1e6
+
+
+def bench_jit(L):
+    """jit_demo.c's workloads on the device: the fused forward at [64,64]
+    (10,000 iterations, as the demo) and [512,512], and the chain's
+    forward + backward at [512,512]."""
+    return {"fwd_64x64_us_per_iter": jit_forward_loop(L, (64, 64), 10000),
+            "fwd_512x512_us_per_iter": jit_forward_loop(L, (512, 512), 2000),
+            "fwd_bwd_512x512_us_per_iter": chain_backward_loop(L, (512, 512), 1000),
+            "reference_published_us_per_iter": {"fwd_64x64_jit": 14.0, "fwd_64x64_eager": 90.0,
+                                                "bwd_512x512_jit": 500.0, "bwd_512x512_eager": 970.0,
+                                                "source": "README.md:126-130, 10,000 iterations"}}
+
+
+def cpu_jit():
+    """The reference's own JIT (oracle/_ref; it compiles the graph with the
+    system C compiler) on the same loops, on this host."""
+    from oracle_lib import REF_SO
+    from picograd_amd.capi import PgLib
+    if not REF_SO.exists():
+        return None
+    R = PgLib(REF_SO, device=False)
+    return {"fwd_64x64_us_per_iter": jit_forward_loop(R, (64, 64), 10000),
+            "fwd_512x512_us_per_iter": jit_forward_loop(R, (512, 512), 200),
+            "fwd_bwd_512x512_us_per_iter": chain_backward_loop(R, (512, 512), 100),
+            "cores": 1, "kind": "reference"}
+
+
 # ---------------------------------------------------------------- config 1
 
 def bench_c1(L, iters=2000):
@@ -649,7 +862,7 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="c2,c3,c4,c1,c5,opt")
+    ap.add_argument("--only", default="c2,c3,c4,c1,c5,opt,ckpt,jit")
     ap.add_argument("--calib", action="store_true",
                     help="first run a plain copy kernel of known size (the HBM counter calibration)")
     ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 counter passes")
@@ -694,6 +907,12 @@ def main(argv=None):
     if "opt" in only:
         extra["opt_adamw_clip_c5_params"] = bench_opt(L, ev, max(3, a.steps), a.warmup)
         log(f"[opt] {extra['opt_adamw_clip_c5_params']}")
+    if "jit" in only:
+        extra["jit_demo"] = bench_jit(L)
+        log(f"[jit] {extra['jit_demo']}")
+    if "ckpt" in only:
+        extra["ckpt_c5_params_and_momentum"] = bench_ckpt(L)
+        log(f"[ckpt] {extra['ckpt_c5_params_and_momentum']}")
     cpu = None
     if not a.no_cpu:
         log("[cpu] reference CPU path, config 2 sample")
@@ -713,6 +932,16 @@ def main(argv=None):
             ocpu = cpu_opt()
             if ocpu:
                 extra.setdefault("opt_adamw_clip_c5_params", {})["cpu_reference"] = ocpu
+        if "ckpt" in only and cpu is not None:
+            log("[cpu] reference CPU path, pg_module_save of config 5's parameters")
+            kcpu = cpu_ckpt()
+            if kcpu:
+                extra.setdefault("ckpt_c5_params_and_momentum", {})["cpu_reference"] = kcpu
+        if "jit" in only and cpu is not None:
+            log("[cpu] reference JIT on jit_demo.c's loops")
+            jcpu = cpu_jit()
+            if jcpu:
+                extra.setdefault("jit_demo", {})["cpu_reference"] = jcpu
     out = {
         "metric": "fused-bwd HBM GB/s",
         "value": round(c2["gbs"], 2),

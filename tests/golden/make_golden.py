@@ -574,6 +574,110 @@ def checkpoint_files(R: PgLib) -> dict:
     return out
 
 
+# pg_jit op codes (jit.h)
+JADD, JSUB, JMUL, JDIV, JNEG, JEXP, JLOG, JSQRT, JSIN, JCOS, JABS, JRELU, JSIGMOID, JTANH, JGELU, JERF, JSTEP = range(17)
+
+
+def _jit_specs():
+    """Forward graphs of the reference's test_jit.c and jit_demo.c, with
+    the inputs fed to them: nodes are ["in", shape], ["const", value] or
+    ["op", code, [ids]]; ids count every node in order."""
+    rng = np.random.default_rng(41)
+    u = lambda shape, lo, hi: rng.uniform(lo, hi, shape).astype(np.float32)
+    specs = []
+    chain = [["in", [64, 64]], ["in", [64, 64]], ["in", [64, 64]], ["op", JADD, [0, 1]], ["op", JMUL, [3, 2]],
+             ["op", JRELU, [4]], ["op", JTANH, [5]]]
+    specs.append(("basic", [["in", [2, 3]]] * 3 + [["op", JADD, [0, 1]], ["op", JMUL, [3, 2]], ["op", JRELU, [4]]],
+                  [5], [np.array([[1, -2, 3], [4, -5, 6]], np.float32), np.array([[6, 5, 4], [3, 2, 1]], np.float32),
+                        np.ones((2, 3), np.float32)]))
+    specs.append(("bcast", [["in", [2, 4]], ["in", [4]], ["op", JADD, [0, 1]], ["op", JRELU, [2]]], [3],
+                  [np.array([[-1, 2, -3, 4], [-5, 6, -7, 8]], np.float32), np.array([10, 20, 30, 40], np.float32)]))
+    specs.append(("bcast3d", [["in", [2, 3, 4]], ["in", [3, 4]], ["in", [4]], ["op", JADD, [0, 1]], ["op", JMUL, [3, 2]]],
+                  [4], [u((2, 3, 4), -2, 2), u((3, 4), -2, 2), u((4,), -2, 2)]))
+    for code, name in ((JNEG, "neg"), (JEXP, "exp"), (JLOG, "log"), (JSQRT, "sqrt"), (JSIN, "sin"), (JCOS, "cos"),
+                       (JABS, "abs"), (JRELU, "relu"), (JSIGMOID, "sigmoid"), (JTANH, "tanh"), (JGELU, "gelu"),
+                       (JERF, "erf"), (JSTEP, "step")):
+        lo, hi = (0.5, 2.0) if code in (JLOG, JSQRT) else (-4.0, 4.0)
+        x = u((1031,), lo, hi)
+        if code not in (JLOG, JSQRT):
+            x[:8] = [0.0, -0.0, 1e-3, -1e-3, 3.9, -3.9, 1e-30, 9.5]
+        specs.append((f"unary_{name}", [["in", [1031]], ["op", code, [0]]], [1], [x]))
+    for code, name in ((JADD, "add"), (JSUB, "sub"), (JMUL, "mul"), (JDIV, "div")):
+        specs.append((f"binary_{name}", [["in", [19, 53]], ["in", [19, 53]], ["op", code, [0, 1]]], [2],
+                      [u((19, 53), -2, 2), u((19, 53), 0.5, 2)]))
+    specs.append(("const", [["in", [2, 4]], ["const", 2.5], ["op", JMUL, [0, 1]], ["op", JRELU, [2]]], [3],
+                  [u((2, 4), -2, 2)]))
+    specs.append(("complex", [["in", [4, 8]], ["in", [8]], ["in", [4, 8]], ["const", 0.5], ["op", JADD, [0, 1]],
+                              ["op", JMUL, [4, 2]], ["op", JADD, [5, 3]], ["op", JTANH, [6]]], [7],
+                  [u((4, 8), -1, 1), u((8,), -0.5, 0.5), u((4, 8), -1, 1)]))
+    specs.append(("multi", [["in", [4]], ["in", [4]], ["op", JADD, [0, 1]], ["op", JMUL, [0, 1]]], [2, 3],
+                  [np.array([1, 2, 3, 4], np.float32), np.array([5, 6, 7, 8], np.float32)]))
+    specs.append(("demo64", chain, [6], [u((64, 64), -1, 1) for _ in range(3)]))
+    specs.append(("gelu_rowbias", [["in", [96, 160]], ["in", [160]], ["in", [96, 160]], ["op", JADD, [0, 1]],
+                                   ["op", JGELU, [3]], ["op", JSIGMOID, [2]], ["op", JMUL, [4, 5]]], [6],
+                  [rng.standard_normal((96, 160)).astype(np.float32),
+                   (0.1 * rng.standard_normal(160)).astype(np.float32),
+                   rng.standard_normal((96, 160)).astype(np.float32)]))
+    return specs
+
+
+def jit_forward(R: PgLib) -> dict:
+    """Forward graphs through the reference's JIT (jit.c:644-806; it
+    compiles each with the system C compiler): test_jit.c's graphs (basic
+    fusion, 2-D and 3-D broadcast, every unary and binary op, a constant,
+    a complex fused chain, two outputs) on larger inputs, and jit_demo.c's
+    (a+b)*c -> relu -> tanh at [64,64]."""
+    import json
+    out, meta = {}, []
+    for name, nodes, outs, inputs in _jit_specs():
+        g = R.pg_jit_graph_new()
+        for nd in nodes:
+            if nd[0] == "in":
+                k, sh = shape_arg(nd[1])
+                assert R.pg_jit_add_input(g, k, sh) >= 0
+            elif nd[0] == "const":
+                assert R.pg_jit_add_const(g, nd[1]) >= 0
+            else:
+                ids = (C.c_int * len(nd[2]))(*nd[2])
+                assert R.pg_jit_add_op(g, nd[1], ids, len(nd[2])) >= 0
+        for o in outs:
+            R.pg_jit_mark_output(g, o)
+        exe = R.pg_jit_compile(g)
+        assert exe, R.pg_jit_last_error()
+        ts = [R.tensor(x) for x in inputs]
+        outs_t = []
+        shapes = _jit_out_shapes(nodes)
+        for o in outs:
+            k, sh = shape_arg(shapes[o])
+            outs_t.append(R.pg_tensor_zeros(k, sh))
+        assert R.pg_jit_run(exe, (C.c_void_p * len(ts))(*ts), len(ts), (C.c_void_p * len(outs_t))(*outs_t),
+                            len(outs_t))
+        for i, x in enumerate(inputs):
+            out[f"{name}_in{i}"] = x
+        for i, t in enumerate(outs_t):
+            out[f"{name}_out{i}"] = R.read(t)
+        for t in ts + outs_t:
+            R.pg_tensor_free(t)
+        R.pg_jit_exe_free(exe)
+        R.pg_jit_graph_free(g)
+        meta.append({"name": name, "nodes": nodes, "outputs": outs, "ninputs": len(inputs)})
+    out["specs"] = np.array(json.dumps(meta))
+    return out
+
+
+def _jit_out_shapes(nodes):
+    """NumPy broadcast shape of every node (consts are scalars)."""
+    shapes = []
+    for nd in nodes:
+        if nd[0] == "in":
+            shapes.append(tuple(nd[1]))
+        elif nd[0] == "const":
+            shapes.append(())
+        else:
+            shapes.append(tuple(np.broadcast_shapes(*[shapes[i] for i in nd[2]])))
+    return shapes
+
+
 CASES = {
     "rng": rng_streams,
     "convert": lambda R: conversions(),
@@ -587,6 +691,7 @@ CASES = {
     "adam": adam_trajectories,
     "clip": clip,
     "ckpt": checkpoint_files,
+    "jit_fwd": jit_forward,
 }
 
 
