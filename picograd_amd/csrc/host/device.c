@@ -69,9 +69,14 @@ int pg_amd_init(void)
 
 bool pgd_ok(void) { return pg_amd_init() == 0; }
 
+static bool up_flush(void);
+static void up_flush_if_overlaps(const void *p, size_t n);
+
 pgk_stream pgd_stream(void)
 {
-    pg_amd_init();
+    /* everything queued from here on sees the pending uploads */
+    if (pg_amd_init() == 0)
+        up_flush();
     return (pgk_stream)g_stream;
 }
 
@@ -81,7 +86,8 @@ bool pgd_sync(void)
 {
     if (!pgd_ok())
         return false;
-    return hip_ok(hipStreamSynchronize(g_stream), "hipStreamSynchronize");
+    bool ok = up_flush();
+    return hip_ok(hipStreamSynchronize(g_stream), "hipStreamSynchronize") && ok;
 }
 
 int pg_amd_sync(void) { return pgd_sync() ? 0 : -1; }
@@ -116,8 +122,10 @@ static size_t bin_of(size_t cls) { return (cls / 256 * 2654435761u) % NBINS; }
 
 static void release_all(void)
 {
-    if (g_init_state > 0)
+    if (g_init_state > 0) {
+        up_flush();
         hipStreamSynchronize(g_stream);
+    }
     for (size_t i = 0; i < NBINS; i++) {
         blk *b = g_bins[i];
         while (b) {
@@ -169,6 +177,7 @@ void pgd_free(void *p, size_t nbytes)
     if (!p)
         return;
     size_t cls = size_class(nbytes ? nbytes : 1);
+    up_flush_if_overlaps(p, cls);
     blk *b = malloc(sizeof *b);
     g_in_use -= cls;
     if (!b) {
@@ -199,25 +208,43 @@ void *pgd_scratch(int slot, size_t nbytes)
     return g_scratch[slot];
 }
 
-/* Small host-to-device copies go through a ring of pinned staging slots so
- * that they queue without a stream sync: the source is copied into the next
- * slot (waiting, if ever, only for that slot's previous copy), and the
- * DMA from the slot is queued on the stream.  Larger copies go straight from
- * pageable memory, which stages them before the call returns. */
+/* Small host-to-device copies (up to 256 KiB) are batched.  The source is
+ * copied into a ring of pinned staging slots that the device reads
+ * directly, and the copy becomes an entry of the pending batch; one scatter
+ * kernel (k_upload) writes the whole batch, launched when anything else is
+ * about to be queued or waited on (pgd_stream, pgd_sync, the copies, the
+ * timer, and a free of a pending destination).  So a run of leaf creations
+ * costs one kernel on the compute queue instead of one DMA each, with no
+ * switch between the copy engine and the compute queue.  A slot is reused
+ * once the last kernel that read it has finished (its event).  Larger
+ * copies go straight from pageable memory, which stages them before the
+ * call returns. */
 #define PGD_STAGE_SLOTS 64
 #define PGD_STAGE_BYTES ((size_t)256 << 10)
-static unsigned char *g_stage;
+static unsigned char *g_stage;     /* host address */
+static unsigned char *g_stage_dev; /* the same memory as the device addresses it */
 static hipEvent_t g_stage_ev[PGD_STAGE_SLOTS];
 static bool g_stage_used[PGD_STAGE_SLOTS];
-static int g_stage_next, g_stage_state; /* 0 = not tried, 1 = ok, -1 = unavailable */
+static int g_stage_state; /* 0 = not tried, 1 = ok, -1 = unavailable */
+static int g_up_slot;
+static size_t g_up_off;
+static pgk_upload g_up[PGK_UPLOAD_MAX];
+static int g_up_n;
 
 static bool stage_ready(void)
 {
     if (g_stage_state)
         return g_stage_state > 0;
     g_stage_state = -1;
-    if (hipHostMalloc((void **)&g_stage, PGD_STAGE_SLOTS * PGD_STAGE_BYTES, hipHostMallocDefault) != hipSuccess) {
+    if (hipHostMalloc((void **)&g_stage, PGD_STAGE_SLOTS * PGD_STAGE_BYTES,
+                      hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess) {
         (void)hipGetLastError();
+        g_stage = NULL;
+        return false;
+    }
+    if (hipHostGetDevicePointer((void **)&g_stage_dev, g_stage, 0) != hipSuccess) {
+        (void)hipGetLastError();
+        hipHostFree(g_stage);
         g_stage = NULL;
         return false;
     }
@@ -235,6 +262,34 @@ static bool stage_ready(void)
     return true;
 }
 
+/* queues the pending batch (no-op when empty) */
+static bool up_flush(void)
+{
+    if (!g_up_n)
+        return true;
+    const int n = g_up_n;
+    g_up_n = 0;
+    bool ok = pgd_check(pgk_upload_scatter(g_up, n, (pgk_stream)g_stream), "upload");
+    g_stage_used[g_up_slot] = hip_ok(hipEventRecord(g_stage_ev[g_up_slot], g_stream), "hipEventRecord");
+    if (!g_stage_used[g_up_slot]) /* no event to wait on later: finish now */
+        ok = hip_ok(hipStreamSynchronize(g_stream), "hipStreamSynchronize") && ok;
+    return ok;
+}
+
+/* a free of device memory a pending entry writes: queue the batch first,
+ * so a later owner of the block is ordered after the write */
+static void up_flush_if_overlaps(const void *p, size_t n)
+{
+    const unsigned char *a = p;
+    for (int i = 0; i < g_up_n; i++) {
+        const unsigned char *d = g_up[i].dst;
+        if (d < a + n && a < d + g_up[i].n) {
+            up_flush();
+            return;
+        }
+    }
+}
+
 bool pgd_h2d(void *dst, const void *src, size_t nbytes)
 {
     if (!nbytes)
@@ -242,19 +297,28 @@ bool pgd_h2d(void *dst, const void *src, size_t nbytes)
     if (!pgd_ok())
         return false;
     if (nbytes <= PGD_STAGE_BYTES && stage_ready()) {
-        const int s = g_stage_next;
-        g_stage_next = (s + 1) % PGD_STAGE_SLOTS;
-        if (g_stage_used[s] && !hip_ok(hipEventSynchronize(g_stage_ev[s]), "hipEventSynchronize"))
-            return false;
-        unsigned char *slot = g_stage + (size_t)s * PGD_STAGE_BYTES;
-        memcpy(slot, src, nbytes);
-        if (!hip_ok(hipMemcpyAsync(dst, slot, nbytes, hipMemcpyHostToDevice, g_stream), "hipMemcpyAsync H2D"))
-            return false;
-        g_stage_used[s] = hip_ok(hipEventRecord(g_stage_ev[s], g_stream), "hipEventRecord");
-        if (!g_stage_used[s])
-            return pgd_sync(); /* no event to wait on later: finish the copy now */
+        up_flush_if_overlaps(dst, nbytes); /* a second write of the same bytes keeps its order */
+        size_t off = (g_up_off + 15) & ~(size_t)15;
+        if (off + nbytes > PGD_STAGE_BYTES || g_up_n == PGK_UPLOAD_MAX) {
+            if (!up_flush())
+                return false;
+            g_up_slot = (g_up_slot + 1) % PGD_STAGE_SLOTS;
+            if (g_stage_used[g_up_slot] && !hip_ok(hipEventSynchronize(g_stage_ev[g_up_slot]), "hipEventSynchronize"))
+                return false;
+            g_stage_used[g_up_slot] = false;
+            off = 0;
+        }
+        const size_t at = (size_t)g_up_slot * PGD_STAGE_BYTES + off;
+        memcpy(g_stage + at, src, nbytes);
+        g_up[g_up_n].dst = dst;
+        g_up[g_up_n].src = g_stage_dev + at;
+        g_up[g_up_n].n = nbytes;
+        g_up_n++;
+        g_up_off = off + nbytes;
         return true;
     }
+    if (!up_flush())
+        return false;
     /* pageable source: the copy is staged before the call returns */
     return hip_ok(hipMemcpyAsync(dst, src, nbytes, hipMemcpyHostToDevice, g_stream),
                   "hipMemcpyAsync H2D") &&
@@ -267,6 +331,8 @@ bool pgd_d2h(void *dst, const void *src, size_t nbytes)
         return false;
     if (!nbytes)
         return pgd_sync();
+    if (!up_flush())
+        return false;
     return hip_ok(hipMemcpyAsync(dst, src, nbytes, hipMemcpyDeviceToHost, g_stream),
                   "hipMemcpyAsync D2H") &&
            hip_ok(hipStreamSynchronize(g_stream), "hipStreamSynchronize");
@@ -277,6 +343,8 @@ bool pgd_d2d(void *dst, const void *src, size_t nbytes)
     if (!nbytes)
         return true;
     if (!pgd_ok())
+        return false;
+    if (!up_flush())
         return false;
     return hip_ok(hipMemcpyAsync(dst, src, nbytes, hipMemcpyDeviceToDevice, g_stream),
                   "hipMemcpyAsync D2D");
@@ -304,6 +372,7 @@ int pgd_tbegin(int kind)
 {
     if (!g_timer_on || !pgd_ok())
         return -1;
+    up_flush();
     if (g_ntev == g_captev) {
         size_t nc = g_captev ? g_captev * 2 : 256;
         tev *p = realloc(g_tev, nc * sizeof *p);

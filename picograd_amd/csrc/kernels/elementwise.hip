@@ -556,7 +556,60 @@ __global__ void __launch_bounds__(64) k_colsum_fin(const float *__restrict__ par
     }
 }
 
+// ---------------------------------------------------------------- uploads
+// One block per 16 KiB of each entry (first[i] = entry i's first block);
+// 16-byte copies when source and destination allow, bytes otherwise.
+struct upload_table {
+    pgk_upload e[PGK_UPLOAD_MAX];
+    unsigned first[PGK_UPLOAD_MAX + 1];
+    int cnt;
+};
+constexpr size_t kUpChunk = (size_t)kBlock * 64;
+
+__global__ void __launch_bounds__(kBlock) k_upload(upload_table tab)
+{
+    const unsigned b = blockIdx.x;
+    int s = 0;
+    for (int i = 1; i < tab.cnt; ++i)
+        s += b >= tab.first[i] ? 1 : 0;
+    const pgk_upload e = tab.e[s];
+    const size_t base = (size_t)(b - tab.first[s]) * kUpChunk;
+    const size_t end = base + kUpChunk < e.n ? base + kUpChunk : e.n;
+    const unsigned char *__restrict__ src = (const unsigned char *)e.src;
+    unsigned char *__restrict__ dst = (unsigned char *)e.dst;
+    if ((((uintptr_t)src) | ((uintptr_t)dst)) % 16 == 0) {
+        for (size_t j = base + 16 * (size_t)threadIdx.x; j + 16 <= end; j += 16 * (size_t)kBlock)
+            *reinterpret_cast<uint4 *>(dst + j) = *reinterpret_cast<const uint4 *>(src + j);
+        for (size_t j = (end & ~(size_t)15) + threadIdx.x; j < end; j += kBlock) // the last 0-15 bytes
+            dst[j] = src[j];
+    } else {
+        for (size_t j = base + threadIdx.x; j < end; j += kBlock)
+            dst[j] = src[j];
+    }
+}
+
 } // namespace
+
+extern "C" int pgk_upload_scatter(const pgk_upload *ents, int n, pgk_stream s)
+{
+    if (n <= 0)
+        return 0;
+    if (n > PGK_UPLOAD_MAX)
+        return (int)hipErrorInvalidValue;
+    upload_table tab = {};
+    unsigned blocks = 0;
+    for (int q = 0; q < n; ++q) {
+        tab.e[q] = ents[q];
+        tab.first[q] = blocks;
+        blocks += (unsigned)((ents[q].n + kUpChunk - 1) / kUpChunk);
+    }
+    tab.first[n] = blocks;
+    tab.cnt = n;
+    if (!blocks)
+        return 0;
+    hipLaunchKernelGGL(k_upload, dim3(blocks), dim3(kBlock), 0, (hipStream_t)s, tab);
+    return status();
+}
 
 // ---------------------------------------------------------------- launchers
 

@@ -36,6 +36,18 @@ typedef struct {
 } pgk_bcast;
 
 int pgk_fill_f32(float *dst, size_t n, float v, pgk_stream s);
+
+/* A batch of small uploads written by one kernel: dst[0..n) = src[0..n)
+ * for each entry, src in pinned host memory the device reads directly (a
+ * device address of it).  At most PGK_UPLOAD_MAX entries per call; the
+ * destinations must not overlap. */
+#define PGK_UPLOAD_MAX 32
+typedef struct {
+    void *dst;
+    const void *src;
+    size_t n;
+} pgk_upload;
+int pgk_upload_scatter(const pgk_upload *ents, int n, pgk_stream s);
 int pgk_fill_u16(uint16_t *dst, size_t n, uint16_t v, pgk_stream s);
 
 /* y = op(x) */
