@@ -269,6 +269,246 @@ static bool bcast_desc(const pg_tensor *a, const pg_tensor *b, size_t *ond, size
     return true;
 }
 
+/* ---------------------------------------------------------------- deferred forward ops
+ * With the JIT on, elementwise forward ops on f32 tensors are recorded
+ * rather than launched.  Each gets its output allocated at once (the node's
+ * value has its address and shape from the start), and the run of recorded
+ * ops executes as ONE fused kernel that writes every op's output, when
+ * anything else is about to be queued on the stream or waited on (the
+ * device layer calls pga_lazy_flush at each such point: every launch,
+ * copy, sync and upload).  The values are the eager kernels' bit for bit:
+ * each op calls the same device function, and the fused body is compiled
+ * without contracting one op's product into another's sum.  A run keeps one
+ * output shape and at most 16 ops and 16 distinct inputs; a recorded op
+ * holds a reference on its operands' and output's storage until it runs,
+ * so freeing a node in between recycles nothing the run still touches. */
+#define LZ_MAX 16
+
+typedef struct {
+    pg_data_ref *ref; /* one reference held while pending */
+    void *dev;
+    size_t ndim, shape[PG_MAX_NDIM];
+} lz_tensor;
+
+typedef struct {
+    int code;  /* PG_JIT_* */
+    int nin;
+    int in[2]; /* >= 0: run input; < 0: -(k + 1) = output of op k */
+    lz_tensor out;
+} lz_op;
+
+static struct {
+    int nops, nin;
+    lz_op op[LZ_MAX];
+    lz_tensor in[LZ_MAX];
+    size_t ndim, shape[PG_MAX_NDIM];
+    bool flushing;
+} g_lz;
+
+bool pga_lazy_pending(void) { return g_lz.nops > 0; }
+
+static int lz_unary_code(int pgk)
+{
+    switch (pgk) {
+    case PGK_NEG: return PG_JIT_NEG;
+    case PGK_EXP: return PG_JIT_EXP;
+    case PGK_LOG: return PG_JIT_LOG;
+    case PGK_SQRT: return PG_JIT_SQRT;
+    case PGK_SIN: return PG_JIT_SIN;
+    case PGK_COS: return PG_JIT_COS;
+    case PGK_RELU: return PG_JIT_RELU;
+    case PGK_SIGMOID: return PG_JIT_SIGMOID;
+    case PGK_TANH: return PG_JIT_TANH;
+    case PGK_GELU: return PG_JIT_GELU;
+    case PGK_ERF: return PG_JIT_ERF;
+    case PGK_ABS: return PG_JIT_ABS;
+    default: return -1; /* parameterised ops run eagerly */
+    }
+}
+
+static int lz_binary_code(int pgk)
+{
+    switch (pgk) {
+    case PGK_ADD: return PG_JIT_ADD;
+    case PGK_SUB: return PG_JIT_SUB;
+    case PGK_MUL: return PG_JIT_MUL;
+    case PGK_DIV: return PG_JIT_DIV;
+    default: return -1;
+    }
+}
+
+static void lz_hold(lz_tensor *d, pg_data_ref *ref, void *dev, size_t ndim, const size_t *shape)
+{
+    d->ref = ref;
+    ref->refs++;
+    d->dev = dev;
+    d->ndim = ndim;
+    memcpy(d->shape, shape, ndim * sizeof(size_t));
+}
+
+/* a stand-in tensor over a pending run's storage, for the launchers */
+static void lz_view(pg_tensor *t, const lz_tensor *x)
+{
+    memset(t, 0, sizeof *t);
+    t->ndim = x->ndim;
+    memcpy(t->shape, x->shape, x->ndim * sizeof(size_t));
+    pgt_set_contig_strides(t);
+    t->numel = pg_shape_numel(x->ndim, x->shape);
+    t->dtype = PG_DTYPE_F32;
+    t->elem_size = 4;
+    t->dev = x->dev;
+    t->data_ref = x->ref;
+}
+
+static bool lz_same(const lz_tensor *x, const pg_tensor *t)
+{
+    return x->dev == t->dev && pg_shape_equal(x->ndim, x->shape, t->ndim, t->shape);
+}
+
+static bool lz_overlaps(const lz_tensor *x, const pg_tensor *t)
+{
+    const char *a = x->dev, *b = t->dev;
+    const size_t na = pg_shape_numel(x->ndim, x->shape) * 4, nb = t->numel * t->elem_size;
+    return a < b + nb && b < a + na;
+}
+
+/* where operand t comes from in the current run: op output (-(k+1)), run
+ * input (>= 0), new input (LZ_MAX), or -LZ_MAX - 1 when it overlaps a
+ * pending output without being one (the run must go first) */
+static int lz_find(const pg_tensor *t)
+{
+    for (int k = 0; k < g_lz.nops; k++) {
+        if (lz_same(&g_lz.op[k].out, t))
+            return -(k + 1);
+        if (lz_overlaps(&g_lz.op[k].out, t))
+            return -LZ_MAX - 1;
+    }
+    for (int j = 0; j < g_lz.nin; j++)
+        if (lz_same(&g_lz.in[j], t))
+            return j;
+    return LZ_MAX;
+}
+
+/* eager launch of recorded op k (when the fused kernel is unavailable) */
+static bool lz_run_eager(int k)
+{
+    const lz_op *o = &g_lz.op[k];
+    pg_tensor x[2], y;
+    for (int i = 0; i < o->nin; i++)
+        lz_view(&x[i], o->in[i] >= 0 ? &g_lz.in[o->in[i]] : &g_lz.op[-o->in[i] - 1].out);
+    lz_view(&y, &o->out);
+    if (o->nin == 1) {
+        int code = -1;
+        for (int c = 0; c < PGK_UNARY_COUNT && code < 0; c++)
+            if (lz_unary_code(c) == o->code)
+                code = c;
+        return pgd_check(pgk_unary_f32(code, x[0].dev, y.dev, y.numel, 0.0f, 0.0f, pgd_stream()), "unary");
+    }
+    size_t nd, shp[PG_MAX_NDIM];
+    pgk_bcast bc;
+    if (!bcast_desc(&x[0], &x[1], &nd, shp, &bc))
+        return false;
+    return pgd_check(pgk_binary_f32(o->code - PG_JIT_ADD + PGK_ADD, x[0].dev, x[1].dev, y.dev, &bc, pgd_stream()),
+                     "binary");
+}
+
+void pga_lazy_flush(void)
+{
+    if (!g_lz.nops || g_lz.flushing)
+        return;
+    g_lz.flushing = true;
+    bool ok = false;
+    pg_jit_graph *g = pg_jit_graph_new();
+    if (g) {
+        pgj_graph_set_exact(g);
+        int idi[LZ_MAX], ido[LZ_MAX];
+        bool built = true;
+        for (int j = 0; j < g_lz.nin && built; j++)
+            built = (idi[j] = pg_jit_add_input(g, g_lz.in[j].ndim, g_lz.in[j].shape)) >= 0;
+        for (int k = 0; k < g_lz.nops && built; k++) {
+            int args[2];
+            for (int i = 0; i < g_lz.op[k].nin; i++)
+                args[i] = g_lz.op[k].in[i] >= 0 ? idi[g_lz.op[k].in[i]] : ido[-g_lz.op[k].in[i] - 1];
+            built = (ido[k] = pg_jit_add_op(g, (pg_jit_op_t)g_lz.op[k].code, args, (size_t)g_lz.op[k].nin)) >= 0;
+        }
+        for (int k = 0; k < g_lz.nops && built; k++)
+            pg_jit_mark_output(g, ido[k]);
+        pg_jit_exe *exe = built ? pg_jit_compile(g) : NULL;
+        if (exe) {
+            pg_tensor tin[LZ_MAX], tout[LZ_MAX];
+            const pg_tensor *pin[LZ_MAX];
+            pg_tensor *pout[LZ_MAX];
+            for (int j = 0; j < g_lz.nin; j++) {
+                lz_view(&tin[j], &g_lz.in[j]);
+                pin[j] = &tin[j];
+            }
+            for (int k = 0; k < g_lz.nops; k++) {
+                lz_view(&tout[k], &g_lz.op[k].out);
+                pout[k] = &tout[k];
+            }
+            ok = pg_jit_run(exe, pin, (size_t)g_lz.nin, pout, (size_t)g_lz.nops);
+            pg_jit_exe_free(exe);
+        }
+        pg_jit_graph_free(g);
+    }
+    for (int k = 0; k < g_lz.nops && !ok; k++)
+        if (!lz_run_eager(k)) /* the device error is recorded; the rest are not run */
+            break;
+    for (int j = 0; j < g_lz.nin; j++)
+        pgt_ref_release(g_lz.in[j].ref);
+    for (int k = 0; k < g_lz.nops; k++)
+        pgt_ref_release(g_lz.op[k].out.ref);
+    g_lz.nops = g_lz.nin = 0;
+    g_lz.flushing = false;
+}
+
+/* records y = op(x...) into the run; NULL when the op must run eagerly
+ * (nothing recorded then) */
+static pg_tensor *lz_record(int code, int nin, const pg_tensor *const *x, size_t nd, const size_t *shape)
+{
+    if (code < 0 || !pg_autograd_is_jit_enabled() || g_lz.flushing)
+        return NULL;
+    if (g_lz.nops && (g_lz.nops == LZ_MAX || !pg_shape_equal(nd, shape, g_lz.ndim, g_lz.shape)))
+        pga_lazy_flush();
+    int src[2], fresh = 0;
+    for (int i = 0; i < nin; i++) {
+        src[i] = lz_find(x[i]);
+        if (src[i] == -LZ_MAX - 1) {
+            pga_lazy_flush();
+            return lz_record(code, nin, x, nd, shape);
+        }
+        fresh += src[i] == LZ_MAX && !(i == 1 && x[1] == x[0]) ? 1 : 0;
+    }
+    if (g_lz.nin + fresh > LZ_MAX) {
+        pga_lazy_flush();
+        return lz_record(code, nin, x, nd, shape);
+    }
+    pg_tensor *y = pgt_alloc(PG_DTYPE_F32, nd, shape);
+    if (!y)
+        return NULL;
+    if (!g_lz.nops) {
+        g_lz.ndim = nd;
+        memcpy(g_lz.shape, shape, nd * sizeof(size_t));
+    }
+    lz_op *o = &g_lz.op[g_lz.nops];
+    o->code = code;
+    o->nin = nin;
+    for (int i = 0; i < nin; i++) {
+        if (src[i] == LZ_MAX) {
+            if (i == 1 && x[1] == x[0]) {
+                src[1] = src[0];
+            } else {
+                lz_hold(&g_lz.in[g_lz.nin], x[i]->data_ref, x[i]->dev, x[i]->ndim, x[i]->shape);
+                src[i] = g_lz.nin++;
+            }
+        }
+        o->in[i] = src[i];
+    }
+    lz_hold(&o->out, y->data_ref, y->dev, nd, shape);
+    g_lz.nops++;
+    return y;
+}
+
 static pg_tensor *binary_fwd(int op, const pg_tensor *a, const pg_tensor *b)
 {
     if (!need_f32(a, "binary op") || !need_f32(b, "binary op"))
@@ -279,7 +519,10 @@ static pg_tensor *binary_fwd(int op, const pg_tensor *a, const pg_tensor *b)
         pga_set_err("binary op: incompatible broadcast shapes");
         return NULL;
     }
-    pg_tensor *y = pgt_alloc(PG_DTYPE_F32, nd, shp);
+    pg_tensor *y = lz_record(lz_binary_code(op), 2, (const pg_tensor *[]){a, b}, nd, shp);
+    if (y)
+        return y;
+    y = pgt_alloc(PG_DTYPE_F32, nd, shp);
     if (!y)
         return NULL;
     if (!pgd_check(pgk_binary_f32(op, (const float *)a->dev, (const float *)b->dev, (float *)y->dev, &bc,
@@ -295,7 +538,10 @@ static pg_tensor *unary_fwd(int op, const pg_tensor *a, float p0, float p1)
 {
     if (!need_f32(a, "unary op"))
         return NULL;
-    pg_tensor *y = pgt_alloc(PG_DTYPE_F32, a->ndim, a->shape);
+    pg_tensor *y = lz_record(lz_unary_code(op), 1, (const pg_tensor *[]){a}, a->ndim, a->shape);
+    if (y)
+        return y;
+    y = pgt_alloc(PG_DTYPE_F32, a->ndim, a->shape);
     if (!y)
         return NULL;
     if (!pgd_check(pgk_unary_f32(op, (const float *)a->dev, (float *)y->dev, a->numel, p0, p1, pgd_stream()),

@@ -72,11 +72,20 @@ bool pgd_ok(void) { return pg_amd_init() == 0; }
 static bool up_flush(void);
 static void up_flush_if_overlaps(const void *p, size_t n);
 
+/* queues what is pending: the batched uploads, then the deferred forward
+ * ops (which may read them) */
+static bool flush_pending(void)
+{
+    bool ok = up_flush();
+    pga_lazy_flush();
+    return ok;
+}
+
 pgk_stream pgd_stream(void)
 {
-    /* everything queued from here on sees the pending uploads */
+    /* everything queued from here on is ordered after the pending work */
     if (pg_amd_init() == 0)
-        up_flush();
+        flush_pending();
     return (pgk_stream)g_stream;
 }
 
@@ -86,7 +95,7 @@ bool pgd_sync(void)
 {
     if (!pgd_ok())
         return false;
-    bool ok = up_flush();
+    bool ok = flush_pending();
     return hip_ok(hipStreamSynchronize(g_stream), "hipStreamSynchronize") && ok;
 }
 
@@ -123,7 +132,7 @@ static size_t bin_of(size_t cls) { return (cls / 256 * 2654435761u) % NBINS; }
 static void release_all(void)
 {
     if (g_init_state > 0) {
-        up_flush();
+        flush_pending();
         hipStreamSynchronize(g_stream);
     }
     for (size_t i = 0; i < NBINS; i++) {
@@ -296,6 +305,9 @@ bool pgd_h2d(void *dst, const void *src, size_t nbytes)
         return true;
     if (!pgd_ok())
         return false;
+    /* deferred ops recorded before this copy may read what it overwrites */
+    if (pga_lazy_pending() && !flush_pending())
+        return false;
     if (nbytes <= PGD_STAGE_BYTES && stage_ready()) {
         up_flush_if_overlaps(dst, nbytes); /* a second write of the same bytes keeps its order */
         size_t off = (g_up_off + 15) & ~(size_t)15;
@@ -331,7 +343,7 @@ bool pgd_d2h(void *dst, const void *src, size_t nbytes)
         return false;
     if (!nbytes)
         return pgd_sync();
-    if (!up_flush())
+    if (!flush_pending())
         return false;
     return hip_ok(hipMemcpyAsync(dst, src, nbytes, hipMemcpyDeviceToHost, g_stream),
                   "hipMemcpyAsync D2H") &&
@@ -344,7 +356,7 @@ bool pgd_d2d(void *dst, const void *src, size_t nbytes)
         return true;
     if (!pgd_ok())
         return false;
-    if (!up_flush())
+    if (!flush_pending())
         return false;
     return hip_ok(hipMemcpyAsync(dst, src, nbytes, hipMemcpyDeviceToDevice, g_stream),
                   "hipMemcpyAsync D2D");
@@ -372,7 +384,7 @@ int pgd_tbegin(int kind)
 {
     if (!g_timer_on || !pgd_ok())
         return -1;
-    up_flush();
+    flush_pending();
     if (g_ntev == g_captev) {
         size_t nc = g_captev ? g_captev * 2 : 256;
         tev *p = realloc(g_tev, nc * sizeof *p);

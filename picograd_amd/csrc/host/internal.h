@@ -47,6 +47,9 @@ void pgd_tend(int slot);
 pg_tensor *pgt_alloc(pg_dtype dtype, size_t ndim, const size_t *shape);
 void pgt_set_contig_strides(pg_tensor *t);
 bool pgt_is_contiguous(const pg_tensor *t);
+/* drops one reference to a storage block, freeing it (and its 16-bit
+ * copy) with the last */
+void pgt_ref_release(pg_data_ref *r);
 /* materialise a pending zero (grad tensors) */
 void pgt_materialize(pg_tensor *t);
 /* 16-bit (RNE) copy of an f32 tensor's elements, kept with its storage:
@@ -68,6 +71,18 @@ bool pgc_file_to_dev(void *dev, size_t nbytes, FILE *fp);
 /* reads one PGT1 record into dst's storage if dtype and shape match;
  * dst is left unchanged otherwise */
 bool pgc_load_into(pg_tensor *dst, FILE *fp);
+
+/* ---- deferred forward ops (autograd.c) ----
+ * elementwise forward ops recorded while the JIT is on and run as one fused
+ * kernel by pga_lazy_flush(), which the device layer calls before anything
+ * else is queued or waited on */
+bool pga_lazy_pending(void);
+void pga_lazy_flush(void);
+
+/* ---- JIT internals (jit.c) ---- */
+/* the graph's kernel is compiled without contracting a product and a sum
+ * into one FMA, so it computes what separate kernels per op compute */
+void pgj_graph_set_exact(pg_jit_graph *g);
 
 /* ---- RNG (tensor.c) ---- */
 void pg_rng_uniform_host(float *out, size_t n, float low, float high);

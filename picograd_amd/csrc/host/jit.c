@@ -62,6 +62,7 @@ struct pg_jit_graph {
     size_t nin;
     jout outs[MAXIO * 2];
     size_t nout;
+    bool exact; /* no FMA contraction between the graph's ops (pgj_graph_set_exact) */
 };
 
 /* one compiled kernel for one (graph, loop shape) */
@@ -113,6 +114,12 @@ size_t pg_amd_jit_cache_hits(void) { return pgj_stat_hits; }
 /* ---------------------------------------------------------------- graph */
 
 pg_jit_graph *pg_jit_graph_new(void) { return calloc(1, sizeof(pg_jit_graph)); }
+
+void pgj_graph_set_exact(pg_jit_graph *g)
+{
+    if (g)
+        g->exact = true;
+}
 
 void pg_jit_graph_free(pg_jit_graph *g)
 {
@@ -352,6 +359,8 @@ uint64_t pg_jit_graph_hash(const pg_jit_graph *g)
     h = fnv(&g->nn, sizeof g->nn, h);
     h = fnv(&g->nin, sizeof g->nin, h);
     h = fnv(&g->nout, sizeof g->nout, h);
+    if (g->exact)
+        h = fnv("exact", 5, h);
     for (size_t i = 0; i < g->nn; i++) {
         const jnode *n = &g->nodes[i];
         h = fnv(&n->kind, sizeof n->kind, h);
@@ -376,7 +385,7 @@ uint64_t pg_jit_graph_hash(const pg_jit_graph *g)
 
 static bool graph_equal(const pg_jit_graph *a, const pg_jit_graph *b)
 {
-    if (a->nn != b->nn || a->nin != b->nin || a->nout != b->nout)
+    if (a->nn != b->nn || a->nin != b->nin || a->nout != b->nout || a->exact != b->exact)
         return false;
     for (size_t i = 0; i < a->nn; i++) {
         const jnode *x = &a->nodes[i], *y = &b->nodes[i];
@@ -811,6 +820,8 @@ static char *gen_source(const pg_jit_graph *g, const plan_t *P, const bool *reac
          * copies' loads issued before either copy's math */
         int vec = P->vec;
         sb_add(&b, "extern \"C\" __global__ void __launch_bounds__(256) pgjit_main(PgArgs a) {\n");
+        if (g->exact)
+            sb_add(&b, "#pragma clang fp contract(off)\n");
         emit_prologue(&b, P);
         sb_add(&b, "  const IDX N = (IDX)%lldULL;\n", (long long)P->numel);
         sb_add(&b, "  const IDX step = (IDX)gridDim.x * 256u * %du;\n", vec);
@@ -834,6 +845,8 @@ static char *gen_source(const pg_jit_graph *g, const plan_t *P, const bool *reac
      * lane walking rows r, r+4, ... of its block's band, two per iteration */
     int vec = (P->C % 4 == 0 && P->vec == 4) ? 4 : 1;
     sb_add(&b, "extern \"C\" __global__ void __launch_bounds__(256) pgjit_main(PgArgs a) {\n");
+    if (g->exact)
+        sb_add(&b, "#pragma clang fp contract(off)\n");
     emit_prologue(&b, P);
     sb_add(&b, "  const IDX R = (IDX)%lldULL, C = (IDX)%lldULL;\n", (long long)P->R, (long long)P->C);
     sb_add(&b, "  const IDX tc = threadIdx.x & 63u, tr = threadIdx.x >> 6;\n");

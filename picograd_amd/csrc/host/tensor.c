@@ -79,17 +79,21 @@ pg_tensor *pgt_alloc(pg_dtype dtype, size_t ndim, const size_t *shape)
     return t;
 }
 
-void pg_tensor_free(pg_tensor *t)
+void pgt_ref_release(pg_data_ref *r)
 {
-    if (!t)
-        return;
-    if (t->data_ref && --t->data_ref->refs == 0) {
-        pg_data_ref *r = t->data_ref;
+    if (r && --r->refs == 0) {
         pgd_free(r->ptr, r->nbytes);
         if (r->shadow)
             pgd_free(r->shadow, r->nbytes / 2);
         free(r);
     }
+}
+
+void pg_tensor_free(pg_tensor *t)
+{
+    if (!t)
+        return;
+    pgt_ref_release(t->data_ref);
     free(t->data_raw);
     free(t);
 }

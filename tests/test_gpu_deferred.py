@@ -1,0 +1,157 @@
+"""Deferred elementwise forward ops: with the JIT on, runs of elementwise ops
+execute as one fused kernel when their values are first needed.  Every value
+must equal what the eager kernels (JIT off) compute, bit for bit, whatever
+the run looks like and whatever happens to its operands meanwhile."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+UNARY = ["neg", "exp", "log", "sqrt", "sin", "cos", "relu", "sigmoid", "tanh", "gelu", "erf", "abs"]
+BINARY = ["add", "sub", "mul", "div"]
+
+
+def bits(x):
+    return np.asarray(x, np.float32).view(np.uint32)
+
+
+def run_both(lib, build):
+    """build(lib) -> (nodes_to_read, nodes_to_free); values with the JIT on
+    (deferred) and off (eager)."""
+    out = {}
+    for jit in (True, False):
+        lib.pg_autograd_set_jit(jit)
+        try:
+            read, made = build(lib)
+            out[jit] = [lib.value(n) for n in read]
+            for n in reversed(made):
+                lib.pg_node_free(n)
+        finally:
+            lib.pg_autograd_set_jit(True)
+    return out[True], out[False]
+
+
+@pytest.mark.parametrize("op", UNARY)
+def test_unary_deferred_equals_eager(lib, op):
+    rng = np.random.default_rng(UNARY.index(op))
+    x = rng.uniform(0.1, 3.0, 5000).astype(np.float32) if op in ("log", "sqrt") else \
+        rng.standard_normal(5000).astype(np.float32) * 3
+
+    def build(L):
+        a = L.var(x)
+        y = L.op(op, a)
+        z = L.op(op, y) if op not in ("log", "sqrt") else L.op("abs", y)  # a run of two
+        return [y, z], [a, y, z]
+
+    d, e = run_both(lib, build)
+    for u, v in zip(d, e):
+        assert np.array_equal(bits(u), bits(v))
+
+
+@pytest.mark.parametrize("op", BINARY)
+def test_binary_broadcast_deferred_equals_eager(lib, op):
+    rng = np.random.default_rng(10 + BINARY.index(op))
+    x = rng.standard_normal((37, 64)).astype(np.float32)
+    b = rng.uniform(0.5, 2.0, 64).astype(np.float32)
+    c = rng.uniform(0.5, 2.0, (37, 1)).astype(np.float32)
+
+    def build(L):
+        nx, nb, nc = L.var(x), L.var(b), L.var(c)
+        y = L.op(op, nx, nb)   # row broadcast
+        z = L.op(op, y, nc)    # column broadcast
+        w = L.op(op, z, z)     # the same operand twice
+        return [y, z, w], [nx, nb, nc, y, z, w]
+
+    d, e = run_both(lib, build)
+    for u, v in zip(d, e):
+        assert np.array_equal(bits(u), bits(v))
+
+
+def test_config_chains_deferred_equal_eager(lib):
+    """Config 1's chain, config 2's forward, an mse tail and a 40-op chain
+    over 20 leaves (runs of at most 16 ops and 16 inputs), read back at the
+    end and once in the middle."""
+    rng = np.random.default_rng(3)
+    a, b, c = (rng.uniform(-1, 1, (64, 64)).astype(np.float32) for _ in range(3))
+    x = rng.standard_normal((96, 160)).astype(np.float32)
+    bias = (0.1 * rng.standard_normal(160)).astype(np.float32)
+    g = rng.standard_normal((96, 160)).astype(np.float32)
+    leaves = [rng.uniform(0.5, 1.5, (33, 7)).astype(np.float32) for _ in range(20)]
+
+    def build(L):
+        made = []
+        na, nb, nc = (L.var(v) for v in (a, b, c))
+        t = L.op("tanh", L.op("relu", L.op("mul", L.op("add", na, nb), nc)))
+        made += [na, nb, nc]
+        nx, nbias, ng = L.var(x), L.var(bias), L.var(g)
+        z = L.op("add", nx, nbias)
+        mid = L.value(z)  # a read in the middle of a run
+        y = L.op("mul", L.op("gelu", z), L.op("sigmoid", ng))
+        d = L.op("sub", y, nx)
+        sq = L.op("mul", d, d)
+        made += [nx, nbias, ng]
+        ls = [L.var(v) for v in leaves]
+        acc = ls[0]
+        for i in range(1, 40):
+            acc = L.op("mul" if i % 2 else "add", acc, ls[i % 20])
+            acc = L.op("sigmoid", acc) if i % 5 == 0 else acc
+        made += ls
+        return [t, z, y, sq, acc], made + [t, z, y, d, sq, acc]
+
+    d, e = run_both(lib, build)
+    for u, v in zip(d, e):
+        assert np.array_equal(bits(u), bits(v))
+
+
+def test_operand_changes_after_recording(lib):
+    """An op recorded before its operand is overwritten (copy_from_host,
+    fill) or freed computes from the operand as it was, as the eager op
+    would; storage freed while a run is pending is not recycled into it."""
+    lib.pg_autograd_set_jit(True)
+    x0 = np.arange(1, 1001, dtype=np.float32)
+    nx = lib.var(x0)
+    y = lib.op("mul", nx, nx)
+    assert lib.pg_tensor_copy_from_host(lib.node(nx).value, (-x0).ctypes.data)
+    z = lib.op("add", nx, nx)
+    assert np.array_equal(lib.value(y), x0 * x0)
+    assert np.array_equal(lib.value(z), -2 * x0)
+    w = lib.op("exp", nx)
+    lib.pg_tensor_fill(lib.node(nx).value, 0.0)
+    assert np.array_equal(bits(lib.value(w)), bits(np.exp(-x0.astype(np.float64)).astype(np.float32))) or \
+        np.allclose(lib.value(w), np.exp(-x0), rtol=1e-6)
+    for n in (y, z, w, nx):
+        lib.pg_node_free(n)
+    vals = []
+    for i in range(30):
+        a = lib.var(np.full(4096, float(i), np.float32))
+        b = lib.op("add", a, a)
+        lib.pg_node_free(a)     # the run still needs a's storage
+        c = lib.var(np.full(4096, 100.0 + i, np.float32))  # may not land on a's block
+        d = lib.op("mul", b, c)
+        vals.append((b, c, d, i))
+    for b, c, d, i in vals:
+        assert np.all(lib.value(b) == 2.0 * i) and np.all(lib.value(d) == 2.0 * i * (100.0 + i))
+        for n in (d, c, b):
+            lib.pg_node_free(n)
+
+
+def test_backward_through_deferred_values(lib, oracle):
+    """pg_backward right after deferred ops: the fused backward reads the
+    run's inputs and its grads equal the oracle's (config 1 chain)."""
+    import ctypes as C
+    lib.pg_autograd_set_jit(True)
+    oracle.orc_seed(11)
+    a, b, c = (oracle.uniform(4096, -1.0, 1.0).reshape(64, 64) for _ in range(3))
+    na, nb, nc = lib.var(a), lib.var(b), lib.var(c)
+    t3 = lib.op("tanh", lib.op("relu", lib.op("mul", lib.op("add", na, nb), nc)))
+    loss = lib.op("sum_all", t3)
+    lib.pg_backward(loss)
+    da, db, dc = oracle.chain1(a.ravel(), b.ravel(), c.ravel())
+    for n, want in ((na, da), (nb, db), (nc, dc)):
+        assert np.max(np.abs(lib.grad(n).ravel() - want)) <= 1e-6
+    want_loss = np.tanh(np.maximum((a.astype(np.float64) + b) * c, 0)).sum()
+    assert abs(float(lib.value(loss)[0]) - want_loss) <= 1e-3
+    for n in (loss, t3, na, nb, nc):
+        lib.pg_node_free(n)
