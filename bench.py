@@ -797,6 +797,22 @@ def chain_backward_loop(X, shape, iters):
     return (time.perf_counter() - t0) / iters * 1e6
 
 
+def cpu_c1():
+    """The reference's own config-1 loop (oracle/_ref) on this host, with
+    its JIT on and off (it runs single-threaded)."""
+    from oracle_lib import REF_SO
+    from picograd_amd.capi import PgLib
+    if not REF_SO.exists():
+        return None
+    R = PgLib(REF_SO, device=False)
+    jit = chain_backward_loop(R, (64, 64), 3000)
+    R.pg_autograd_set_jit(False)
+    eager = chain_backward_loop(R, (64, 64), 3000)
+    R.pg_autograd_set_jit(True)
+    return {"value": jit, "unit": "us/iter", "eager_us_per_iter": eager, "cores": 1, "kind": "reference",
+            "sample": "3000 iterations of the config-1 loop, JIT on (value) and off"}
+
+
 def bench_jit(L):
     """jit_demo.c's workloads on the device: the fused forward at [64,64]
     (10,000 iterations, as the demo) and [512,512], and the chain's
@@ -937,6 +953,11 @@ def main(argv=None):
             kcpu = cpu_ckpt()
             if kcpu:
                 extra.setdefault("ckpt_c5_params_and_momentum", {})["cpu_reference"] = kcpu
+        if "c1" in only and cpu is not None:
+            log("[cpu] reference CPU path, config 1 loop")
+            c1cpu = cpu_c1()
+            if c1cpu:
+                extra.setdefault("c1_chain_64x64", {})["cpu_reference"] = c1cpu
         if "jit" in only and cpu is not None:
             log("[cpu] reference JIT on jit_demo.c's loops")
             jcpu = cpu_jit()
