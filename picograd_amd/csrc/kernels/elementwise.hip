@@ -800,12 +800,13 @@ extern "C" int pgk_sgd_multi(const pgk_sgd_seg *segs, int nseg, float lr, float 
     return 0;
 }
 
-// rows per block of k_act_bwd16: a multiple of 16 giving about 2048 blocks
-// (fewer for narrow grads)
+// rows per block of k_act_bwd16: a multiple of 16 giving about 1024 blocks
+// (fewer for narrow grads); measured on config 5's [4096, 4096] grads,
+// 1024 blocks of 8 rows per lane beat 2048 of 4 (7 %) and 512 of 16
 static size_t act_bwd_rpb(size_t m, size_t ldd)
 {
     const size_t xb = (ldd + 127) / 128;
-    size_t nrb = 2048 / (xb ? xb : 1);
+    size_t nrb = 1024 / (xb ? xb : 1);
     if (nrb > 64)
         nrb = 64; // the finisher adds at most 64 partials per column
     if (nrb < 1)
