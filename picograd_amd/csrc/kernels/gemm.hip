@@ -8,10 +8,10 @@
 // dgrad (dC . W^T), wgrad (A^T . dC) and the forward product (A . W) all
 // read their operands where they lie, with no transposed copies.
 //
-// Data path, per block tile BM x BN x 64:
+// Data path, per block tile BM x BN x KB (KB = 32 or 64):
 //  - global -> LDS directly (global_load_lds_dwordx4: 64 lanes x 16 bytes
-//    per instruction, no staging registers) into a two-stage LDS ring; the
-//    next k-tile's loads are in flight while the current one is computed;
+//    per instruction, no staging registers) into an S-stage LDS ring; the
+//    next S - 1 k-tiles' loads are in flight while one is computed;
 //  - K-contiguous tiles sit in LDS as [rows][64] with 16-byte chunks
 //    XOR-swizzled by (r ^ r >> 3) & 7 and reach the MFMA with ds_read_b128;
 //    MN-contiguous tiles sit as [64][rows] with chunks swizzled by
@@ -19,7 +19,8 @@
 //    LDS read (within each 16-lane group, lane i of the result takes element
 //    i % 4 of the 8 bytes lane 4p + i / 4 addressed, for slot p);
 //  - fragment reads for the next 16-wide k step are issued before the MFMAs
-//    of the current one;
+//    of the current one, and the k-loop has no branches between two
+//    barriers, so each MFMA waits only for its own fragments;
 //  - tiles are remapped so the blocks that share operand panels run on one
 //    XCD (and its L2), grouped 8 tile-rows at a time.
 // A partial last k-tile loads zeros past K: its out-of-range chunks (K % 8
@@ -61,9 +62,10 @@ __device__ __forceinline__ float act_f(int act, float v)
     return v;
 }
 
-// s_waitcnt immediate waiting for vmcnt <= n only (gfx9 encoding: vmcnt in
-// bits 3:0 and 15:14; expcnt 6:4 and lgkmcnt 11:8 left at their maxima)
-constexpr int vmcnt_imm(int n) { return (n & 0xF) | 0x70 | 0xF00 | (((n >> 4) & 3) << 14); }
+// s_waitcnt immediate waiting for vmcnt <= n and lgkmcnt == 0 (gfx9
+// encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4 left at its maximum,
+// lgkmcnt 11:8)
+constexpr int vmcnt_lgkm0_imm(int n) { return (n & 0xF) | 0x70 | (((n >> 4) & 3) << 14); }
 
 template <bool F16>
 __device__ __forceinline__ f32x16 mfma32(const uint4 &a, const uint4 &b, const f32x16 &c)
@@ -82,11 +84,13 @@ __device__ __forceinline__ f32x16 mfma32(const uint4 &a, const uint4 &b, const f
 // read); the k-loop waits on these loads explicitly.  M0 is reserved to
 // the compiler, which therefore ignores a clobber of it: the GEMM kernels
 // below generate no other M0 use (checked on their gfx950 assembly), so
-// writing it here disturbs nothing.
+// writing it here disturbs nothing.  An SALU write of M0 needs one wait
+// state before an LDS DMA reads it (a gfx9 hazard the compiler's hazard
+// recognizer cannot see inside asm): the s_nop.
 __device__ __forceinline__ void dma16(const void *src, LDS uint4 *dst)
 {
     const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)dst);
-    __asm__ volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src) : "memory");
+    __asm__ volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src) : "memory");
 }
 
 // 16 zero bytes in global memory: the DMA source of every chunk past the
@@ -257,32 +261,44 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1)
     const int krem = k_total - (int)blockIdx.z * kz_step;
     const int kend = krem < K ? krem : K;
     const int KT = (kend + KB - 1) / KB;
-    // Two-stage ring, tile t in stage t & 1.  Tiles 0 and 1 are in flight
-    // before the loop; tile t+2 is loaded while tile t+1 is computed.  The
-    // one barrier per tile sits between the fragment reads and the MFMAs of
-    // a tile's last k-step: by then every wave has read the whole stage
-    // (its last fragments are in registers), so after it the stage is
-    // refilled with tile t+2 and tile t+1's first fragments are read while
-    // the last MFMAs of tile t still run -- the matrix units do not drain at
-    // the barrier.
-    static_assert(S == 2 && (KB / 16) % 2 == 0, "two stages, an even number of k-steps per tile");
+    // S-stage ring, tile t in stage t % S.  Between two barriers the
+    // k-loop is straight-line code, so the compiler's LDS wait counts stay
+    // exact: at a control-flow merge it falls back to waiting for every
+    // outstanding LDS read, which would stall each wave on the fragment
+    // reads it has just issued for the next k-step.
+    //  - k-step s of a tile reads the fragments of step s + 1, then runs
+    //    its MFMAs on those read one step earlier;
+    //  - a tile's last k-step ("tail") starts with the one barrier per tile:
+    //    every wave has then read the whole stage (its last fragments are in
+    //    registers), so the stage is refilled with tile t + S during that
+    //    step's MFMAs and the next tile's first fragments are read while
+    //    they run -- the matrix units do not drain at the barrier;
+    //  - a "link" is the tail of tile t and the other k-steps ("head") of
+    //    tile t + 1, so each link starts at the barrier, whose explicit wait
+    //    leaves no LDS read outstanding, and the branches between links
+    //    (S per loop iteration, for constant stage offsets) cost no waits;
+    //  - tiles 0 .. S-1 are in flight before the first tile and tile t + S
+    //    is loaded during tile t's tail also when t + S >= KT: such tiles lie
+    //    past kend and every chunk comes from the zero page (never read: no
+    //    stage is read after the last tile).
+    static_assert(S >= 2 && (KB / 16) % 2 == 0, "two or more stages, an even number of k-steps per tile");
     constexpr int LPT = OA::NQ + OB::NQ; // DMA instructions per thread per tile
+    static_assert((S - 1) * LPT < 64, "the loads in flight fit the vmcnt counter");
     constexpr int KS = KB / 16, NM = FM * FN;
+    const int links = KT > 1 ? KT - 1 : 0;
     auto dma = [&](int q, int t, LDS uint4 *dA, LDS uint4 *dB) {
         if (q < OA::NQ)
             OA::load_q(q, Ab, lda, m0, a_extent, t * KB, kend, dA, tid);
         else
             OB::load_q(q - OA::NQ, Bb, ldb, n0, b_extent, t * KB, kend, dB, tid);
     };
-    // a bare s_barrier after an explicit wait on this wave's loads: the
+    // a bare s_barrier after an explicit wait on this wave's loads (all but
+    // the newest NEWER tiles' landed in LDS) and on its LDS reads: the
     // fence of __syncthreads() would drain every outstanding memory
     // operation; the empty asm statements keep LDS accesses from moving
     // across it
-    auto sync_tile = [&](bool newer_in_flight) {
-        if (newer_in_flight)
-            __builtin_amdgcn_s_waitcnt(vmcnt_imm(LPT));
-        else
-            __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    auto sync_tile = [&](auto newer) {
+        __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0_imm(decltype(newer)::value * LPT));
         __asm__ volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
         __asm__ volatile("" ::: "memory");
@@ -296,58 +312,63 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1)
         for (int j = 0; j < FN; ++j)
             xb[j] = OB::frag(cB, wn * WN + j * 32, s, lane);
     };
+    // MFMAs of k-step s; in a tail, tile `reload` goes into stage (dA, dB),
+    // a few loads per MFMA rather than one burst at the vector-memory queue
+    auto mfmas = [&](int s, bool tail, int reload, LDS uint4 *dA, LDS uint4 *dB) {
+        // keep this step's fragment reads (issued just before) ahead of its
+        // MFMAs: left alone, the scheduler sinks each read to just before
+        // its first use and the LDS latency shows at every step
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int q = 0; q < LPT; ++q)
-        if (KT > 0)
-            dma(q, 0, stA(0), stB(0));
+        for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int q = 0; q < LPT; ++q)
-        if (KT > 1)
-            dma(q, 1, stA(1), stB(1));
-    sync_tile(KT > 1);
-    rd(stA(0), stB(0), 0, fa[0], fb[0]);
-
-    // tile kt from stage (cA, cB); the other stage (oA, oB) holds tile kt+1
-    auto tile = [&](int kt, LDS uint4 *cA, LDS uint4 *cB, LDS uint4 *oA, LDS uint4 *oB) {
+            for (int j = 0; j < FN; ++j) {
+                acc[i][j] = mfma32<F16>(fa[s & 1][i], fb[s & 1][j], acc[i][j]);
+                if (tail) {
+                    const int g = i * FN + j;
 #pragma unroll
-        for (int s = 0; s < KS; ++s) {
-            const int cur = s & 1;
-            const bool last = s == KS - 1;
-            if (!last) {
-                rd(cA, cB, s + 1, fa[cur ^ 1], fb[cur ^ 1]);
-            } else if (kt + 1 < KT) {
-                sync_tile(false);
-                rd(oA, oB, 0, fa[cur ^ 1], fb[cur ^ 1]);
-            }
-            // keep the next step's fragment reads ahead of this step's
-            // MFMAs: left alone, the scheduler sinks each read to just
-            // before its first use and the LDS latency shows at every step
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int i = 0; i < FM; ++i)
-#pragma unroll
-                for (int j = 0; j < FN; ++j) {
-                    acc[i][j] = mfma32<F16>(fa[cur][i], fb[cur][j], acc[i][j]);
-                    if (last) {
-                        // tile kt+2 into the stage just freed, a few loads
-                        // per MFMA rather than one burst at the vector-memory
-                        // queue
-                        const int g = i * FN + j;
-#pragma unroll
-                        for (int q = g * LPT / NM; q < (g + 1) * LPT / NM; ++q)
-                            if (kt + 2 < KT)
-                                dma(q, kt + 2, cA, cB);
-                        __builtin_amdgcn_sched_barrier(0);
-                    }
+                    for (int q = g * LPT / NM; q < (g + 1) * LPT / NM; ++q)
+                        dma(q, reload, dA, dB);
+                    __builtin_amdgcn_sched_barrier(0);
                 }
-            __builtin_amdgcn_sched_barrier(0);
+            }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // k-steps 0 .. KS-2 of the tile in stage (cA, cB); step 0's fragments
+    // are in fa[0], fb[0]
+    auto head = [&](const LDS uint4 *cA, const LDS uint4 *cB) {
+#pragma unroll
+        for (int s = 0; s < KS - 1; ++s) {
+            rd(cA, cB, s + 1, fa[(s + 1) & 1], fb[(s + 1) & 1]);
+            mfmas(s, false, 0, nullptr, nullptr);
         }
     };
-    for (int kt = 0; kt < KT; kt += 2) {
-        tile(kt, stA(0), stB(0), stA(1), stB(1));
-        if (kt + 1 < KT)
-            tile(kt + 1, stA(1), stB(1), stA(0), stB(0));
+    // the tail of tile t (stage cA, cB) and the head of tile t + 1 (oA, oB)
+    auto link = [&](int t, LDS uint4 *cA, LDS uint4 *cB, LDS uint4 *oA, LDS uint4 *oB) {
+        // tile t + 1 landed; tiles t + 2 .. t + S - 1 may be in flight
+        sync_tile(std::integral_constant<int, S - 2>{});
+        rd(oA, oB, 0, fa[0], fb[0]);
+        mfmas(KS - 1, true, t + S, cA, cB);
+        head(oA, oB);
+    };
+#pragma unroll
+    for (int t = 0; t < S; ++t)
+#pragma unroll
+        for (int q = 0; q < LPT; ++q)
+            dma(q, t, stA(t), stB(t));
+    sync_tile(std::integral_constant<int, S - 1>{}); // tile 0 landed
+    rd(stA(0), stB(0), 0, fa[0], fb[0]);
+    head(stA(0), stB(0));
+    for (int t = 0; t < links; t += S) {
+#pragma unroll
+        for (int u = 0; u < S; ++u)
+            if (t + u < links)
+                link(t + u, stA(u), stB(u), stA((u + 1) % S), stB((u + 1) % S));
     }
+    mfmas(KS - 1, false, 0, nullptr, nullptr); // the last tile's tail
+    // the loads of the tiles past the end land before the LDS is reused
+    // (the epilogue's staging, or the next block on this CU)
+    __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0_imm(0));
 
     // epilogue: lane holds column lane % 32 of rows (e/4)*8 + (lane/32)*4 + e%4
     const int lrow = lane & 31, lk = lane >> 5;
@@ -587,11 +608,13 @@ int launch_tile(const gemm_args &g, const pgk_epi &epi, hipStream_t s)
 template <bool TA, bool TB, bool F16, bool EPI = false>
 int launch_layout(const gemm_args &g, hipStream_t s, const pgk_epi &epi = pgk_epi{})
 {
-    // 256 x 256 tiles (eight waves, each 128 x 64) whenever they still give
-    // most CUs a tile; else 128 x 128 (four waves, each 64 x 64)
+    // 256 x 256 tiles (eight waves, each 128 x 64; k-tiles of 32 in a
+    // four-stage ring, 128 KiB of LDS) whenever they still give most CUs a
+    // tile; else 128 x 128 (four waves, each 64 x 64; k-tiles of 64, two
+    // stages)
     const size_t big = (size_t)((g.m + 255) / 256) * ((g.n + 255) / 256) * g.batch;
     if (g.tile == 2 || (g.tile == 0 && big >= 128))
-        return launch_tile<256, 256, 2, 4, TA, TB, F16, EPI>(g, epi, s);
+        return launch_tile<256, 256, 2, 4, TA, TB, F16, EPI, 32, 4>(g, epi, s);
     return launch_tile<128, 128, 2, 2, TA, TB, F16, EPI>(g, epi, s);
 }
 
@@ -760,7 +783,9 @@ extern "C" int pgk_gemm16(int dtype, int ta, int tb, size_t m, size_t n, size_t 
     const bool has_epi = epi && (epi->bias || epi->act != PGK_ACT_NONE || epi->z || epi->c16);
     if (has_epi && (beta || batch != 1 || (epi->c16 && epi->dtype16 != 1 && epi->dtype16 != 2)))
         return (int)hipErrorInvalidValue;
-    if (m > 0x7fffffff || n > 0x7fffffff || k > 0x7fffffff || batch > 65535)
+    // k leaves headroom for the k offsets of the tiles the kernel loads
+    // past the end (from the zero page) to stay within int
+    if (m > 0x7fffffff || n > 0x7fffffff || k > 0x7fff0000 || batch > 65535)
         return (int)hipErrorInvalidValue;
     // 16-byte global loads: aligned bases, leading dims and batch strides
     if ((((uintptr_t)a | (uintptr_t)b) & 15) || (lda & 7) || (ldb & 7) || (stride_a & 7) || (stride_b & 7))

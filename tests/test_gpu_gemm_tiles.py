@@ -1,0 +1,101 @@
+"""The 256 x 256-tile MFMA GEMM path (eight waves, global -> LDS ring) in
+each operand layout the autograd uses, at shapes large enough that the
+launch plan picks it (at least 128 such tiles, no split-K), with ragged
+edges in every dim:
+
+- forward C = A . W (A K-contiguous, W MN-contiguous): M = 2900 rows (a
+  partial last tile row), K = 3000 (a partial last k-tile, K % 8 == 0);
+- dgrad dA = dC . W^T (both K-contiguous): K = 3080;
+- wgrad dW = A^T . dC (both MN-contiguous): K = 2900, K % 8 == 4, the
+  last k-tile reading zero rows past K;
+- the fused bias + GELU epilogue on the forward layout (pg_amd_ag_linear16).
+
+The oracle checks sampled rows and columns (each against the
+f32-accumulating product of the same 16-bit operands, relative Frobenius
+<= 1e-5: identical operands, summation order only); exact linearity in the
+upstream grad and bit-for-bit determinism cover the rest.
+"""
+import numpy as np
+import pytest
+
+from oracle_lib import bf16_to_f32, f16_to_f32, rel_fro
+from picograd_amd.capi import BF16, F16, F32
+
+pytestmark = pytest.mark.gpu
+
+M, K, N = 2900, 3000, 3080
+
+
+def _to_f32(dt, h):
+    return f16_to_f32(h) if dt == F16 else bf16_to_f32(h)
+
+
+def _backward(lib, dt, a16, w16, g16, scale=1.0):
+    na, nw = lib.var(a16, dtype=dt), lib.var(w16, dtype=dt)
+    c = lib.op("matmul", na, nw)
+    out = lib.value(c)
+    seed = lib.tensor(_to_f32(dt, g16) * np.float32(scale))
+    lib.pg_amd_backward_from(c, seed)
+    da, dw = lib.grad(na), lib.grad(nw)
+    lib.pg_tensor_free(seed)
+    for n in (c, na, nw):
+        lib.pg_node_free(n)
+    return out, da, dw
+
+
+@pytest.mark.parametrize("dt", [BF16, F16])
+def test_big_tile_matmul_all_layouts(lib, oracle, dt):
+    print(f"gemm 256-tile matmul fwd/bwd dt={dt} {M}x{K}x{N}", flush=True)
+    oracle.orc_seed(50 + dt)
+    a = oracle.cast16(dt, oracle.normal(M * K, 0.0, 1.0).reshape(M, K))
+    w = oracle.cast16(dt, oracle.normal(K * N, 0.0, 0.02).reshape(K, N))
+    g = oracle.cast16(dt, oracle.normal(M * N, 0.0, 1.0).reshape(M, N))
+    out, da, dw = _backward(lib, dt, a, w, g)
+    assert out.shape == (M, N) and da.shape == (M, K) and dw.shape == (K, N)
+    rng = np.random.default_rng(dt)
+    rows = np.unique(np.concatenate([rng.choice(M, 40, replace=False), [0, 255, 256, 2815, 2816, M - 1]]))
+    # forward rows: C[r, :] = A[r, :] . W
+    ref = oracle.gemm(dt, np.ascontiguousarray(a[rows]), w, threads=16)
+    assert rel_fro(out[rows], ref) <= 1e-5
+    # dgrad rows: dA[r, :] = dC[r, :] . W^T
+    ref = oracle.gemm(dt, np.ascontiguousarray(g[rows]), w, tb=True, threads=16)
+    assert rel_fro(da[rows], ref) <= 1e-5
+    # wgrad rows: dW[k, :] = A[:, k]^T . dC
+    ks = np.unique(np.concatenate([rng.choice(K, 24, replace=False), [0, 2815, 2816, K - 1]]))
+    ref = oracle.gemm(dt, np.ascontiguousarray(a[:, ks]), g, ta=True, threads=16)
+    assert rel_fro(dw[ks], ref) <= 1e-5
+    # columns at tile edges, all rows
+    js = np.array([0, 255, 256, 3071, 3072, N - 1])
+    ref = oracle.gemm(dt, a, np.ascontiguousarray(w[:, js]), threads=16)
+    assert rel_fro(out[:, js], ref) <= 1e-5
+    ref = oracle.gemm(dt, a, np.ascontiguousarray(g[:, js]), ta=True, threads=16)
+    assert rel_fro(dw[:, js], ref) <= 1e-5
+    # exact linearity in the upstream grad, and determinism
+    _, da2, dw2 = _backward(lib, dt, a, w, g, scale=2.0)
+    assert np.array_equal(da2, 2 * da) and np.array_equal(dw2, 2 * dw)
+    out3, da3, dw3 = _backward(lib, dt, a, w, g)
+    assert np.array_equal(out3, out) and np.array_equal(da3, da) and np.array_equal(dw3, dw)
+
+
+@pytest.mark.parametrize("dt", [BF16, F16])
+def test_big_tile_fused_epilogue(lib, oracle, dt):
+    """out = gelu(q(x) . q(W) + b) from one launch with the epilogue fused
+    (K = 520: no k-tail, no split)."""
+    kk = 520
+    print(f"gemm 256-tile linear16 gelu dt={dt} {M}x{kk}x{N}", flush=True)
+    rng = np.random.default_rng(60 + dt)
+    x = rng.standard_normal((M, kk)).astype(np.float32)
+    wt = (rng.standard_normal((kk, N)) / np.sqrt(kk)).astype(np.float32)
+    b = (0.3 * rng.standard_normal(N)).astype(np.float32)
+    nx, nw, nb = lib.var(x), lib.var(wt), lib.var(b)
+    out = lib._check(lib.pg_amd_ag_linear16(nx, nw, nb, 2, dt))
+    got = lib.value(out)
+    rows = np.unique(np.concatenate([rng.choice(M, 32, replace=False), [0, 2815, 2816, M - 1]]))
+    qx = _to_f32(dt, oracle.cast16(dt, np.ascontiguousarray(x[rows])))
+    qw = _to_f32(dt, oracle.cast16(dt, wt))
+    z = oracle.gemm(F32, qx, qw).astype(np.float64) + b
+    from math import erf
+    want = 0.5 * z * (1.0 + np.vectorize(erf)(z / np.sqrt(2.0)))
+    assert rel_fro(got[rows], want) <= 1e-5
+    for n in (out, nx, nw, nb):
+        lib.pg_node_free(n)
