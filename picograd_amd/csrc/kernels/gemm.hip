@@ -93,6 +93,18 @@ __device__ __forceinline__ void dma16(const void *src, LDS uint4 *dst)
     __asm__ volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src) : "memory");
 }
 
+// The same copy from a wave-uniform base address in SGPRs plus a 32-bit
+// per-lane byte offset: the form for k-tiles that lie wholly below the end
+// of the reduction dim, whose per-lane offsets stay fixed from tile to tile
+// (only the scalar base moves), so the loop spends no vector ALU work on
+// addresses.  `sbase` must be wave-uniform.
+__device__ __forceinline__ void dma16s(uint32_t voff, const void *sbase, LDS uint4 *dst)
+{
+    const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)dst);
+    __asm__ volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(voff), "s"(sbase)
+                     : "memory");
+}
+
 // 16 zero bytes in global memory: the DMA source of every chunk past the
 // end of the reduction dim, so a partial last k-tile lands zero-filled
 __device__ const uint4 g_zero16 = {0u, 0u, 0u, 0u};
@@ -131,12 +143,31 @@ struct TileK {
         const void *src = kc < kend ? (const void *)(p + (size_t)gr * ld + kc) : (const void *)&g_zero16;
         dma16(src, dst + base);
     }
-    __device__ __forceinline__ static void load(const uint16_t *__restrict__ p, size_t ld, int row0, int extent,
-                                                int k0, int kend, LDS uint4 *dst, int tid)
+    // Fast form of load q (k-tiles below kend): the scalar base is row
+    // `srow` (the first row load q touches, clamped like the rows) and each
+    // lane's offset is (its clamped row - srow) ld + its chunk, in bytes;
+    // the 64 lanes span 64 / CH rows, so the offset fits 32 bits for
+    // ld < 2^26.  `wave` must be wave-uniform.
+    struct Fast {
+        uint32_t voff;
+        int srow;
+    };
+    __device__ __forceinline__ static Fast fast_q(int q, size_t ld, int row0, int extent, int wave, int lane)
     {
-#pragma unroll
-        for (int q = 0; q < NQ; ++q)
-            load_q(q, p, ld, row0, extent, k0, kend, dst, tid);
+        const int base = (wave * NQ + q) * 64;
+        const int qrow = row0 + base / CH;
+        const int srow = qrow < extent ? qrow : extent - 1;
+        const int slot = base + lane;
+        const int row = slot / CH;
+        const int logical = swz(slot % CH, row);
+        int gr = row0 + row;
+        gr = gr < extent ? gr : extent - 1;
+        return {(uint32_t)((size_t)(gr - srow) * ld * 2 + (size_t)logical * 16), srow};
+    }
+    __device__ __forceinline__ static void load_fast(int q, const Fast &f, const uint16_t *__restrict__ p, size_t ld,
+                                                     int /*row0*/, int k0, LDS uint4 *dst, int wave)
+    {
+        dma16s(f.voff, p + (size_t)f.srow * ld + k0, dst + (wave * NQ + q) * 64);
     }
 
     // MFMA operand fragment: rows r0 + lane % 32, k = 16 s + 8 (lane / 32) .. + 7
@@ -179,12 +210,29 @@ struct TileMN {
             k0 + k < kend ? (const void *)(p + (size_t)(k0 + k) * ld + mn) : (const void *)&g_zero16;
         dma16(src, dst + base);
     }
-    __device__ __forceinline__ static void load(const uint16_t *__restrict__ p, size_t ld, int row0, int extent,
-                                                int k0, int kend, LDS uint4 *dst, int tid)
+    // Fast form of load q (k-tiles below kend): the scalar base is k-row
+    // k0 + kq (the first k-row load q touches), column row0, and each lane's
+    // offset is (its k-row - kq) ld + (its clamped column - row0), in bytes;
+    // the 64 lanes span 64 / CPR <= 4 k-rows.  `wave` must be wave-uniform.
+    struct Fast {
+        uint32_t voff;
+        int srow;
+    };
+    __device__ __forceinline__ static Fast fast_q(int q, size_t ld, int row0, int extent, int wave, int lane)
     {
-#pragma unroll
-        for (int q = 0; q < NQ; ++q)
-            load_q(q, p, ld, row0, extent, k0, kend, dst, tid);
+        const int base = (wave * NQ + q) * 64;
+        const int kq = base / CPR;
+        const int slot = base + lane;
+        const int k = slot / CPR;
+        const int logical = (slot % CPR) ^ fk(k);
+        int mn = row0 + logical * 8;
+        mn = mn < extent ? mn : extent - 8;
+        return {(uint32_t)(((size_t)(k - kq) * ld + (size_t)(mn - row0)) * 2), kq};
+    }
+    __device__ __forceinline__ static void load_fast(int q, const Fast &f, const uint16_t *__restrict__ p, size_t ld,
+                                                     int row0, int k0, LDS uint4 *dst, int wave)
+    {
+        dma16s(f.voff, p + (size_t)(k0 + f.srow) * ld + row0, dst + (wave * NQ + q) * 64);
     }
 
     // MFMA operand fragment from two ds_read_b64_tr_b16: in 16-lane group g
@@ -211,7 +259,7 @@ template <int BM, int BN, int WGM, int WGN, bool TA, bool TB, bool F16, bool EPI
 __global__ void __launch_bounds__(64 * WGM * WGN, 1)
     k_gemm16(const uint16_t *__restrict__ A, size_t lda, size_t sA, int a_extent, const uint16_t *__restrict__ B,
              size_t ldb, size_t sB, int b_extent, float *__restrict__ C, size_t ldc, size_t sC, int M, int N, int K,
-             int beta, int tiles_m, int tiles_n, pgk_epi epi, int k_total, int kz_step)
+             int beta, int tiles_m, int tiles_n, pgk_epi epi, int k_total, int kz_step, int fast_ok)
 {
     constexpr int NT = 64 * WGM * WGN;
     constexpr int WM = BM / WGM, WN = BN / WGN;
@@ -245,6 +293,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1)
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WGN, wn = wave % WGN;
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
 
     f32x16 acc[FM][FN];
 #pragma unroll
@@ -292,6 +341,22 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1)
         else
             OB::load_q(q - OA::NQ, Bb, ldb, n0, b_extent, t * KB, kend, dB, tid);
     };
+    // per-lane offsets of the fast form (tiles wholly below kend, leading
+    // dims under 2^26: fast_ok), fixed for the whole k-loop
+    typename OA::Fast fA[OA::NQ];
+    typename OB::Fast fB[OB::NQ];
+#pragma unroll
+    for (int q = 0; q < OA::NQ; ++q)
+        fA[q] = OA::fast_q(q, lda, m0, a_extent, wave_u, lane);
+#pragma unroll
+    for (int q = 0; q < OB::NQ; ++q)
+        fB[q] = OB::fast_q(q, ldb, n0, b_extent, wave_u, lane);
+    auto dma_fast = [&](int q, int t, LDS uint4 *dA, LDS uint4 *dB) {
+        if (q < OA::NQ)
+            OA::load_fast(q, fA[q], Ab, lda, m0, t * KB, dA, wave_u);
+        else
+            OB::load_fast(q - OA::NQ, fB[q - OA::NQ], Bb, ldb, n0, t * KB, dB, wave_u);
+    };
     // a bare s_barrier after an explicit wait on this wave's loads (all but
     // the newest NEWER tiles' landed in LDS) and on its LDS reads: the
     // fence of __syncthreads() would drain every outstanding memory
@@ -313,8 +378,9 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1)
             xb[j] = OB::frag(cB, wn * WN + j * 32, s, lane);
     };
     // MFMAs of k-step s; in a tail, tile `reload` goes into stage (dA, dB),
-    // a few loads per MFMA rather than one burst at the vector-memory queue
-    auto mfmas = [&](int s, bool tail, int reload, LDS uint4 *dA, LDS uint4 *dB) {
+    // a few loads per MFMA rather than one burst at the vector-memory queue,
+    // in the fast form when FAST (a compile-time tag)
+    auto mfmas = [&](int s, bool tail, int reload, LDS uint4 *dA, LDS uint4 *dB, auto fast) {
         // keep this step's fragment reads (issued just before) ahead of its
         // MFMAs: left alone, the scheduler sinks each read to just before
         // its first use and the LDS latency shows at every step
@@ -327,8 +393,12 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1)
                 if (tail) {
                     const int g = i * FN + j;
 #pragma unroll
-                    for (int q = g * LPT / NM; q < (g + 1) * LPT / NM; ++q)
-                        dma(q, reload, dA, dB);
+                    for (int q = g * LPT / NM; q < (g + 1) * LPT / NM; ++q) {
+                        if constexpr (decltype(fast)::value)
+                            dma_fast(q, reload, dA, dB);
+                        else
+                            dma(q, reload, dA, dB);
+                    }
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }
@@ -340,15 +410,15 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1)
 #pragma unroll
         for (int s = 0; s < KS - 1; ++s) {
             rd(cA, cB, s + 1, fa[(s + 1) & 1], fb[(s + 1) & 1]);
-            mfmas(s, false, 0, nullptr, nullptr);
+            mfmas(s, false, 0, nullptr, nullptr, std::false_type{});
         }
     };
     // the tail of tile t (stage cA, cB) and the head of tile t + 1 (oA, oB)
-    auto link = [&](int t, LDS uint4 *cA, LDS uint4 *cB, LDS uint4 *oA, LDS uint4 *oB) {
+    auto link = [&](int t, LDS uint4 *cA, LDS uint4 *cB, LDS uint4 *oA, LDS uint4 *oB, auto fast) {
         // tile t + 1 landed; tiles t + 2 .. t + S - 1 may be in flight
         sync_tile(std::integral_constant<int, S - 2>{});
         rd(oA, oB, 0, fa[0], fb[0]);
-        mfmas(KS - 1, true, t + S, cA, cB);
+        mfmas(KS - 1, true, t + S, cA, cB, fast);
         head(oA, oB);
     };
 #pragma unroll
@@ -359,13 +429,25 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1)
     sync_tile(std::integral_constant<int, S - 1>{}); // tile 0 landed
     rd(stA(0), stB(0), 0, fa[0], fb[0]);
     head(stA(0), stB(0));
-    for (int t = 0; t < links; t += S) {
+    // link t reloads tile t + S: in the fast form while that tile lies
+    // wholly below kend, for whole groups of S links (so the second loop
+    // starts at stage 0), then the general form
+    const int full_tiles = kend / KB;
+    int fast_links = full_tiles > S ? full_tiles - S : 0;
+    fast_links = fast_ok ? (fast_links < links ? fast_links : links) / S * S : 0;
+    int t = 0;
+    for (; t < fast_links; t += S) {
+#pragma unroll
+        for (int u = 0; u < S; ++u)
+            link(t + u, stA(u), stB(u), stA((u + 1) % S), stB((u + 1) % S), std::true_type{});
+    }
+    for (; t < links; t += S) {
 #pragma unroll
         for (int u = 0; u < S; ++u)
             if (t + u < links)
-                link(t + u, stA(u), stB(u), stA((u + 1) % S), stB((u + 1) % S));
+                link(t + u, stA(u), stB(u), stA((u + 1) % S), stB((u + 1) % S), std::false_type{});
     }
-    mfmas(KS - 1, false, 0, nullptr, nullptr); // the last tile's tail
+    mfmas(KS - 1, false, 0, nullptr, nullptr, std::false_type{}); // the last tile's tail
     // the loads of the tiles past the end land before the LDS is reused
     // (the epilogue's staging, or the next block on this CU)
     __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0_imm(0));
@@ -601,7 +683,8 @@ int launch_tile(const gemm_args &g, const pgk_epi &epi, hipStream_t s)
     const int tm = (g.m + BM - 1) / BM, tn = (g.n + BN - 1) / BN;
     hipLaunchKernelGGL((k_gemm16<BM, BN, WGM, WGN, TA, TB, F16, EPI, KB, S>), dim3((unsigned)(tm * tn), 1, g.batch),
                        dim3(64 * WGM * WGN), 0, s, g.a, g.lda, g.sa, g.a_extent, g.b, g.ldb, g.sb, g.b_extent, g.c,
-                       g.ldc, g.sc, g.m, g.n, g.k, g.beta, tm, tn, epi, g.k_total ? g.k_total : g.k, g.kz_step);
+                       g.ldc, g.sc, g.m, g.n, g.k, g.beta, tm, tn, epi, g.k_total ? g.k_total : g.k, g.kz_step,
+                       (int)(g.lda < ((size_t)1 << 26) && g.ldb < ((size_t)1 << 26)));
     return (int)hipGetLastError();
 }
 
