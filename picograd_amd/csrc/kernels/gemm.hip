@@ -691,13 +691,19 @@ int launch_tile(const gemm_args &g, const pgk_epi &epi, hipStream_t s)
 template <bool TA, bool TB, bool F16, bool EPI = false>
 int launch_layout(const gemm_args &g, hipStream_t s, const pgk_epi &epi = pgk_epi{})
 {
-    // 256 x 256 tiles (eight waves, each 128 x 64; k-tiles of 32 in a
-    // four-stage ring, 128 KiB of LDS) whenever they still give most CUs a
-    // tile; else 128 x 128 (four waves, each 64 x 64; k-tiles of 64, two
-    // stages)
+    // 256 x 256 tiles (eight waves, each 128 x 64) whenever they still give
+    // most CUs a tile; else 128 x 128 (four waves, each 64 x 64; k-tiles of
+    // 64, two stages).  Big tiles take k-tiles of 32 in a four-stage ring
+    // (128 KiB of LDS), except with both operands K-contiguous: there a
+    // k-tile of 32 covers half of each 128-byte row segment per load, and
+    // k-tiles of 64 in two stages measure faster
     const size_t big = (size_t)((g.m + 255) / 256) * ((g.n + 255) / 256) * g.batch;
-    if (g.tile == 2 || (g.tile == 0 && big >= 128))
-        return launch_tile<256, 256, 2, 4, TA, TB, F16, EPI, 32, 4>(g, epi, s);
+    if (g.tile == 2 || (g.tile == 0 && big >= 128)) {
+        if constexpr (!TA && !TB)
+            return launch_tile<256, 256, 2, 4, TA, TB, F16, EPI, 64, 2>(g, epi, s);
+        else
+            return launch_tile<256, 256, 2, 4, TA, TB, F16, EPI, 32, 4>(g, epi, s);
+    }
     return launch_tile<128, 128, 2, 2, TA, TB, F16, EPI>(g, epi, s);
 }
 
