@@ -51,6 +51,8 @@ typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 #define LDS __attribute__((address_space(3)))
 
+// alignment of split-K slices and of the zero-padded k-tail slabs: a
+// multiple of every kernel k-tile depth (32 and 64)
 constexpr int BK = 64;
 
 __device__ __forceinline__ float act_f(int act, float v)
