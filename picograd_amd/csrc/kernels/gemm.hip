@@ -582,18 +582,33 @@ __global__ void __launch_bounds__(256) k_pack_slab(int mn_major, const uint16_t 
 }
 
 // split-K finish: C = (beta ? C : 0) + sum over the `splits` partial
-// products (each m x n, dense), added in split order
+// products (each m x n, dense), added in split order.  Rows run along
+// grid y (stride gridDim.y) and columns along x, four per thread when n and
+// ldc allow 16-byte accesses: no index division anywhere
 __global__ void __launch_bounds__(256) k_splitk_sum(const float *__restrict__ part, int splits, int m, int n,
                                                     float *__restrict__ c, size_t ldc, int beta)
 {
     const size_t mn = (size_t)m * n;
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < mn; i += (size_t)gridDim.x * blockDim.x) {
-        float acc = 0.0f;
-        for (int z = 0; z < splits; ++z)
-            acc += part[(size_t)z * mn + i];
-        const size_t r = i / n, col = i - r * n;
-        float *p = c + r * ldc + col;
-        *p = beta ? *p + acc : acc;
+    const bool v4 = ((n | (int)(ldc & 3)) & 3) == 0 && (((uintptr_t)c | (uintptr_t)part) & 15) == 0;
+    const int cols = v4 ? n >> 2 : n;
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= cols)
+        return;
+    for (int r = blockIdx.y; r < m; r += gridDim.y) {
+        const float *p = part + (size_t)r * n;
+        float *o = c + (size_t)r * ldc;
+        if (v4) {
+            f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+            for (int z = 0; z < splits; ++z)
+                acc += *(const f32x4 *)(p + (size_t)z * mn + 4 * j);
+            f32x4 *q = (f32x4 *)(o + 4 * j);
+            *q = beta ? *q + acc : acc;
+        } else {
+            float acc = 0.0f;
+            for (int z = 0; z < splits; ++z)
+                acc += p[(size_t)z * mn + j];
+            o[j] = beta ? o[j] + acc : acc;
+        }
     }
 }
 
@@ -922,7 +937,12 @@ extern "C" int pgk_gemm16(int dtype, int ta, int tb, size_t m, size_t n, size_t 
         rc = launch_any(f16, ta, tb, g, st);
         if (rc)
             return rc;
-        hipLaunchKernelGGL(k_splitk_sum, dim3(gmn), dim3(256), 0, st, part, sp, (int)m, (int)n, c, ldc, beta);
+        {
+            const bool v4 = ((n | (ldc & 3)) & 3) == 0 && (((uintptr_t)c | (uintptr_t)part) & 15) == 0;
+            const size_t cols = v4 ? n / 4 : n;
+            hipLaunchKernelGGL(k_splitk_sum, dim3((unsigned)((cols + 255) / 256), (unsigned)(m < 65535 ? m : 65535)),
+                               dim3(256), 0, st, part, sp, (int)m, (int)n, c, ldc, beta);
+        }
         rc = (int)hipGetLastError();
         if (rc)
             return rc;
