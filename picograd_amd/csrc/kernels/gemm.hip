@@ -690,8 +690,10 @@ struct gemm_args {
     size_t ldc, sc;
     int m, n, k, beta;
     unsigned batch;
-    int tile;         // 2: 256 x 256 tiles, 1: 128 x 128, 0: by tile count
-    int k_total, kz_step; // split-K: slice z reduces [z kz_step, min(k_total, (z+1) kz_step))
+    int tile = 0;     // 2: 256 x 256 tiles, 1: 128 x 128, 0: by tile count
+    // split-K: slice z reduces [z kz_step, min(k_total, (z+1) kz_step));
+    // k_total = 0: no split
+    int k_total = 0, kz_step = 0;
 };
 
 template <int BM, int BN, int WGM, int WGN, bool TA, bool TB, bool F16, bool EPI, int KB = 64, int S = 2>
