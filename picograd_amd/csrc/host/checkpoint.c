@@ -12,18 +12,29 @@
  * The elements move between HBM and the file through two pinned host
  * buffers of 8 MiB: while one chunk is written to the file, the next is
  * copied from the device on the library stream (and the reverse on load),
- * so a checkpoint costs about max(PCIe, file) time, not their sum.  Saves
- * are ordered after all queued device work; loads complete before they
- * return.
+ * so a checkpoint costs about max(PCIe, file) time, not their sum.  On a
+ * seekable file each chunk's read is split over CK_THREADS threads (pread
+ * at explicit offsets; the FILE position is moved past the data
+ * afterwards): one thread's copy out of the page cache bounds a
+ * single-stream load.  Saves stay one stream: writes that extend a file
+ * hold its inode lock, so threaded pwrite to one file measured slower.
+ * Saves are ordered after all queued device work; loads complete before
+ * they return.
  */
 #define _POSIX_C_SOURCE 200809L
 #include "internal.h"
 
+#include <errno.h>
 #include <hip/hip_runtime_api.h>
+#include <pthread.h>
 #include <stdlib.h>
 #include <string.h>
+#include <sys/types.h>
+#include <unistd.h>
 
 #define CK_CHUNK ((size_t)8 << 20)
+#define CK_THREADS 4
+#define CK_MIN_SLICE ((size_t)1 << 20)
 #define PGT1_MAGIC "PGT1"
 #define PGT1_VERSION 1u
 #define PGMD_MAGIC "PGMD"
@@ -52,6 +63,75 @@ static bool ck_ready(void)
 }
 
 static hipStream_t stream(void) { return (hipStream_t)pgd_stream(); }
+
+/* one thread's share of a chunk's file read */
+typedef struct {
+    int fd;
+    unsigned char *buf;
+    size_t len;
+    off_t off;
+    int ok;
+} ck_slice;
+
+static void *ck_slice_run(void *arg)
+{
+    ck_slice *sl = arg;
+    size_t done = 0;
+    sl->ok = 1;
+    while (done < sl->len) {
+        const ssize_t r = pread(sl->fd, sl->buf + done, sl->len - done, sl->off + (off_t)done);
+        if (r < 0 && errno == EINTR)
+            continue;
+        if (r <= 0) { /* an error, or end of file */
+            sl->ok = 0;
+            break;
+        }
+        done += (size_t)r;
+    }
+    return NULL;
+}
+
+/* reads [buf, buf + len) from file offset `off` in slices of at least
+ * CK_MIN_SLICE, one per thread (the caller takes the first; a slice whose
+ * thread cannot be started runs here too); false on any short read */
+static bool ck_pread_split(int fd, unsigned char *buf, size_t len, off_t off)
+{
+    ck_slice sl[CK_THREADS];
+    pthread_t th[CK_THREADS];
+    int started[CK_THREADS] = {0};
+    size_t per = (len + CK_THREADS - 1) / CK_THREADS;
+    per = per < CK_MIN_SLICE ? CK_MIN_SLICE : (per + 4095) & ~(size_t)4095;
+    int n = 0;
+    for (size_t o = 0; o < len && n < CK_THREADS; o += per, n++)
+        sl[n] = (ck_slice){fd, buf + o, len - o < per ? len - o : per, off + (off_t)o, 0};
+    for (int i = 1; i < n; i++)
+        started[i] = pthread_create(&th[i], NULL, ck_slice_run, &sl[i]) == 0;
+    ck_slice_run(&sl[0]);
+    bool ok = sl[0].ok;
+    for (int i = 1; i < n; i++) {
+        if (started[i])
+            pthread_join(th[i], NULL);
+        else
+            ck_slice_run(&sl[i]);
+        ok = ok && sl[i].ok;
+    }
+    return ok;
+}
+
+/* The file descriptor and offset for threaded reads of `nbytes` at the
+ * stream's position, or -1 to use stdio (small transfers, or a stream that
+ * cannot seek, such as a pipe). */
+static int ck_fd(FILE *fp, size_t nbytes, off_t *base)
+{
+    if (nbytes < 2 * CK_MIN_SLICE || fflush(fp) != 0)
+        return -1;
+    const int fd = fileno(fp);
+    const off_t pos = ftello(fp);
+    if (fd < 0 || pos < 0 || lseek(fd, 0, SEEK_CUR) < 0)
+        return -1;
+    *base = pos;
+    return fd;
+}
 
 bool pgc_dev_to_file(const void *dev, size_t nbytes, FILE *fp)
 {
@@ -99,6 +179,8 @@ bool pgc_file_to_dev(void *dev, size_t nbytes, FILE *fp)
     const size_t nch = (nbytes + CK_CHUNK - 1) / CK_CHUNK;
     unsigned char *dst = dev;
     bool ok = true;
+    off_t base = 0;
+    const int fd = ck_fd(fp, nbytes, &base);
     for (size_t c = 0; c < nch && ok; c++) {
         const int b = (int)(c & 1);
         const size_t off = c * CK_CHUNK, len = nbytes - off < CK_CHUNK ? nbytes - off : CK_CHUNK;
@@ -109,7 +191,7 @@ bool pgc_file_to_dev(void *dev, size_t nbytes, FILE *fp)
             ok = false;
             break;
         }
-        if (fread(g_ck[b], 1, len, fp) != len) {
+        if (fd >= 0 ? !ck_pread_split(fd, g_ck[b], len, base + (off_t)off) : fread(g_ck[b], 1, len, fp) != len) {
             ok = false;
             break;
         }
@@ -124,6 +206,9 @@ bool pgc_file_to_dev(void *dev, size_t nbytes, FILE *fp)
         pgd_set_err("checkpoint: host-to-device copy failed");
         ok = false;
     }
+    /* the stream continues after the data */
+    if (ok && fd >= 0 && fseeko(fp, base + (off_t)nbytes, SEEK_SET) != 0)
+        ok = false;
     return ok;
 }
 
