@@ -391,12 +391,19 @@ __global__ void __launch_bounds__(kBlock) k_copy16(int dtype, const TS *__restri
 }
 
 // ---------------------------------------------------------------- SGD
-// One launch updates every parameter: blockIdx.y selects the segment.
+// One launch updates every parameter: every tensor is cut into chunks of
+// kSgdChunk elements, one block each, and first[i] is the first block of
+// tensor i (so a 4096-element bias takes 2 blocks and a 16M-element weight
+// 8192, with no idle blocks).
 // g' = g + wd*p; buf = mu*buf + (1-damp)*g'; u = nesterov ? g' + mu*buf : buf;
 // p -= lr*u  (the reference's sgd.c:147-160 update, per element).
 #define PGK_SGD_MAX_SEG 32
+constexpr int kSgdVec = 2; // float4 per lane per block, all loads issued first
+constexpr size_t kSgdChunk = (size_t)kBlock * 4 * kSgdVec;
 struct sgd_table {
     pgk_sgd_seg seg[PGK_SGD_MAX_SEG];
+    unsigned first[PGK_SGD_MAX_SEG + 1];
+    int cnt;
 };
 
 __device__ __forceinline__ void sgd_elem(float &p, float g, float &b, bool has_buf, float lr, float mu,
@@ -419,42 +426,68 @@ __device__ __forceinline__ void sgd_elem(float &p, float g, float &b, bool has_b
 __global__ void __launch_bounds__(kBlock) k_sgd(sgd_table tab, float lr, float mu, float damp, float wd,
                                                 int nesterov)
 {
-    const pgk_sgd_seg sg = tab.seg[blockIdx.y];
-    size_t n = sg.n;
-    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    size_t stride = (size_t)gridDim.x * blockDim.x;
-    bool has_buf = sg.buf != nullptr;
-    bool aligned = ((((uintptr_t)sg.p) | ((uintptr_t)sg.g) | ((uintptr_t)sg.buf)) & 15) == 0 &&
-                   (((uintptr_t)sg.shadow) & 7) == 0;
-    size_t n4 = aligned ? n / 4 : 0;
-    for (size_t j = i; j < n4; j += stride) {
-        float4 p = reinterpret_cast<float4 *>(sg.p)[j];
-        float4 g = reinterpret_cast<const float4 *>(sg.g)[j];
-        float4 b = has_buf ? reinterpret_cast<float4 *>(sg.buf)[j] : make_float4(0, 0, 0, 0);
-        sgd_elem(p.x, g.x, b.x, has_buf, lr, mu, damp, wd, nesterov);
-        sgd_elem(p.y, g.y, b.y, has_buf, lr, mu, damp, wd, nesterov);
-        sgd_elem(p.z, g.z, b.z, has_buf, lr, mu, damp, wd, nesterov);
-        sgd_elem(p.w, g.w, b.w, has_buf, lr, mu, damp, wd, nesterov);
-        reinterpret_cast<float4 *>(sg.p)[j] = p;
-        if (has_buf)
-            reinterpret_cast<float4 *>(sg.buf)[j] = b;
-        if (sg.shadow) {
-            ushort4 o;
-            o.x = to16(sg.shadow_dtype, p.x);
-            o.y = to16(sg.shadow_dtype, p.y);
-            o.z = to16(sg.shadow_dtype, p.z);
-            o.w = to16(sg.shadow_dtype, p.w);
-            reinterpret_cast<ushort4 *>(sg.shadow)[j] = o;
+    const unsigned blk = blockIdx.x;
+    int si = 0;
+    for (int q = 1; q < tab.cnt; ++q)
+        si += blk >= tab.first[q] ? 1 : 0;
+    const pgk_sgd_seg sg = tab.seg[si];
+    const size_t n = sg.n, base = (size_t)(blk - tab.first[si]) * kSgdChunk;
+    const bool has_buf = sg.buf != nullptr;
+    const bool aligned = ((((uintptr_t)sg.p) | ((uintptr_t)sg.g) | ((uintptr_t)sg.buf)) & 15) == 0 &&
+                         (((uintptr_t)sg.shadow) & 7) == 0;
+    if (aligned) {
+        float4 p[kSgdVec], g[kSgdVec], b[kSgdVec];
+        size_t e[kSgdVec];
+#pragma unroll
+        for (int k = 0; k < kSgdVec; ++k) {
+            e[k] = base + 4 * ((size_t)threadIdx.x + (size_t)k * kBlock);
+            if (e[k] + 4 <= n) {
+                p[k] = reinterpret_cast<const float4 *>(sg.p + e[k])[0];
+                g[k] = reinterpret_cast<const float4 *>(sg.g + e[k])[0];
+                b[k] = has_buf ? reinterpret_cast<const float4 *>(sg.buf + e[k])[0] : make_float4(0, 0, 0, 0);
+            }
         }
-    }
-    for (size_t j = n4 * 4 + i; j < n; j += stride) {
-        float p = sg.p[j], b = has_buf ? sg.buf[j] : 0.0f;
-        sgd_elem(p, sg.g[j], b, has_buf, lr, mu, damp, wd, nesterov);
-        sg.p[j] = p;
-        if (has_buf)
-            sg.buf[j] = b;
-        if (sg.shadow)
-            sg.shadow[j] = to16(sg.shadow_dtype, p);
+#pragma unroll
+        for (int k = 0; k < kSgdVec; ++k) {
+            if (e[k] + 4 <= n) {
+                sgd_elem(p[k].x, g[k].x, b[k].x, has_buf, lr, mu, damp, wd, nesterov);
+                sgd_elem(p[k].y, g[k].y, b[k].y, has_buf, lr, mu, damp, wd, nesterov);
+                sgd_elem(p[k].z, g[k].z, b[k].z, has_buf, lr, mu, damp, wd, nesterov);
+                sgd_elem(p[k].w, g[k].w, b[k].w, has_buf, lr, mu, damp, wd, nesterov);
+                reinterpret_cast<float4 *>(sg.p + e[k])[0] = p[k];
+                if (has_buf)
+                    reinterpret_cast<float4 *>(sg.buf + e[k])[0] = b[k];
+                if (sg.shadow) {
+                    ushort4 o;
+                    o.x = to16(sg.shadow_dtype, p[k].x);
+                    o.y = to16(sg.shadow_dtype, p[k].y);
+                    o.z = to16(sg.shadow_dtype, p[k].z);
+                    o.w = to16(sg.shadow_dtype, p[k].w);
+                    reinterpret_cast<ushort4 *>(sg.shadow + e[k])[0] = o;
+                }
+            } else {
+                for (size_t j = e[k]; j < n; ++j) { // the last 1-3 elements
+                    float pj = sg.p[j], bj = has_buf ? sg.buf[j] : 0.0f;
+                    sgd_elem(pj, sg.g[j], bj, has_buf, lr, mu, damp, wd, nesterov);
+                    sg.p[j] = pj;
+                    if (has_buf)
+                        sg.buf[j] = bj;
+                    if (sg.shadow)
+                        sg.shadow[j] = to16(sg.shadow_dtype, pj);
+                }
+            }
+        }
+    } else {
+        const size_t end = base + kSgdChunk < n ? base + kSgdChunk : n;
+        for (size_t j = base + threadIdx.x; j < end; j += kBlock) {
+            float pj = sg.p[j], bj = has_buf ? sg.buf[j] : 0.0f;
+            sgd_elem(pj, sg.g[j], bj, has_buf, lr, mu, damp, wd, nesterov);
+            sg.p[j] = pj;
+            if (has_buf)
+                sg.buf[j] = bj;
+            if (sg.shadow)
+                sg.shadow[j] = to16(sg.shadow_dtype, pj);
+        }
     }
 }
 
@@ -782,17 +815,20 @@ extern "C" int pgk_sgd_multi(const pgk_sgd_seg *segs, int nseg, float lr, float 
     for (int base = 0; base < nseg; base += PGK_SGD_MAX_SEG) {
         int cnt = nseg - base < PGK_SGD_MAX_SEG ? nseg - base : PGK_SGD_MAX_SEG;
         sgd_table tab = {};
-        size_t maxn = 0;
+        tab.cnt = cnt;
+        size_t blocks = 0;
         for (int q = 0; q < cnt; ++q) {
             tab.seg[q] = segs[base + q];
-            if (segs[base + q].n > maxn)
-                maxn = segs[base + q].n;
+            tab.first[q] = (unsigned)blocks;
+            blocks += (segs[base + q].n + kSgdChunk - 1) / kSgdChunk;
+            if (blocks > 0x7fffffffu)
+                return (int)hipErrorInvalidValue;
         }
-        if (!maxn)
+        tab.first[cnt] = (unsigned)blocks;
+        if (!blocks)
             continue;
-        int gx = grid_for(maxn, 16);
-        hipLaunchKernelGGL(k_sgd, dim3(gx, cnt), dim3(kBlock), 0, (hipStream_t)s, tab, lr, momentum, dampening,
-                           weight_decay, nesterov);
+        hipLaunchKernelGGL(k_sgd, dim3((unsigned)blocks), dim3(kBlock), 0, (hipStream_t)s, tab, lr, momentum,
+                           dampening, weight_decay, nesterov);
         int st = status();
         if (st)
             return st;
