@@ -582,33 +582,43 @@ __global__ void __launch_bounds__(256) k_pack_slab(int mn_major, const uint16_t 
 }
 
 // split-K finish: C = (beta ? C : 0) + sum over the `splits` partial
-// products (each m x n, dense), added in split order.  Rows run along
-// grid y (stride gridDim.y) and columns along x, four per thread when n and
-// ldc allow 16-byte accesses: no index division anywhere
+// products (each m x n, dense), added in split order.  With n and ldc
+// allowing 16-byte accesses, rows run along grid y (stride gridDim.y) and
+// columns along x, four per thread; otherwise (narrow outputs such as
+// n = 10) one element per thread over the flattened m x n, indexed with a
+// 32-bit division when m n fits
 __global__ void __launch_bounds__(256) k_splitk_sum(const float *__restrict__ part, int splits, int m, int n,
-                                                    float *__restrict__ c, size_t ldc, int beta)
+                                                    float *__restrict__ c, size_t ldc, int beta, int v4)
 {
     const size_t mn = (size_t)m * n;
-    const bool v4 = ((n | (int)(ldc & 3)) & 3) == 0 && (((uintptr_t)c | (uintptr_t)part) & 15) == 0;
-    const int cols = v4 ? n >> 2 : n;
-    const int j = blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= cols)
-        return;
-    for (int r = blockIdx.y; r < m; r += gridDim.y) {
-        const float *p = part + (size_t)r * n;
-        float *o = c + (size_t)r * ldc;
-        if (v4) {
+    if (v4) {
+        const int j = blockIdx.x * blockDim.x + threadIdx.x;
+        if (j >= n >> 2)
+            return;
+        for (int r = blockIdx.y; r < m; r += gridDim.y) {
+            const float *p = part + (size_t)r * n + 4 * j;
             f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
             for (int z = 0; z < splits; ++z)
-                acc += *(const f32x4 *)(p + (size_t)z * mn + 4 * j);
-            f32x4 *q = (f32x4 *)(o + 4 * j);
+                acc += *(const f32x4 *)(p + (size_t)z * mn);
+            f32x4 *q = (f32x4 *)(c + (size_t)r * ldc + 4 * j);
             *q = beta ? *q + acc : acc;
-        } else {
-            float acc = 0.0f;
-            for (int z = 0; z < splits; ++z)
-                acc += p[(size_t)z * mn + j];
-            o[j] = beta ? o[j] + acc : acc;
         }
+        return;
+    }
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < mn; i += (size_t)gridDim.x * blockDim.x) {
+        size_t r, col;
+        if (mn <= 0xffffffffu) {
+            r = (uint32_t)i / (uint32_t)n;
+            col = (uint32_t)i - (uint32_t)r * (uint32_t)n;
+        } else {
+            r = i / n;
+            col = i - r * n;
+        }
+        float acc = 0.0f;
+        for (int z = 0; z < splits; ++z)
+            acc += part[(size_t)z * mn + i];
+        float *o = c + r * ldc + col;
+        *o = beta ? *o + acc : acc;
     }
 }
 
@@ -941,9 +951,8 @@ extern "C" int pgk_gemm16(int dtype, int ta, int tb, size_t m, size_t n, size_t 
             return rc;
         {
             const bool v4 = ((n | (ldc & 3)) & 3) == 0 && (((uintptr_t)c | (uintptr_t)part) & 15) == 0;
-            const size_t cols = v4 ? n / 4 : n;
-            hipLaunchKernelGGL(k_splitk_sum, dim3((unsigned)((cols + 255) / 256), (unsigned)(m < 65535 ? m : 65535)),
-                               dim3(256), 0, st, part, sp, (int)m, (int)n, c, ldc, beta);
+            const dim3 grid = v4 ? dim3((unsigned)((n / 4 + 255) / 256), (unsigned)(m < 65535 ? m : 65535)) : dim3(gmn);
+            hipLaunchKernelGGL(k_splitk_sum, grid, dim3(256), 0, st, part, sp, (int)m, (int)n, c, ldc, beta, (int)v4);
         }
         rc = (int)hipGetLastError();
         if (rc)
