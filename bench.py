@@ -65,6 +65,32 @@ class HipEvents:
             getattr(self.hip, fn).argtypes = args
             getattr(self.hip, fn).restype = C.c_int
 
+    def time_segments(self, segments) -> float:
+        """segments: (prepare, fn, n) triples, run in order on the stream:
+        prepare() untimed, then fn() n times between two events.  Nothing
+        waits in between, so the host keeps enqueueing ahead of the device.
+        Returns the summed milliseconds of the timed parts."""
+        evs = []
+        for prepare, fn, n in segments:
+            a, b = C.c_void_p(), C.c_void_p()
+            self.hip.hipEventCreate(C.byref(a))
+            self.hip.hipEventCreate(C.byref(b))
+            prepare()
+            self.hip.hipEventRecord(a, self.stream)
+            for _ in range(n):
+                fn()
+            self.hip.hipEventRecord(b, self.stream)
+            evs.append((a, b))
+        total = 0.0
+        for a, b in evs:
+            self.hip.hipEventSynchronize(b)
+            ms = C.c_float()
+            self.hip.hipEventElapsedTime(C.byref(ms), a, b)
+            total += ms.value
+            self.hip.hipEventDestroy(a)
+            self.hip.hipEventDestroy(b)
+        return total
+
     def time(self, fn, steps: int) -> float:
         a, b = C.c_void_p(), C.c_void_p()
         self.hip.hipEventCreate(C.byref(a))
@@ -254,6 +280,39 @@ def _ref_threads() -> int:
     return min(os.cpu_count() or 1, 64)
 
 
+def host_info() -> dict:
+    """What the CPU figures were measured on: CPU model, the ISA extensions
+    that decide which reference micro-kernels run (backend/cpu/gemm.c:259-360),
+    logical CPUs available, glibc, and the compiler and flags of the
+    reference build in oracle/_ref."""
+    model, flags = None, set()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name") and model is None:
+                    model = line.split(":", 1)[1].strip()
+                elif line.startswith("flags") and not flags:
+                    flags = set(line.split(":", 1)[1].split())
+    except OSError:
+        pass
+    isa = {k: k in flags for k in ("avx2", "fma", "f16c", "avx512f", "avx512_bf16", "avx512_fp16",
+                                   "amx_bf16", "amx_tile")}
+    try:
+        cpus = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        cpus = os.cpu_count()
+    build = None
+    info = ROOT / "oracle" / "_ref" / "build_info.txt"
+    if info.exists():
+        build = info.read_text().strip().splitlines()
+    try:
+        glibc = os.confstr("CS_GNU_LIBC_VERSION")
+    except (ValueError, OSError):
+        glibc = None
+    return {"cpu_model": model, "isa": isa, "logical_cpus": cpus, "glibc": glibc,
+            "reference_build": build, "reference_pool_threads": _ref_threads()}
+
+
 def cpu_c2(rows=2048, Cc=4096, budget_s=20.0):
     """The reference CPU path (oracle/_ref) on a row sample of config 2."""
     from oracle_lib import REF_SO
@@ -356,7 +415,9 @@ def cpu_c3(M=1024, K=4096, N=4096, budget_s=20.0):
         R.pg_node_free(n)
     t = float(np.median(times))
     flops = 2 * 2 * M * N * K
-    return {"value": flops / t / 1e12, "unit": "TFLOP/s", "sample": f"M={M} of 8192", "ms": t * 1e3}
+    return {"value": flops / t / 1e12, "unit": "TFLOP/s", "cores": _ref_threads(), "kind": "reference",
+            "sample": f"bwd_matmul at M={M} of 8192 (bf16 upcast, transposes, the pool's f32 sgemm), "
+                      f"median of {len(times)}", "ms": t * 1e3}
 
 
 # ---------------------------------------------------------------- config 4
@@ -431,9 +492,21 @@ def c5_counts(dims=C5_DIMS, batch=C5_BATCH):
     return fwd, bwd, params, 20 * params + 2 * shadow
 
 
+C5_CHUNK = 3  # steps between restores of the initial state
+
+
 def bench_c5(L, ev, steps, warmup, dims=C5_DIMS, batch=C5_BATCH, fused=True):
     """Config 5: forward + pg_backward + pg_sgd_step of the bf16-GEMM MLP,
-    layers as pg_amd_ag_linear16 nodes (fused) or matmul16 + add + gelu."""
+    layers as pg_amd_ag_linear16 nodes (fused) or matmul16 + add + gelu.
+
+    The reference's mean_all makes this loss a sum over the batch, so at
+    lr 0.01 it diverges (inf by step 4, NaN by step 5, in the reference as
+    here).  Every run of C5_CHUNK steps therefore starts from the initial
+    state: parameters copied back on the device from a snapshot, momentum
+    buffers zeroed (as before the first step) and the bf16 weight copies
+    remade, all enqueued outside the timed events.  Each timed step is one of
+    steps 1-3 of the same trajectory, and every timed step's loss is checked
+    finite."""
     from picograd_amd.capi import BF16, shape_arg
     from picograd_amd.mlp import Mlp
     log(f"[c5] MLP {dims}, batch {batch}, bf16 GEMM operands, f32 masters, fused={fused}")
@@ -443,15 +516,40 @@ def bench_c5(L, ev, steps, warmup, dims=C5_DIMS, batch=C5_BATCH, fused=True):
     nd, sh = shape_arg((batch, dims[-1]))
     t = L._check(L.pg_var_normal(nd, sh, 0.0, 1.0, False))
     mlp = Mlp.seeded(L, dims, BF16, fused=fused)
-    loss0 = mlp.step(x, t, keep_loss=True)
-    first = float(L.value(loss0)[0])
-    L.pg_node_free(loss0)
-    for _ in range(max(0, warmup - 1)):
-        mlp.step(x, t)
+    params = [L.node(n).value for n in mlp.Ws + mlp.bs]
+    snap = [L.pg_tensor_clone(p) for p in params]
+    losses = []
+
+    def one():
+        n = mlp.step(x, t, keep_loss=True)
+        losses.append(L.pg_tensor_view(L.node(n).value))  # keeps the 4 bytes, not the graph
+        L.pg_node_free(n)
+
+    one()  # creates the momentum buffers
+    bufs = [L.pg_amd_sgd_buffer(mlp.opt, i) for i in range(len(params))]
+    assert all(bufs), "momentum buffers missing after the first step"
+
+    def restore():
+        for p, s0 in zip(params, snap):
+            L.pg_tensor_copy_from(p, s0)
+        for b in bufs:
+            L.pg_tensor_fill(b, 0.0)
+        for p in params:
+            L.pg_amd_tensor_refresh16(p)
+
+    def segments(n):
+        out = []
+        while n > 0:
+            k = min(C5_CHUNK, n)
+            out.append((restore, one, k))
+            n -= k
+        return out
+
+    ev.time_segments(segments(max(warmup, C5_CHUNK)))
     L.sync()
     L.pg_amd_timer_reset()
     L.pg_amd_timer_enable(1)
-    ev.time(lambda: mlp.step(x, t), steps)
+    ev.time_segments(segments(steps))
     L.pg_amd_timer_enable(0)
     g_ms, g_n = timer_ms(L, T_GEMM16)
     s_ms, s_n = timer_ms(L, T_SGD)
@@ -459,15 +557,21 @@ def bench_c5(L, ev, steps, warmup, dims=C5_DIMS, batch=C5_BATCH, fused=True):
     f_ms, f_n = timer_ms(L, T_JIT_FIN)
     a_ms, a_n = timer_ms(L, T_STAGE)
     L.pg_amd_timer_reset()
-    ms = ev.time(lambda: mlp.step(x, t), steps)
-    lossN = mlp.step(x, t, keep_loss=True)
-    last = float(L.value(lossN)[0])
-    L.pg_node_free(lossN)
+    n_before = len(losses)
+    ms = ev.time_segments(segments(steps))
+    vals = [float(L.read(v)[0]) for v in losses]
+    timed = vals[n_before:]
+    for v in losses:
+        L.pg_tensor_free(v)
+    for s0 in snap:
+        L.pg_tensor_free(s0)
     mlp.free()
     L.pg_node_free(x)
     L.pg_node_free(t)
     L.sync()
-    fwd, bwd, params, sgd_bytes = c5_counts(dims, batch)
+    if not all(math.isfinite(v) for v in vals):
+        raise RuntimeError(f"config 5: a non-finite loss among the measured steps: {vals}")
+    fwd, bwd, params_n, sgd_bytes = c5_counts(dims, batch)
     step_ms = ms / steps
     gemm_ms = g_ms / steps
     sgd_ms = s_ms / max(s_n, 1)
@@ -476,14 +580,12 @@ def bench_c5(L, ev, steps, warmup, dims=C5_DIMS, batch=C5_BATCH, fused=True):
             "gemm_ms_per_step": gemm_ms, "gemm_tflops": (fwd + bwd) / (gemm_ms * 1e-3) / 1e12,
             "gemm_launches_per_step": g_n / steps,
             "sgd_ms": sgd_ms, "sgd_gbs": sgd_bytes / (sgd_ms * 1e-3) / 1e9, "sgd_bytes": sgd_bytes,
-            "params": params, "fused_bwd_ms_per_step": (j_ms + f_ms) / steps,
+            "params": params_n, "fused_bwd_ms_per_step": (j_ms + f_ms) / steps,
             "act_bwd_ms_per_step": a_ms / steps,
-            # the reference's mean_all makes this loss a sum over the batch, so
-            # lr 0.01 diverges within a few steps (as in the reference); a
-            # non-finite loss is reported as null to keep the line strict JSON
-            "loss_first": first if math.isfinite(first) else None,
-            "loss_last": last if math.isfinite(last) else None,
-            "steps_run": 1 + max(0, warmup - 1) + 2 * steps + 1}
+            "restore_every": C5_CHUNK,
+            "loss_first": vals[0], "loss_last": timed[-1],
+            "losses_timed": sorted(set(round(v, 3) for v in timed)),
+            "steps_run": len(vals)}
 
 
 def cpu_c5(dims=C5_DIMS, batch=C5_BATCH, budget_s=25.0):
@@ -811,12 +913,12 @@ def cpu_c1():
     if not REF_SO.exists():
         return None
     R = PgLib(REF_SO, device=False)
-    jit = chain_backward_loop(R, (64, 64), 3000)
+    jit = chain_backward_loop(R, (64, 64), 10000)
     R.pg_autograd_set_jit(False)
-    eager = chain_backward_loop(R, (64, 64), 3000)
+    eager = chain_backward_loop(R, (64, 64), 10000)
     R.pg_autograd_set_jit(True)
     return {"value": jit, "unit": "us/iter", "eager_us_per_iter": eager, "cores": 1, "kind": "reference",
-            "sample": "3000 iterations of the config-1 loop, JIT on (value) and off"}
+            "sample": "10,000 iterations of the config-1 loop, JIT on (value) and off"}
 
 
 def bench_jit(L):
@@ -847,7 +949,7 @@ def cpu_jit():
 
 # ---------------------------------------------------------------- config 1
 
-def bench_c1(L, iters=2000):
+def bench_c1(L, iters=10000):
     from oracle_lib import Oracle
     o = Oracle()
     o.orc_seed(42)
@@ -939,6 +1041,8 @@ def main(argv=None):
     if not a.no_cpu:
         log("[cpu] reference CPU path, config 2 sample")
         cpu = cpu_c2()
+        if cpu is not None:
+            cpu["host"] = host_info()
         if "c3" in only and cpu is not None:
             log("[cpu] reference CPU path, config 3 sample")
             c3cpu = cpu_c3()

@@ -61,6 +61,12 @@ pg_node *pg_amd_ag_matmul16(pg_node *a, pg_node *b, pg_dtype dtype);
  * sync_device, pg_jit_run outputs, pg_sgd_step) are tracked already. */
 void pg_amd_tensor_modified(pg_tensor *t);
 
+/* Remakes t's kept 16-bit copy now if it has one that a write made stale
+ * (the next GEMM would otherwise remake it on first use).  Enqueued on the
+ * library stream; false on a device error.  No counterpart in the
+ * reference, which keeps no such copies. */
+bool pg_amd_tensor_refresh16(pg_tensor *t);
+
 /* Activation codes of pg_amd_ag_linear16: the reference's PG_ACT_* values
  * (backend/cpu/gemm.h:37-39). */
 #ifndef PG_ACT_NONE
@@ -109,6 +115,13 @@ bool pg_amd_params_save(pg_node *const *params, size_t n, const char *path);
 bool pg_amd_params_save_fp(pg_node *const *params, size_t n, FILE *fp);
 bool pg_amd_params_load_into(pg_node *const *params, size_t n, const char *path);
 bool pg_amd_params_load_into_fp(pg_node *const *params, size_t n, FILE *fp);
+
+/* The momentum buffer of the optimiser's i-th parameter (registration
+ * order), owned by the optimiser; NULL before the first pg_sgd_step that
+ * updated it, without momentum, or for i out of range.  The reference keeps
+ * the buffers private (opt/sgd.c:6-16); callers that save, restore or reset
+ * optimiser state on the device read them here. */
+pg_tensor *pg_amd_sgd_buffer(pg_sgd *opt, size_t i);
 
 /* Optimiser state, which the reference cannot checkpoint (its SGD momentum
  * and Adam moments live only in memory; adam.h:42-44 lets a caller restore

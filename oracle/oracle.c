@@ -383,6 +383,7 @@ typedef struct {
     const void *a, *b;
     void *c;
     size_t r0, r1;
+    const float *panels; /* f32 path: B upcast into [n/16][k][16] */
 } gemm_job;
 
 static inline float ld_elem(int dtype, const void *p, size_t idx)
@@ -393,9 +394,62 @@ static inline float ld_elem(int dtype, const void *p, size_t idx)
     return dtype == ORC_F16 ? orc_f16_to_f32(h) : orc_bf16_to_f32(h);
 }
 
+/* f32 accumulation, four rows x 16 columns at a time.  Every output is still
+ * acc = 0; acc = acc + a[p]*b[p] for p = 0..k-1 in order, each product and
+ * sum rounded on its own (the file is built with -ffp-contract=off and AVX2
+ * has no FMA without -mfma), so the result is the serial dot product bit for
+ * bit; the vectors only run 64 of those chains side by side.  B is upcast
+ * once into 16-column panels [n/16][k][16] shared by all threads. */
+typedef float orc_v8 __attribute__((vector_size(32)));
+
+__attribute__((target("avx2"))) static void gemm_worker_f32(gemm_job *j, const float *panels)
+{
+    size_t k = j->k, npan = (j->n + 15) / 16;
+    float *arows = malloc((k ? k : 1) * sizeof(float) * 4);
+    for (size_t i0 = j->r0; i0 < j->r1; i0 += 4) {
+        size_t ni = j->r1 - i0 < 4 ? j->r1 - i0 : 4;
+        for (size_t r = 0; r < 4; r++)
+            for (size_t p = 0; p < k; p++) {
+                size_t i = i0 + (r < ni ? r : 0);
+                size_t idx = j->ta ? p * j->lda + i : i * j->lda + p;
+                arows[r * k + p] = ld_elem(j->dtype, j->a, idx);
+            }
+        for (size_t pj = 0; pj < npan; pj++) {
+            const float *bp = panels + pj * k * 16;
+            orc_v8 acc[4][2];
+            memset(acc, 0, sizeof acc);
+            for (size_t p = 0; p < k; p++) {
+                orc_v8 b0, b1;
+                memcpy(&b0, bp + p * 16, 32);
+                memcpy(&b1, bp + p * 16 + 8, 32);
+                for (size_t r = 0; r < 4; r++) {
+                    float av = arows[r * k + p];
+                    orc_v8 a8 = {av, av, av, av, av, av, av, av};
+                    orc_v8 p0 = a8 * b0, p1 = a8 * b1;
+                    acc[r][0] = acc[r][0] + p0;
+                    acc[r][1] = acc[r][1] + p1;
+                }
+            }
+            size_t jb = pj * 16, nj = j->n - jb < 16 ? j->n - jb : 16;
+            for (size_t r = 0; r < ni; r++) {
+                float out[16];
+                memcpy(out, acc[r], sizeof out);
+                float *cp = (float *)j->c + (i0 + r) * j->ldc + jb;
+                for (size_t q = 0; q < nj; q++)
+                    cp[q] = j->beta ? cp[q] + out[q] : out[q];
+            }
+        }
+    }
+    free(arows);
+}
+
 static void *gemm_worker(void *arg)
 {
     gemm_job *j = arg;
+    if (!j->f64) {
+        gemm_worker_f32(j, j->panels);
+        return NULL;
+    }
     float *arow = malloc(j->k * sizeof(float));
     float *bcol = malloc(j->k * sizeof(float) * 16);
     for (size_t jb = 0; jb < j->n; jb += 16) {
@@ -444,11 +498,24 @@ static void gemm_run(int dtype, int ta, int tb, size_t m, size_t n, size_t k,
     gemm_job *jobs = calloc((size_t)nthreads, sizeof(gemm_job));
     pthread_t *th = calloc((size_t)nthreads, sizeof(pthread_t));
     size_t per = (m + (size_t)nthreads - 1) / (size_t)nthreads;
+    float *panels = NULL;
+    if (!f64) {
+        size_t npan = (n + 15) / 16;
+        size_t nf = npan * k * 16;
+        panels = malloc((nf ? nf : 1) * sizeof(float));
+        for (size_t pj = 0; pj < npan; pj++)
+            for (size_t p = 0; p < k; p++)
+                for (size_t q = 0; q < 16; q++) {
+                    size_t col = pj * 16 + q;
+                    size_t idx = tb ? col * ldb + p : p * ldb + col;
+                    panels[(pj * k + p) * 16 + q] = col < n ? ld_elem(dtype, b, idx) : 0.0f;
+                }
+    }
     for (int t = 0; t < nthreads; t++) {
         gemm_job *j = &jobs[t];
         j->dtype = dtype; j->ta = ta; j->tb = tb; j->beta = beta; j->f64 = f64;
         j->m = m; j->n = n; j->k = k; j->lda = lda; j->ldb = ldb; j->ldc = ldc;
-        j->a = a; j->b = b; j->c = c;
+        j->a = a; j->b = b; j->c = c; j->panels = panels;
         j->r0 = (size_t)t * per < m ? (size_t)t * per : m;
         j->r1 = j->r0 + per < m ? j->r0 + per : m;
     }
@@ -457,6 +524,7 @@ static void gemm_run(int dtype, int ta, int tb, size_t m, size_t n, size_t k,
     gemm_worker(&jobs[0]);
     for (int t = 1; t < nthreads; t++)
         pthread_join(th[t], NULL);
+    free(panels);
     free(jobs);
     free(th);
 }
@@ -497,6 +565,14 @@ static float gelu_grad(float x)
     float erf_term = erff(x * inv_sqrt2);
     float phi = expf(-0.5f * x * x) / sqrt_2pi;
     return 0.5f * (1.0f + erf_term) + x * phi;
+}
+
+void orc_gelu_backward(const float *z, const float *g, float *out, size_t n)
+{
+    /* bwd_unary_elemwise with grad_gelu (autograd.c:519-559, :794-801):
+     * out = g * gelu'(z) */
+    for (size_t i = 0; i < n; i++)
+        out[i] = g[i] * gelu_grad(z[i]);
 }
 
 void orc_chain1_backward(const float *a, const float *b, const float *c,

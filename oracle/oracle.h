@@ -124,6 +124,9 @@ void orc_gemm_acc64(int dtype, int ta, int tb, size_t m, size_t n, size_t k,
                     const void *a, size_t lda, const void *b, size_t ldb,
                     double *c, size_t ldc, int nthreads);
 
+/* out = g * gelu'(z), the eager GELU backward (autograd.c:519-559, :794-801) */
+void orc_gelu_backward(const float *z, const float *g, float *out, size_t n);
+
 /*
  * Config-1 chain: loss = sum_all(tanh(relu((a+b)*c))), flat n elements.
  * Writes dL/da, dL/db, dL/dc (autograd.c:2166-2297 chain rule as the JIT

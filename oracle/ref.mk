@@ -39,6 +39,10 @@ $(OUT)/libref_convert.so: $(dir $(lastword $(MAKEFILE_LIST)))ref_convert_shim.c
 	@mkdir -p $(OUT)
 	$(CC_REF) $(CFLAGS_REF) -shared -o $@ $<
 
-ref: $(OUT)/libpicograd_ref.so $(OUT)/libref_convert.so
+# compiler and flags of this build, reported beside the CPU timings
+$(OUT)/build_info.txt: $(OUT)/libpicograd_ref.so
+	@{ $(CC_REF) --version | head -1; echo "CFLAGS $(CFLAGS_REF)"; } > $@
+
+ref: $(OUT)/libpicograd_ref.so $(OUT)/libref_convert.so $(OUT)/build_info.txt
 .PHONY: ref
 .DEFAULT_GOAL := ref

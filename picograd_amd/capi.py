@@ -179,6 +179,11 @@ _AMD_PROTOS = {
     "pg_amd_ag_matmul16": (vp, [vp, vp, ip]),
     "pg_amd_ag_linear16": (vp, [vp, vp, vp, ip, ip]),
     "pg_amd_tensor_modified": (None, [vp]),
+    "pg_amd_tensor_refresh16": (bo, [vp]),
+    "pg_amd_sgd_buffer": (vp, [vp, sz]),
+    "pg_tensor_clone": (vp, [vp]),
+    "pg_tensor_view": (vp, [vp]),
+    "pg_tensor_copy_from": (None, [vp, vp]),
     "pg_amd_jit_compiles": (sz, []),
     "pg_amd_jit_cache_hits": (sz, []),
     "pg_tensor_sync_host": (bo, [vp]),

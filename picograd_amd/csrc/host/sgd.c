@@ -79,6 +79,11 @@ int pg_sgd_add_param(pg_sgd *opt, pg_node *param)
 
 size_t pg_sgd_num_params(const pg_sgd *opt) { return opt ? opt->n : 0; }
 
+pg_tensor *pg_amd_sgd_buffer(pg_sgd *opt, size_t i)
+{
+    return opt && i < opt->n ? opt->st[i].buf : NULL;
+}
+
 void pg_sgd_zero_grad(pg_sgd *opt)
 {
     assert(opt);

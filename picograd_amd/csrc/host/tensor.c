@@ -262,6 +262,16 @@ void pgt_touch(pg_tensor *t)
 
 void pg_amd_tensor_modified(pg_tensor *t) { pgt_touch(t); }
 
+bool pg_amd_tensor_refresh16(pg_tensor *t)
+{
+    if (!t || !t->data_ref)
+        return false;
+    pg_data_ref *r = t->data_ref;
+    if (!r->shadow || !r->shadow_stale)
+        return true;
+    return pgt_shadow16(t, (pg_dtype)r->shadow_dtype) != NULL;
+}
+
 const uint16_t *pgt_shadow16(pg_tensor *t, pg_dtype dt)
 {
     if (!t || !t->data_ref || t->dtype != PG_DTYPE_F32 || (dt != PG_DTYPE_F16 && dt != PG_DTYPE_BF16)) {

@@ -47,6 +47,7 @@ class Oracle:
             "orc_chain1_backward": (None, [_vp, _vp, _vp, _sz, _vp, _vp, _vp]),
             "orc_chain2_backward": (None, [_vp, _vp, _vp, _sz, _sz, _vp, _vp, _vp, _vp]),
             "orc_gelu": (_fl, [_fl]),
+            "orc_gelu_backward": (None, [_vp, _vp, _vp, _sz]),
             "orc_sigmoid": (_fl, [_fl]),
             "orc_mse_grad_scale": (_fl, [_sz, C.POINTER(_sz), C.c_bool]),
             "orc_mlp_step": (None, [_ip, _sz, C.POINTER(_sz), _sz, _vp, _vp, C.POINTER(_vp), C.POINTER(_vp),
@@ -138,6 +139,15 @@ class Oracle:
     def pgt1_check(self, blob: bytes) -> int:
         buf = (C.c_ubyte * max(1, len(blob))).from_buffer_copy(blob + b"\0" * (len(blob) == 0))
         return self.orc_pgt1_check(buf, len(blob))
+
+    def gelu_backward(self, z, g):
+        """g * gelu'(z) elementwise (f32 arrays of one shape)."""
+        z = np.ascontiguousarray(z, np.float32)
+        g = np.ascontiguousarray(g, np.float32)
+        assert z.shape == g.shape
+        out = np.empty_like(z)
+        self.orc_gelu_backward(z.ctypes.data, g.ctypes.data, out.ctypes.data, z.size)
+        return out
 
     def chain1(self, a, b, c):
         da, db, dc = (np.empty_like(a) for _ in range(3))

@@ -459,6 +459,24 @@ def test_chain2_gelu_grad_closed_form_and_planted_mistake(oracle):
     assert max_rel(s * Phi, g["dx_jit"]) > 1e-3
 
 
+def test_gelu_backward_matches_reference_eager_grad(oracle):
+    """orc_gelu_backward(z, g) = g * gelu'(z): the reference's eager chain-2
+    backward computes dx = sigmoid(g) * grad_gelu(x + bias) with exactly this
+    call (autograd.c:519-559, :794-801), so its golden dx_eager is reproduced
+    to f32 rounding; the f64 closed form Phi + x phi agrees, and dropping the
+    x phi term fails."""
+    g = golden("chain2")
+    t0 = (g["x"] + g["bias"]).astype(np.float32)
+    s = (1.0 / (1.0 + np.exp(-g["g"].astype(np.float64)))).astype(np.float32)
+    got = oracle.gelu_backward(t0, s)
+    assert max_rel(got, g["dx_eager"]) <= 1e-5
+    t = t0.astype(np.float64)
+    Phi = 0.5 * (1.0 + np.vectorize(math.erf)(t / math.sqrt(2.0)))
+    phi = np.exp(-0.5 * t * t) / math.sqrt(2.0 * math.pi)
+    assert max_rel(got, s * (Phi + t * phi)) <= 1e-5
+    assert max_rel(s * Phi, got) > 1e-3
+
+
 # ---------------------------------------------------------------- GEMM
 
 def _gemm_keys(g):
@@ -510,6 +528,32 @@ def test_gemm_brute_force_and_transpose_flags(oracle):
         assert rel_fro(oracle.gemm(BF16, a16, np.ascontiguousarray(b16.T), tb=True), want) <= 1e-6
         if m == n == k:
             assert rel_fro(oracle.gemm(BF16, a16, b16, ta=True), want) > 1e-2
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1), (1, 1)])
+def test_gemm_acc32_is_the_serial_dot_product(oracle, ta, tb):
+    """orc_gemm_acc32 computes each output as acc = acc + a*b over k in order,
+    every product and sum rounded to f32: numpy float32 arithmetic over the
+    whole output at once does the same per element, so the two agree bit for
+    bit (ragged m, n; beta = 1 adds the sum to the old C after the loop)."""
+    rng = np.random.default_rng(5)
+    m, n, k = 7, 37, 300
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float32)
+    a16, b16 = oracle.cast16(BF16, a), oracle.cast16(BF16, b)
+    af, bf = bf16_to_f32(a16), bf16_to_f32(b16)
+    acc = np.zeros((m, n), np.float32)
+    for p in range(k):
+        acc = acc + np.outer(af[:, p], bf[p, :]).astype(np.float32)
+    A = np.ascontiguousarray(a16.T) if ta else a16
+    B = np.ascontiguousarray(b16.T) if tb else b16
+    got = oracle.gemm(BF16, A, B, ta=bool(ta), tb=bool(tb), threads=3)
+    assert np.array_equal(got.view(np.uint32), acc.view(np.uint32))
+    c0 = rng.standard_normal((m, n)).astype(np.float32)
+    c = c0.copy()
+    oracle.orc_gemm_acc32(BF16, ta, tb, m, n, k, A.ctypes.data, A.shape[1], B.ctypes.data, B.shape[1],
+                          c.ctypes.data, n, 1, 2)
+    assert np.array_equal(c.view(np.uint32), (c0 + acc).view(np.uint32))
 
 
 def test_matmul_backward_matches_reference(oracle):
