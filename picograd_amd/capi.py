@@ -180,6 +180,7 @@ _AMD_PROTOS = {
     "pg_amd_ag_linear16": (vp, [vp, vp, vp, ip, ip]),
     "pg_amd_tensor_modified": (None, [vp]),
     "pg_amd_tensor_refresh16": (bo, [vp]),
+    "pg_amd_gemm_ex_noalloc": (ip, [ip, sz, sz, sz, vp, sz, vp, sz, vp, sz]),
     "pg_amd_sgd_buffer": (vp, [vp, sz]),
     "pg_tensor_clone": (vp, [vp]),
     "pg_tensor_view": (vp, [vp]),
@@ -191,6 +192,7 @@ _AMD_PROTOS = {
     "pg_tensor_copy_to_host": (bo, [vp, vp]),
     "pg_tensor_copy_from_host": (bo, [vp, vp]),
     "pg_tensor_empty_dtype": (vp, [ip, sz, SZP]),
+    "pg_tensor_full_dtype": (vp, [ip, sz, SZP, fl]),
     "pg_amd_timer_enable": (None, [ip]),
     "pg_amd_mfma_probe": (C.c_double, [ip]),
     "pg_amd_timer_read": (C.c_double, [ip, C.POINTER(C.c_size_t)]),

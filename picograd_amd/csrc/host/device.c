@@ -63,9 +63,16 @@ int pg_amd_init(void)
         g_init_state = -1;
         return -1;
     }
+    /* the device address of the no-alloc workspace (pg_amd_gemm_ex_noalloc) */
+    if (!pgd_check(pgk_noalloc_scratch_init(), "no-alloc workspace")) {
+        g_init_state = -1;
+        return -1;
+    }
     g_init_state = 1;
     return 0;
 }
+
+bool pgd_initialised(void) { return g_init_state > 0; }
 
 bool pgd_ok(void) { return pg_amd_init() == 0; }
 

@@ -365,6 +365,72 @@ void pg_gemm_ex(pg_dtype dtype, size_t m, size_t n, size_t k, const void *a, siz
         pgd_free(bp, bbytes);
 }
 
+/* pg_gemm_ex with every buffer it needs (the zero-padded operand copies,
+ * split-K partials, k-tail slabs) carved from the fixed no-alloc workspace
+ * instead of the library allocator.  The operands take the same path as in
+ * pg_gemm_ex (read in place when the leading dims and bases allow 16-byte
+ * loads and n is a multiple of 8, else both padded to [m, K8] and [K8, N8]),
+ * so the kernels, the launch plan and the result bits are the same. */
+static size_t up256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+int pg_amd_gemm_ex_noalloc(pg_dtype dtype, size_t m, size_t n, size_t k, const void *a, size_t lda, const void *b,
+                           size_t ldb, float *c, size_t ldc)
+{
+    if (!pgd_initialised()) {
+        pgd_set_err("pg_amd_gemm_ex_noalloc: call pg_amd_init first (initialising may allocate)");
+        return -1;
+    }
+    if (dtype != PG_DTYPE_F32 && dtype != PG_DTYPE_F16 && dtype != PG_DTYPE_BF16) {
+        pgd_set_err("pg_amd_gemm_ex_noalloc: dtype %d is not f32, f16 or bf16", (int)dtype);
+        return -1;
+    }
+    if (!m || !n)
+        return 0;
+    if ((k && (!a || !b)) || !c || lda < k || ldb < n || ldc < n) {
+        pgd_set_err("pg_amd_gemm_ex_noalloc: null operand or a leading dim below its row length");
+        return -1;
+    }
+    pgk_stream st = pgd_stream();
+    if (dtype == PG_DTYPE_F32)
+        return pgd_check(pgk_gemm_f32(0, 0, m, n, k, a, lda, 0, b, ldb, 0, c, ldc, 0, 1, 0, st),
+                         "pg_amd_gemm_ex_noalloc")
+                   ? 0
+                   : -1;
+    unsigned char *ws = pgk_noalloc_scratch();
+    const size_t cap = pgk_noalloc_scratch_bytes();
+    if (!ws) {
+        pgd_set_err("pg_amd_gemm_ex_noalloc: no workspace on the current device");
+        return -1;
+    }
+    int dt = (int)dtype;
+    bool direct = !(lda & 7) && !(ldb & 7) && !(((uintptr_t)a | (uintptr_t)b) & 15) && !(n & 7);
+    size_t K8 = direct ? k : up8(k), N8 = up8(n) < 8 ? 8 : up8(n);
+    size_t abytes = direct ? 0 : up256(m * K8 * 2), bbytes = direct ? 0 : up256(K8 * N8 * 2);
+    size_t wsz = pgk_gemm16_workspace(0, 1, m, n, K8, 1);
+    size_t need = abytes + bbytes + wsz;
+    if (need > cap) {
+        pgd_set_err("pg_amd_gemm_ex_noalloc: %zux%zux%zu needs %zu bytes of workspace, above the no-alloc "
+                    "maximum of %zu",
+                    m, n, k, need, cap);
+        return -1;
+    }
+    const uint16_t *ap = a, *bp = b;
+    size_t lda2 = lda, ldb2 = ldb, bext = n;
+    if (!direct) {
+        uint16_t *pa = (uint16_t *)ws, *pb = (uint16_t *)(ws + abytes);
+        if (!pgd_check(pgk_copy_to16(dt, dt, a, m, k, lda, pa, K8, m, 1, 0, 0, st), "pg_amd_gemm_ex_noalloc") ||
+            !pgd_check(pgk_copy_to16(dt, dt, b, k, n, ldb, pb, N8, K8, 1, 0, 0, st), "pg_amd_gemm_ex_noalloc"))
+            return -1;
+        ap = pa;
+        bp = pb;
+        lda2 = K8;
+        ldb2 = bext = N8;
+    }
+    int rc = pgk_gemm16(dt, 0, 1, m, n, K8, ap, lda2, 0, m, bp, ldb2, 0, bext, c, ldc, 0, 1, 0, NULL,
+                        wsz ? ws + abytes + bbytes : NULL, st);
+    return pgd_check(rc, "pg_amd_gemm_ex_noalloc") ? 0 : -1;
+}
+
 void pg_hgemm(size_t m, size_t n, size_t k, const uint16_t *a, size_t lda, const uint16_t *b, size_t ldb, float *c,
               size_t ldc)
 {

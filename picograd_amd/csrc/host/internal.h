@@ -21,6 +21,7 @@
 
 /* ---- device layer (device.c) ---- */
 bool pgd_ok(void);                 /* init on first use; false if no device */
+bool pgd_initialised(void);        /* pg_amd_init has succeeded (never inits) */
 pgk_stream pgd_stream(void);
 void *pgd_malloc(size_t nbytes);   /* cached, stream-ordered reuse */
 void pgd_free(void *p, size_t nbytes);

@@ -35,6 +35,14 @@ typedef struct {
     int64_t sb[PGK_MAX_NDIM];
 } pgk_bcast;
 
+/* The no-alloc workspace (scratch.hip): a fixed device array per device.
+ * _init records the current device's address of it (once per device) and
+ * returns a hipError_t value; pgk_noalloc_scratch returns that address
+ * (initialising first for a device not seen yet), NULL on failure. */
+size_t pgk_noalloc_scratch_bytes(void);
+int pgk_noalloc_scratch_init(void);
+void *pgk_noalloc_scratch(void);
+
 int pgk_fill_f32(float *dst, size_t n, float v, pgk_stream s);
 
 /* A batch of small uploads written by one kernel: dst[0..n) = src[0..n)
