@@ -61,6 +61,14 @@ pg_node *pg_amd_ag_matmul16(pg_node *a, pg_node *b, pg_dtype dtype);
  * sync_device, pg_jit_run outputs, pg_sgd_step) are tracked already. */
 void pg_amd_tensor_modified(pg_tensor *t);
 
+/* A new tensor of t's elements converted to `dtype` on the device: f32 to
+ * f16/bf16 rounds to nearest even with the bit rules of the reference's
+ * core/convert.h:15-104 (f16 subnormals IEEE-correct), 16-bit to f32 is
+ * exact, equal dtypes copy.  The device form of convert.h:106-152's batch
+ * converters, which the reference exposes only as inline host functions.
+ * NULL (pg_amd_last_error) on failure. */
+pg_tensor *pg_amd_tensor_to_dtype(const pg_tensor *t, pg_dtype dtype);
+
 /* Remakes t's kept 16-bit copy now if it has one that a write made stale
  * (the next GEMM would otherwise remake it on first use).  Enqueued on the
  * library stream; false on a device error.  No counterpart in the

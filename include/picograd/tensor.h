@@ -72,8 +72,11 @@ pg_tensor *pg_tensor_zeros(size_t ndim, const size_t *shape);
 pg_tensor *pg_tensor_ones(size_t ndim, const size_t *shape);
 pg_tensor *pg_tensor_full(size_t ndim, const size_t *shape, float value);
 pg_tensor *pg_tensor_from_data(size_t ndim, const size_t *shape, const float *data);
+pg_tensor *pg_tensor_arange(float start, float stop, float step);
 pg_tensor *pg_tensor_uniform(size_t ndim, const size_t *shape, float low, float high);
 pg_tensor *pg_tensor_normal(size_t ndim, const size_t *shape, float mean, float stddev);
+pg_tensor *pg_tensor_linspace(float start, float stop, size_t num);
+pg_tensor *pg_tensor_eye(size_t n);
 
 pg_tensor *pg_tensor_clone(const pg_tensor *t);
 void pg_tensor_free(pg_tensor *t);
@@ -86,6 +89,12 @@ static inline size_t pg_tensor_nbytes(const pg_tensor *t) { return t->numel * t-
 /* splitmix64 stream shared by pg_tensor_uniform/normal (tensor.c:289-339) */
 void pg_seed(unsigned long long seed);
 
+/* tensor.h:68-69: one element at a multi-index (strides honoured).  get
+ * waits for the queued work and reads the element from device memory; set
+ * queues the write (rounded to nearest even for f16/bf16). */
+float pg_tensor_get(const pg_tensor *t, const size_t *idx);
+void pg_tensor_set(pg_tensor *t, const size_t *idx, float value);
+
 void pg_tensor_fill(pg_tensor *t, float value);
 void pg_tensor_copy_from(pg_tensor *dst, const pg_tensor *src);
 bool pg_tensor_reshape(pg_tensor *t, size_t ndim, const size_t *shape);
@@ -93,8 +102,16 @@ bool pg_tensor_reshape(pg_tensor *t, size_t ndim, const size_t *shape);
 size_t pg_shape_numel(size_t ndim, const size_t *shape);
 bool pg_shape_equal(size_t ndim_a, const size_t *shape_a, size_t ndim_b, const size_t *shape_b);
 
+/* tensor.h:78-79: both wait for the queued work.  allclose compares
+ * |a - b| <= atol + rtol |b| elementwise in f32 (f16/bf16 widened), false
+ * for different shapes; print writes the reference's nested-bracket text. */
+bool pg_tensor_allclose(const pg_tensor *a, const pg_tensor *b, float rtol, float atol);
+void pg_tensor_print(const pg_tensor *t, FILE *out);
+
+/* views share the storage (reference counted); tensor.h:82-84 */
 pg_tensor *pg_tensor_view(const pg_tensor *src);
 pg_tensor *pg_tensor_reshape_view(const pg_tensor *src, size_t ndim, const size_t *shape);
+pg_tensor *pg_tensor_permute_view(const pg_tensor *src, const size_t *order);
 
 /* serialization, tensor.h:86-91 of the reference: the PGT1 format ("PGT1",
  * u32 version 1, u32 dtype, u32 ndim, u64 shape[ndim], u64 numel, u64
@@ -108,6 +125,13 @@ bool pg_tensor_save(const pg_tensor *t, const char *path);
 pg_tensor *pg_tensor_load(const char *path);
 bool pg_tensor_save_fp(const pg_tensor *t, FILE *fp);
 pg_tensor *pg_tensor_load_fp(FILE *fp);
+
+/* tensor.h:93-95: the reference pools freed host buffers; here the pool
+ * is the device allocator's cache of freed blocks (count and bytes held;
+ * clear returns them to the driver after the queued work). */
+void pg_tensor_pool_clear(void);
+size_t pg_tensor_pool_size(void);
+size_t pg_tensor_pool_bytes(void);
 
 /* ---- appended: host/device synchronisation ---- */
 /* Waits for queued device work, then copies the elements into the host

@@ -180,6 +180,7 @@ _AMD_PROTOS = {
     "pg_amd_ag_linear16": (vp, [vp, vp, vp, ip, ip]),
     "pg_amd_tensor_modified": (None, [vp]),
     "pg_amd_tensor_refresh16": (bo, [vp]),
+    "pg_amd_tensor_to_dtype": (vp, [vp, ip]),
     "pg_amd_gemm_ex_noalloc": (ip, [ip, sz, sz, sz, vp, sz, vp, sz, vp, sz]),
     "pg_amd_sgd_buffer": (vp, [vp, sz]),
     "pg_tensor_clone": (vp, [vp]),

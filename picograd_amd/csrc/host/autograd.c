@@ -509,7 +509,7 @@ static pg_tensor *lz_record(int code, int nin, const pg_tensor *const *x, size_t
     return y;
 }
 
-static pg_tensor *binary_fwd(int op, const pg_tensor *a, const pg_tensor *b)
+pg_tensor *pga_binary_fwd(int op, const pg_tensor *a, const pg_tensor *b)
 {
     if (!need_f32(a, "binary op") || !need_f32(b, "binary op"))
         return NULL;
@@ -534,7 +534,7 @@ static pg_tensor *binary_fwd(int op, const pg_tensor *a, const pg_tensor *b)
     return y;
 }
 
-static pg_tensor *unary_fwd(int op, const pg_tensor *a, float p0, float p1)
+pg_tensor *pga_unary_fwd(int op, const pg_tensor *a, float p0, float p1)
 {
     if (!need_f32(a, "unary op"))
         return NULL;
@@ -596,9 +596,9 @@ static void bwd_div(pg_node *n)
     accum_binary(pa, g, PGK_DIV, pb->value, 1.0f);
     if (pb->requires_grad) {
         /* -(g * a) / (b * b)  (autograd.c:497-509) */
-        pg_tensor *d = binary_fwd(PGK_MUL, pb->value, pb->value);
-        pg_tensor *num = d ? binary_fwd(PGK_MUL, g, pa->value) : NULL;
-        pg_tensor *t = num ? binary_fwd(PGK_DIV, num, d) : NULL;
+        pg_tensor *d = pga_binary_fwd(PGK_MUL, pb->value, pb->value);
+        pg_tensor *num = d ? pga_binary_fwd(PGK_MUL, g, pa->value) : NULL;
+        pg_tensor *t = num ? pga_binary_fwd(PGK_DIV, num, d) : NULL;
         if (t)
             accum(pb, t, -1.0f);
         pg_tensor_free(d);
@@ -691,7 +691,7 @@ void pga_backward_node(pg_node *n)
             pga_set_err(#name ": null operand");                                                                  \
             return NULL;                                                                                          \
         }                                                                                                         \
-        pg_tensor *v = binary_fwd(code, a->value, b->value);                                                      \
+        pg_tensor *v = pga_binary_fwd(code, a->value, b->value);                                                  \
         return v ? attach(v, 2, (pg_node *[]){a, b}, bwd, NULL, agop) : NULL;                                     \
     }
 
@@ -707,7 +707,7 @@ static pg_node *unary_ag(pg_node *a, int code, pg_ag_op_t op, void (*bwd)(pg_nod
         pga_set_err("unary op: null operand");
         return NULL;
     }
-    pg_tensor *v = unary_fwd(code, a->value, p0, p1);
+    pg_tensor *v = pga_unary_fwd(code, a->value, p0, p1);
     if (!v)
         return NULL;
     pga_param_ctx *cx = NULL;

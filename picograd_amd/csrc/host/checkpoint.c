@@ -226,23 +226,29 @@ bool pg_tensor_save_fp(const pg_tensor *t, FILE *fp)
         pgd_set_err("pg_tensor_save: tensor has no device storage");
         return false;
     }
-    if (!pgt_is_contiguous(t)) {
-        pgd_set_err("pg_tensor_save: strided tensors are not supported");
+    pgt_materialize((pg_tensor *)t); /* a pending zero is written as zeros */
+    /* a strided view is written in logical row-major order, as the
+     * reference's odometer loop writes it (tensor.c:628-647) */
+    pg_tensor *own;
+    const pg_tensor *src = pgt_contiguous(t, &own);
+    if (!src)
+        return false;
+    const uint32_t ver = PGT1_VERSION, dtype = (uint32_t)t->dtype, ndim = (uint32_t)t->ndim;
+    if (!put(fp, PGT1_MAGIC, 4) || !put(fp, &ver, 4) || !put(fp, &dtype, 4) || !put(fp, &ndim, 4)) {
+        pg_tensor_free(own);
         return false;
     }
-    pgt_materialize((pg_tensor *)t); /* a pending zero is written as zeros */
-    const uint32_t ver = PGT1_VERSION, dtype = (uint32_t)t->dtype, ndim = (uint32_t)t->ndim;
-    if (!put(fp, PGT1_MAGIC, 4) || !put(fp, &ver, 4) || !put(fp, &dtype, 4) || !put(fp, &ndim, 4))
-        return false;
     for (size_t i = 0; i < t->ndim; i++) {
         const uint64_t d = (uint64_t)t->shape[i];
-        if (!put(fp, &d, 8))
+        if (!put(fp, &d, 8)) {
+            pg_tensor_free(own);
             return false;
+        }
     }
     const uint64_t numel = (uint64_t)t->numel, elem = (uint64_t)t->elem_size;
-    if (!put(fp, &numel, 8) || !put(fp, &elem, 8))
-        return false;
-    return pgc_dev_to_file(t->dev, t->numel * t->elem_size, fp);
+    bool ok = put(fp, &numel, 8) && put(fp, &elem, 8) && pgc_dev_to_file(src->dev, t->numel * t->elem_size, fp);
+    pg_tensor_free(own);
+    return ok;
 }
 
 bool pg_tensor_save(const pg_tensor *t, const char *path)

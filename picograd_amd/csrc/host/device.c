@@ -118,7 +118,7 @@ typedef struct blk {
 
 #define NBINS 1024
 static blk *g_bins[NBINS];
-static size_t g_in_use, g_cached;
+static size_t g_in_use, g_cached, g_cached_blocks;
 
 static size_t size_class(size_t n)
 {
@@ -148,6 +148,7 @@ static void release_all(void)
             blk *nx = b->next;
             hipFree(b->p);
             g_cached -= b->cls;
+            g_cached_blocks--;
             free(b);
             b = nx;
         }
@@ -158,6 +159,7 @@ static void release_all(void)
 void pg_amd_release_cached(void) { release_all(); }
 size_t pg_amd_bytes_in_use(void) { return g_in_use; }
 size_t pg_amd_bytes_cached(void) { return g_cached; }
+size_t pgd_cached_blocks(void) { return g_cached_blocks; }
 
 void *pgd_malloc(size_t nbytes)
 {
@@ -171,6 +173,7 @@ void *pgd_malloc(size_t nbytes)
             *pp = b->next;
             free(b);
             g_cached -= cls;
+            g_cached_blocks--;
             g_in_use += cls;
             return p;
         }
@@ -206,6 +209,7 @@ void pgd_free(void *p, size_t nbytes)
     b->next = g_bins[bin_of(cls)];
     g_bins[bin_of(cls)] = b;
     g_cached += cls;
+    g_cached_blocks++;
 }
 
 static void *g_scratch[PGD_SCRATCH_SLOTS];

@@ -22,6 +22,7 @@
 /* ---- device layer (device.c) ---- */
 bool pgd_ok(void);                 /* init on first use; false if no device */
 bool pgd_initialised(void);        /* pg_amd_init has succeeded (never inits) */
+size_t pgd_cached_blocks(void);    /* freed blocks held by the allocator's cache */
 pgk_stream pgd_stream(void);
 void *pgd_malloc(size_t nbytes);   /* cached, stream-ordered reuse */
 void pgd_free(void *p, size_t nbytes);
@@ -60,6 +61,10 @@ void pgt_materialize(pg_tensor *t);
 const uint16_t *pgt_shadow16(pg_tensor *t, pg_dtype dt);
 /* records an in-place write of t's elements: its shadow is stale */
 void pgt_touch(pg_tensor *t);
+/* t itself when contiguous, else a new contiguous tensor holding t's
+ * elements in row-major order (*owned set to it; free with
+ * pg_tensor_free).  NULL on failure. */
+const pg_tensor *pgt_contiguous(const pg_tensor *t, pg_tensor **owned);
 
 /* ---- checkpoint I/O (checkpoint.c) ---- */
 #include <stdio.h>
@@ -101,6 +106,12 @@ void pga_backward_node(pg_node *n); /* eager device backward of one node */
  * node is a plain constant and ctx is freed at once */
 pg_node *pga_attach(pg_tensor *value, size_t np, pg_node **parents, void (*bwd)(pg_node *), void *ctx,
                     pg_ag_op_t op);
+
+/* forward of an elementwise op on f32 tensors (PGK_* codes), broadcast for
+ * binary ops; recorded as a deferred op while the JIT is on, else launched.
+ * NULL (autograd error set) on bad input. */
+pg_tensor *pga_binary_fwd(int op, const pg_tensor *a, const pg_tensor *b);
+pg_tensor *pga_unary_fwd(int op, const pg_tensor *a, float p0, float p1);
 
 typedef struct { size_t axis; bool keepdim; } pga_red_ctx;
 typedef struct { float p0, p1; } pga_param_ctx;

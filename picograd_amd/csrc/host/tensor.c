@@ -6,6 +6,7 @@
 #define _POSIX_C_SOURCE 200809L
 #include "internal.h"
 
+#include <assert.h>
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -262,6 +263,44 @@ void pgt_touch(pg_tensor *t)
 
 void pg_amd_tensor_modified(pg_tensor *t) { pgt_touch(t); }
 
+pg_tensor *pg_amd_tensor_to_dtype(const pg_tensor *t, pg_dtype dtype)
+{
+    if (!t || !pg_dtype_is_float(dtype)) {
+        pgd_set_err("pg_amd_tensor_to_dtype: null tensor or unknown dtype");
+        return NULL;
+    }
+    if (t->dtype == dtype)
+        return pg_tensor_clone(t);
+    pg_tensor *own;
+    const pg_tensor *src = pgt_contiguous(t, &own);
+    if (!src)
+        return NULL;
+    pg_tensor *y = pgt_alloc(dtype, t->ndim, t->shape);
+    bool ok = y != NULL;
+    if (ok && (t->pg_flags & PG_TENSOR_ZERO_PENDING)) {
+        ok = fill_value(y, 0.0f);
+    } else if (ok && t->dtype == PG_DTYPE_F32) {
+        ok = pgd_check(pgk_cast_to16((int)dtype, src->dev, y->dev, t->numel, pgd_stream()), "pg_amd_tensor_to_dtype");
+    } else if (ok && dtype == PG_DTYPE_F32) {
+        ok = pgd_check(pgk_cast_from16((int)t->dtype, src->dev, y->dev, t->numel, pgd_stream()),
+                       "pg_amd_tensor_to_dtype");
+    } else if (ok) {
+        /* f16 <-> bf16 through f32 (the widening is exact) */
+        float *tmp = pgd_malloc(t->numel * 4 ? t->numel * 4 : 1);
+        ok = tmp && pgd_check(pgk_cast_from16((int)t->dtype, src->dev, tmp, t->numel, pgd_stream()),
+                              "pg_amd_tensor_to_dtype") &&
+             pgd_check(pgk_cast_to16((int)dtype, tmp, y->dev, t->numel, pgd_stream()), "pg_amd_tensor_to_dtype");
+        if (tmp)
+            pgd_free(tmp, t->numel * 4);
+    }
+    pg_tensor_free(own);
+    if (!ok) {
+        pg_tensor_free(y);
+        return NULL;
+    }
+    return y;
+}
+
 bool pg_amd_tensor_refresh16(pg_tensor *t)
 {
     if (!t || !t->data_ref)
@@ -307,12 +346,28 @@ pg_tensor *pg_tensor_clone(const pg_tensor *t)
         return c;
     }
     if (!pgt_is_contiguous(t)) {
-        pgd_set_err("pg_tensor_clone: strided source not supported");
-        pg_tensor_free(c);
-        return NULL;
+        /* a strided view: its elements in row-major order */
+        if (!pgd_check(pgk_gather_strided(t->elem_size, t->dev, c->dev, (int)t->ndim, t->shape, t->stride,
+                                          pgd_stream()),
+                       "pg_tensor_clone")) {
+            pg_tensor_free(c);
+            return NULL;
+        }
+        return c;
     }
     pgd_d2d(c->dev, t->dev, t->numel * t->elem_size);
     return c;
+}
+
+const pg_tensor *pgt_contiguous(const pg_tensor *t, pg_tensor **owned)
+{
+    *owned = NULL;
+    if (!t)
+        return NULL;
+    if (pgt_is_contiguous(t))
+        return t;
+    *owned = pg_tensor_clone(t);
+    return *owned;
 }
 
 void pg_tensor_fill(pg_tensor *t, float value)
@@ -350,9 +405,45 @@ bool pg_tensor_reshape(pg_tensor *t, size_t ndim, const size_t *shape)
 
 pg_tensor *pg_tensor_view(const pg_tensor *src)
 {
-    if (!src)
+    if (!src || !src->data_ref)
         return NULL;
-    return pg_tensor_reshape_view(src, src->ndim, src->shape);
+    pg_tensor *v = calloc(1, sizeof *v);
+    if (!v)
+        return NULL;
+    v->ndim = src->ndim;
+    memcpy(v->shape, src->shape, sizeof v->shape);
+    memcpy(v->stride, src->stride, sizeof v->stride);
+    v->numel = src->numel;
+    v->dtype = src->dtype;
+    v->elem_size = src->elem_size;
+    v->data_ref = src->data_ref;
+    v->data_ref->refs++;
+    v->dev = src->dev;
+    v->is_view = true;
+    v->view_parent = (pg_tensor *)src;
+    v->pg_flags = src->pg_flags;
+    return v;
+}
+
+/* tensor.c:575-595: shape and strides permuted, storage shared */
+pg_tensor *pg_tensor_permute_view(const pg_tensor *src, const size_t *order)
+{
+    if (!src || !order)
+        return NULL;
+    bool seen[PG_MAX_NDIM] = {0};
+    for (size_t i = 0; i < src->ndim; i++) {
+        if (order[i] >= src->ndim || seen[order[i]])
+            return NULL;
+        seen[order[i]] = true;
+    }
+    pg_tensor *v = pg_tensor_view(src);
+    if (!v)
+        return NULL;
+    for (size_t i = 0; i < src->ndim; i++) {
+        v->shape[i] = src->shape[order[i]];
+        v->stride[i] = src->stride[order[i]];
+    }
+    return v;
 }
 
 pg_tensor *pg_tensor_reshape_view(const pg_tensor *src, size_t ndim, const size_t *shape)
@@ -421,3 +512,251 @@ bool pg_tensor_sync_device(pg_tensor *t)
         return false;
     return pg_tensor_copy_from_host(t, t->data_raw);
 }
+
+/* ---- host-side helpers of the reference's tensor utilities ---- */
+
+/* IEEE round-to-nearest-even f32 -> f16 (the device cast's rounding) */
+static uint16_t host_f32_to_f16(float f)
+{
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    uint32_t sign = (x >> 16) & 0x8000u, ex = (x >> 23) & 0xFFu, man = x & 0x7FFFFFu;
+    if (ex == 255)
+        return (uint16_t)(sign | 0x7C00u | (man ? 0x200u | (man >> 13) : 0u));
+    int32_t e = (int32_t)ex - 112;
+    if (e >= 31)
+        return (uint16_t)(sign | 0x7C00u);
+    if (e <= 0) {
+        if (e < -10)
+            return (uint16_t)sign;
+        man |= 0x800000u;
+        uint32_t sh = (uint32_t)(14 - e), keep = man >> sh, rem = man & ((1u << sh) - 1u), half = 1u << (sh - 1u);
+        if (rem > half || (rem == half && (keep & 1u)))
+            keep++;
+        return (uint16_t)(sign | keep);
+    }
+    uint32_t r = man + 0xFFFu + ((man >> 13) & 1u);
+    if (r & 0x800000u) {
+        r = 0;
+        e++;
+    }
+    return e >= 31 ? (uint16_t)(sign | 0x7C00u) : (uint16_t)(sign | ((uint32_t)e << 10) | (r >> 13));
+}
+
+static float host_f16_to_f32(uint16_t h)
+{
+    uint32_t sign = ((uint32_t)h & 0x8000u) << 16, ex = ((uint32_t)h >> 10) & 0x1Fu, man = (uint32_t)h & 0x3FFu;
+    uint32_t bits;
+    if (ex == 0 && man == 0) {
+        bits = sign;
+    } else if (ex == 0) {
+        int32_t e = 1;
+        while (!(man & 0x400u)) {
+            man <<= 1;
+            e--;
+        }
+        bits = sign | ((uint32_t)(e + 112) << 23) | ((man & 0x3FFu) << 13);
+    } else {
+        bits = sign | (ex == 31 ? 0x7F800000u : (ex + 112u) << 23) | (man << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+static float host_elem(const pg_tensor *t, const void *p)
+{
+    if (t->dtype == PG_DTYPE_F32) {
+        float f;
+        memcpy(&f, p, 4);
+        return f;
+    }
+    uint16_t h;
+    memcpy(&h, p, 2);
+    if (t->dtype == PG_DTYPE_F16)
+        return host_f16_to_f32(h);
+    uint32_t bits = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+/* t's elements in row-major order in a malloc'd host buffer (waits) */
+static void *host_copy(const pg_tensor *t)
+{
+    pg_tensor *own;
+    const pg_tensor *c = pgt_contiguous(t, &own);
+    if (!c)
+        return NULL;
+    size_t nb = t->numel * t->elem_size;
+    void *h = malloc(nb ? nb : 1);
+    if (h && !pg_tensor_copy_to_host(c, h)) {
+        free(h);
+        h = NULL;
+    }
+    pg_tensor_free(own);
+    return h;
+}
+
+static pg_tensor *from_host_f32(size_t n, const float *v)
+{
+    return pg_tensor_from_data(1, &n, v);
+}
+
+/* tensor.c:276-287: n = ceil((stop - start) / step) elements start + step*i */
+pg_tensor *pg_tensor_arange(float start, float stop, float step)
+{
+    if (step <= 0.0f || stop <= start)
+        return NULL;
+    size_t n = (size_t)ceilf((stop - start) / step);
+    float *v = malloc((n ? n : 1) * sizeof *v);
+    if (!v)
+        return NULL;
+    for (size_t i = 0; i < n; i++)
+        v[i] = start + step * (float)i;
+    pg_tensor *t = from_host_f32(n, v);
+    free(v);
+    return t;
+}
+
+/* tensor.c:341-357: num points, the last exactly stop */
+pg_tensor *pg_tensor_linspace(float start, float stop, size_t num)
+{
+    if (num == 0)
+        return NULL;
+    float *v = malloc(num * sizeof *v);
+    if (!v)
+        return NULL;
+    if (num == 1) {
+        v[0] = start;
+    } else {
+        float step = (stop - start) / (float)(num - 1);
+        for (size_t i = 0; i + 1 < num; i++)
+            v[i] = start + step * (float)i;
+        v[num - 1] = stop;
+    }
+    pg_tensor *t = from_host_f32(num, v);
+    free(v);
+    return t;
+}
+
+/* tensor.c:359-371 */
+pg_tensor *pg_tensor_eye(size_t n)
+{
+    if (n == 0)
+        return NULL;
+    size_t shape[2] = {n, n};
+    float *v = calloc(n * n, sizeof *v);
+    if (!v)
+        return NULL;
+    for (size_t i = 0; i < n; i++)
+        v[i * n + i] = 1.0f;
+    pg_tensor *t = pg_tensor_from_data(2, shape, v);
+    free(v);
+    return t;
+}
+
+static size_t flat_offset(const pg_tensor *t, const size_t *idx)
+{
+    size_t off = 0;
+    for (size_t i = 0; i < t->ndim; i++) {
+        assert(idx[i] < t->shape[i]);
+        off += idx[i] * t->stride[i];
+    }
+    return off;
+}
+
+/* tensor.c:390-398: one element, waiting for the queued work that writes it */
+float pg_tensor_get(const pg_tensor *t, const size_t *idx)
+{
+    assert(t && idx);
+    if (t->pg_flags & PG_TENSOR_ZERO_PENDING)
+        return 0.0f;
+    unsigned char b[4] = {0};
+    if (!pgd_d2h(b, (const char *)t->dev + flat_offset(t, idx) * t->elem_size, t->elem_size))
+        return 0.0f;
+    return host_elem(t, b);
+}
+
+/* tensor.c:400-407: one element written (rounded to nearest even for
+ * f16/bf16), queued on the stream */
+void pg_tensor_set(pg_tensor *t, const size_t *idx, float value)
+{
+    assert(t && idx);
+    pgt_materialize(t);
+    pgt_touch(t);
+    size_t off = flat_offset(t, idx) * t->elem_size;
+    if (t->dtype == PG_DTYPE_F32) {
+        pgd_h2d((char *)t->dev + off, &value, 4);
+        return;
+    }
+    uint16_t h;
+    if (t->dtype == PG_DTYPE_F16) {
+        h = host_f32_to_f16(value);
+    } else {
+        uint32_t x;
+        memcpy(&x, &value, 4);
+        h = (x & 0x7F800000u) == 0x7F800000u && (x & 0x7FFFFFu) ? (uint16_t)(0x7FC0u | ((x >> 16) & 1u))
+                                                                 : (uint16_t)((x + 0x7FFFu + ((x >> 16) & 1u)) >> 16);
+    }
+    pgd_h2d((char *)t->dev + off, &h, 2);
+}
+
+/* tensor.c:473-520: |a - b| <= atol + rtol |b| elementwise in f32, 16-bit
+ * elements widened; false for other shapes.  Waits for queued work. */
+bool pg_tensor_allclose(const pg_tensor *a, const pg_tensor *b, float rtol, float atol)
+{
+    if (!a || !b || !pg_shape_equal(a->ndim, a->shape, b->ndim, b->shape))
+        return false;
+    unsigned char *ha = host_copy(a), *hb = ha ? host_copy(b) : NULL;
+    bool ok = ha && hb;
+    for (size_t i = 0; ok && i < a->numel; i++) {
+        float av = host_elem(a, ha + i * a->elem_size), bv = host_elem(b, hb + i * b->elem_size);
+        float diff = fabsf(av - bv);
+        if (!(diff <= atol + rtol * fabsf(bv)))
+            ok = false;
+    }
+    free(ha);
+    free(hb);
+    return ok;
+}
+
+/* tensor.c:522-545, :597-602: nested brackets, %g elements, rows after the
+ * first indented by their depth */
+static void print_rec(const pg_tensor *t, const unsigned char *h, size_t dim, size_t off, FILE *out)
+{
+    fputc('[', out);
+    size_t inner = 1;
+    for (size_t d = dim + 1; d < t->ndim; d++)
+        inner *= t->shape[d];
+    for (size_t i = 0; i < t->shape[dim]; i++) {
+        if (dim + 1 == t->ndim) {
+            fprintf(out, i ? ", %g" : "%g", host_elem(t, h + (off + i) * t->elem_size));
+        } else {
+            if (i)
+                fprintf(out, ",\n%*s", (int)(dim + 1), "");
+            print_rec(t, h, dim + 1, off + i * inner, out);
+        }
+    }
+    fputc(']', out);
+}
+
+void pg_tensor_print(const pg_tensor *t, FILE *out)
+{
+    assert(t && out);
+    unsigned char *h = host_copy(t);
+    if (!h)
+        return;
+    if (t->ndim)
+        print_rec(t, h, 0, 0, out);
+    else
+        fprintf(out, "%g", host_elem(t, h));
+    fputc('\n', out);
+    free(h);
+}
+
+/* tensor.c:99-118: the reference pools freed host buffers; here the pool is
+ * the device allocator's cache of freed blocks */
+void pg_tensor_pool_clear(void) { pg_amd_release_cached(); }
+size_t pg_tensor_pool_size(void) { return pgd_cached_blocks(); }
+size_t pg_tensor_pool_bytes(void) { return pg_amd_bytes_cached(); }

@@ -621,7 +621,56 @@ __global__ void __launch_bounds__(kBlock) k_upload(upload_table tab)
     }
 }
 
+// ---------------------------------------------------------------- strided gather
+// dst[i] = src[offset of logical index i], row-major over `shape`, source
+// strides in elements (a permuted or otherwise strided view made contiguous)
+struct gather_desc {
+    int ndim;
+    int64_t shape[PGK_MAX_NDIM];
+    int64_t stride[PGK_MAX_NDIM];
+};
+
+template <typename T>
+__global__ void __launch_bounds__(kBlock) k_gather(const T *__restrict__ src, T *__restrict__ dst, size_t n,
+                                                   gather_desc d)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        size_t t = i;
+        int64_t off = 0;
+        for (int q = d.ndim - 1; q >= 0; --q) {
+            const size_t c = t % (size_t)d.shape[q];
+            t /= (size_t)d.shape[q];
+            off += (int64_t)c * d.stride[q];
+        }
+        dst[i] = src[off];
+    }
+}
+
 } // namespace
+
+extern "C" int pgk_gather_strided(size_t elem_size, const void *src, void *dst, int ndim, const size_t *shape,
+                                  const size_t *stride, pgk_stream s)
+{
+    if (ndim < 0 || ndim > PGK_MAX_NDIM || (elem_size != 2 && elem_size != 4))
+        return (int)hipErrorInvalidValue;
+    gather_desc d = {};
+    d.ndim = ndim;
+    size_t n = 1;
+    for (int q = 0; q < ndim; ++q) {
+        d.shape[q] = (int64_t)shape[q];
+        d.stride[q] = (int64_t)stride[q];
+        n *= shape[q];
+    }
+    if (!n)
+        return 0;
+    if (elem_size == 4)
+        hipLaunchKernelGGL(k_gather<uint32_t>, dim3(grid_for(n)), dim3(kBlock), 0, (hipStream_t)s,
+                           (const uint32_t *)src, (uint32_t *)dst, n, d);
+    else
+        hipLaunchKernelGGL(k_gather<uint16_t>, dim3(grid_for(n)), dim3(kBlock), 0, (hipStream_t)s,
+                           (const uint16_t *)src, (uint16_t *)dst, n, d);
+    return status();
+}
 
 extern "C" int pgk_upload_scatter(const pgk_upload *ents, int n, pgk_stream s)
 {

@@ -90,6 +90,11 @@ int pgk_sum_axis_f32(const float *x, float *y, size_t outer, size_t len, size_t 
 /* dtype casts with the reference's RNE bit rules; dtype 1 = f16, 2 = bf16 */
 int pgk_cast_to16(int dtype, const float *src, uint16_t *dst, size_t n, pgk_stream s);
 int pgk_cast_from16(int dtype, const uint16_t *src, float *dst, size_t n, pgk_stream s);
+/* dst (contiguous) = the ndim-dim strided view at src in row-major order;
+ * elem_size 2 or 4 bytes, strides in elements */
+int pgk_gather_strided(size_t elem_size, const void *src, void *dst, int ndim, const size_t *shape,
+                       const size_t *stride, pgk_stream s);
+
 /*
  * Operand staging for the MFMA GEMM (only where a dimension needs padding
  * to a multiple of 8, and for the f32 -> 16-bit cast of an upstream grad):

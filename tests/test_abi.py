@@ -160,3 +160,35 @@ def test_jit_codegen_compiles_for_gfx950_without_a_gpu(host_lib):
         L.pg_jit_graph_free(g)
     finally:
         del os.environ["PG_JIT_FORCE_COMPILE_ERROR"]
+
+
+def test_reference_style_c_caller_compiles_and_links(tmp_path):
+    """tests/c_callers/*.c, written against include/picograd the way the
+    reference's tests and examples are (C11, the reference's entry points by
+    name), compile warning-free and link against the library alone."""
+    from picograd_amd.build import C_CALLERS, LIBDIR
+    srcs = sorted(C_CALLERS.glob("*.c"))
+    assert srcs
+    for src in srcs:
+        exe = tmp_path / src.stem
+        res = subprocess.run(["gcc", "-std=c11", "-O2", "-Wall", "-Wextra", "-Werror", f"-I{ROOT / 'include'}",
+                              str(src), "-o", str(exe), f"-L{LIBDIR}", "-lpicograd_amd", "-lm",
+                              f"-Wl,-rpath,{LIBDIR}"], capture_output=True, text=True)
+        assert res.returncode == 0, res.stdout + res.stderr
+        deps = subprocess.run(["ldd", str(exe)], capture_output=True, text=True).stdout
+        assert "libpicograd_amd.so" in deps and "not found" not in deps
+
+
+def test_tensor_and_ops_abi_is_complete():
+    """The tensor utilities (core/tensor.h:52-95) and the tensor-level ops of
+    ops/elementwise.h, activations.h and matmul.h that the configs' own
+    callers use are declared and exported."""
+    every = {n for v in declared_functions().values() for n in v}
+    lib = C.CDLL(str(LIB))
+    for name in ("pg_tensor_allclose", "pg_tensor_arange", "pg_tensor_linspace", "pg_tensor_eye",
+                 "pg_tensor_get", "pg_tensor_set", "pg_tensor_print", "pg_tensor_permute_view",
+                 "pg_tensor_pool_clear", "pg_tensor_pool_size", "pg_tensor_pool_bytes",
+                 "pg_add", "pg_sub", "pg_mul", "pg_div", "pg_neg", "pg_exp", "pg_log", "pg_sqrt", "pg_sin",
+                 "pg_cos", "pg_erf", "pg_abs", "pg_clamp", "pg_relu", "pg_leaky_relu", "pg_sigmoid", "pg_tanh",
+                 "pg_gelu", "pg_matmul", "pg_bmm"):
+        assert name in every and hasattr(lib, name), name
