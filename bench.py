@@ -111,6 +111,22 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def warm(L, step, min_steps, min_seconds=0.1):
+    """Untimed warmup: at least min_steps steps and min_seconds of device
+    work.  Under sustained MFMA load the chip settles at a higher clock
+    after some tens of milliseconds than in the first few (the GEMMs run
+    ~10 % slower during the first ~20 ms), so the GEMM legs warm up by
+    time, not by a step count alone."""
+    t0, n = time.perf_counter(), 0
+    while n < min_steps or time.perf_counter() - t0 < min_seconds:
+        step()
+        n += 1
+        if n % 8 == 0:
+            L.sync()
+    L.sync()
+    return n
+
+
 def timer_ms(lib, kind):
     cnt = C.c_size_t()
     total = lib.pg_amd_timer_read(kind, C.byref(cnt))
@@ -357,9 +373,7 @@ def bench_c3(L, ev, steps, warmup, M=8192, K=4096, N=4096):
     del a16, w16, dc
     L.sync()
     step = lambda: L.pg_amd_backward_from(c, seed)
-    for _ in range(warmup):
-        step()
-    L.sync()
+    warm(L, step, warmup)
     L.pg_amd_timer_reset()
     L.pg_amd_timer_enable(1)
     ev.time(step, steps)
@@ -451,9 +465,7 @@ def bench_c4(L, ev, steps, warmup):
         L.pg_amd_backward_from(c, dc_t)
         L.pg_amd_backward_from(s, ds_t)
 
-    for _ in range(warmup):
-        step()
-    L.sync()
+    warm(L, step, warmup)
     L.pg_amd_timer_reset()
     L.pg_amd_timer_enable(1)
     ev.time(step, steps)
@@ -545,8 +557,11 @@ def bench_c5(L, ev, steps, warmup, dims=C5_DIMS, batch=C5_BATCH, fused=True):
             n -= k
         return out
 
-    ev.time_segments(segments(max(warmup, C5_CHUNK)))
-    L.sync()
+    t0 = time.perf_counter()
+    while True:  # warm up by time as well (see warm)
+        ev.time_segments(segments(max(warmup, C5_CHUNK)))
+        if time.perf_counter() - t0 >= 0.1:
+            break
     L.pg_amd_timer_reset()
     L.pg_amd_timer_enable(1)
     ev.time_segments(segments(steps))

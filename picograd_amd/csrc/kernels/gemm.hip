@@ -18,9 +18,9 @@
 //    4 (k & 3) and reach it with ds_read_b64_tr_b16, the gfx950 transposing
 //    LDS read (within each 16-lane group, lane i of the result takes element
 //    i % 4 of the 8 bytes lane 4p + i / 4 addressed, for slot p);
-//  - fragment reads for the next 16-wide k step are issued before the MFMAs
-//    of the current one, and the k-loop has no branches between two
-//    barriers, so each MFMA waits only for its own fragments;
+//  - fragment reads for the next 16-wide k step are issued one per MFMA of
+//    the current one, and the k-loop has no branches between two barriers,
+//    so each MFMA waits only for its own fragments;
 //  - tiles are remapped so the blocks that share operand panels run on one
 //    XCD (and its L2), grouped 8 tile-rows at a time.
 // A partial last k-tile loads zeros past K: its out-of-range chunks (K % 8
@@ -317,8 +317,8 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1)
     // exact: at a control-flow merge it falls back to waiting for every
     // outstanding LDS read, which would stall each wave on the fragment
     // reads it has just issued for the next k-step.
-    //  - k-step s of a tile reads the fragments of step s + 1, then runs
-    //    its MFMAs on those read one step earlier;
+    //  - k-step s of a tile runs its MFMAs on the fragments read one step
+    //    earlier and reads those of step s + 1 between them;
     //  - a tile's last k-step ("tail") starts with the one barrier per tile:
     //    every wave has then read the whole stage (its last fragments are in
     //    registers), so the stage is refilled with tile t + S during that
@@ -381,9 +381,15 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1)
     };
     // MFMAs of k-step s; in a tail, tile `reload` goes into stage (dA, dB),
     // a few loads per MFMA rather than one burst at the vector-memory queue,
-    // in the fast form when FAST (a compile-time tag)
-    auto mfmas = [&](int s, bool tail, int reload, LDS uint4 *dA, LDS uint4 *dB, auto fast) {
-        // keep this step's fragment reads (issued just before) ahead of its
+    // in the fast form when FAST (a compile-time tag).  With `next`, the
+    // fragments of k-step ns of the tile in stage (nA, nB) are read into the
+    // other fragment buffer one per MFMA, so the LDS reads spread over the
+    // step instead of arriving in one burst ahead of it (wgrad's
+    // transposing reads, two per fragment, gain the most).  `next` is a
+    // flag rather than a null test of nA: LDS address 0 is a valid stage.
+    auto mfmas = [&](int s, bool tail, int reload, LDS uint4 *dA, LDS uint4 *dB, auto fast, bool next,
+                     const LDS uint4 *nA, const LDS uint4 *nB, int ns) {
+        // keep the reads and loads placed here in their slots between the
         // MFMAs: left alone, the scheduler sinks each read to just before
         // its first use and the LDS latency shows at every step
         __builtin_amdgcn_sched_barrier(0);
@@ -392,6 +398,15 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1)
 #pragma unroll
             for (int j = 0; j < FN; ++j) {
                 acc[i][j] = mfma32<F16>(fa[s & 1][i], fb[s & 1][j], acc[i][j]);
+                if (next) {
+                    const int g = i * FN + j;
+                    static_assert(FM * FN >= FM + FN, "one fragment read per MFMA at most");
+                    if (g < FM)
+                        fa[(s + 1) & 1][g] = OA::frag(nA, wm * WM + g * 32, ns, lane);
+                    else if (g < FM + FN)
+                        fb[(s + 1) & 1][g - FM] = OB::frag(nB, wn * WN + (g - FM) * 32, ns, lane);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
                 if (tail) {
                     const int g = i * FN + j;
 #pragma unroll
@@ -410,17 +425,14 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1)
     // are in fa[0], fb[0]
     auto head = [&](const LDS uint4 *cA, const LDS uint4 *cB) {
 #pragma unroll
-        for (int s = 0; s < KS - 1; ++s) {
-            rd(cA, cB, s + 1, fa[(s + 1) & 1], fb[(s + 1) & 1]);
-            mfmas(s, false, 0, nullptr, nullptr, std::false_type{});
-        }
+        for (int s = 0; s < KS - 1; ++s)
+            mfmas(s, false, 0, nullptr, nullptr, std::false_type{}, true, cA, cB, s + 1);
     };
     // the tail of tile t (stage cA, cB) and the head of tile t + 1 (oA, oB)
     auto link = [&](int t, LDS uint4 *cA, LDS uint4 *cB, LDS uint4 *oA, LDS uint4 *oB, auto fast) {
         // tile t + 1 landed; tiles t + 2 .. t + S - 1 may be in flight
         sync_tile(std::integral_constant<int, S - 2>{});
-        rd(oA, oB, 0, fa[0], fb[0]);
-        mfmas(KS - 1, true, t + S, cA, cB, fast);
+        mfmas(KS - 1, true, t + S, cA, cB, fast, true, oA, oB, 0);
         head(oA, oB);
     };
 #pragma unroll
@@ -449,7 +461,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1)
             if (t + u < links)
                 link(t + u, stA(u), stB(u), stA((u + 1) % S), stB((u + 1) % S), std::false_type{});
     }
-    mfmas(KS - 1, false, 0, nullptr, nullptr, std::false_type{}); // the last tile's tail
+    mfmas(KS - 1, false, 0, nullptr, nullptr, std::false_type{}, false, nullptr, nullptr, 0); // the last tail
     // the loads of the tiles past the end land before the LDS is reused
     // (the epilogue's staging, or the next block on this CU)
     __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0_imm(0));
