@@ -88,6 +88,39 @@ static bool flush_pending(void)
     return ok;
 }
 
+/* A second stream for work that runs beside the main stream's: pgd_fork
+ * orders it after everything queued so far, pgd_join orders everything
+ * queued later on the main stream after it.  Default priority, as the
+ * main stream.  Buffers the side work uses must be allocated before the
+ * fork and freed after the join (the allocator's reuse is ordered on the
+ * main stream). */
+static hipStream_t g_side;
+static hipEvent_t g_fork_ev, g_join_ev;
+
+pgk_stream pgd_fork(void)
+{
+    pgk_stream main_s = pgd_stream(); /* flushes pending work first */
+    if (!pgd_ok())
+        return NULL;
+    if (!g_side) {
+        if (!hip_ok(hipStreamCreateWithFlags(&g_side, hipStreamNonBlocking), "hipStreamCreate (side)") ||
+            !hip_ok(hipEventCreateWithFlags(&g_fork_ev, hipEventDisableTiming), "hipEventCreate") ||
+            !hip_ok(hipEventCreateWithFlags(&g_join_ev, hipEventDisableTiming), "hipEventCreate")) {
+            return NULL;
+        }
+    }
+    if (!hip_ok(hipEventRecord(g_fork_ev, (hipStream_t)main_s), "hipEventRecord") ||
+        !hip_ok(hipStreamWaitEvent(g_side, g_fork_ev, 0), "hipStreamWaitEvent"))
+        return NULL;
+    return (pgk_stream)g_side;
+}
+
+bool pgd_join(void)
+{
+    return hip_ok(hipEventRecord(g_join_ev, g_side), "hipEventRecord") &&
+           hip_ok(hipStreamWaitEvent(g_stream, g_join_ev, 0), "hipStreamWaitEvent");
+}
+
 pgk_stream pgd_stream(void)
 {
     /* everything queued from here on is ordered after the pending work */

@@ -84,24 +84,44 @@ static bool mm_shapes(const pg_tensor *a, const pg_tensor *b, mm_shape *s, size_
 
 static void *tmp_alloc(size_t nbytes) { return pgd_malloc(nbytes ? nbytes : 1); }
 
-/* one MFMA GEMM (pgk_gemm16 semantics, optional epilogue), bracketed by the
- * kernel timer; the split-K partials and k-tail slabs come from the library
- * scratch (stream-ordered, so consecutive GEMMs may share it) */
+/* Where a GEMM runs: the main stream with the whole chip, or one of two
+ * concurrent launches (main or side stream) with a CU budget and its own
+ * scratch slot */
+typedef struct {
+    pgk_stream st; /* NULL: the main stream */
+    int slot;      /* scratch slot of its split-K partials / k-tail slabs */
+    int cus;       /* CU budget, 0 = all */
+    bool timed;    /* bracket it with the kernel timer */
+} gemm_place;
+
+static const gemm_place PLACE_MAIN = {NULL, 1, 0, true};
+
+/* one MFMA GEMM (pgk_gemm16 semantics, optional epilogue); the split-K
+ * partials and k-tail slabs come from the library scratch (stream-ordered,
+ * so consecutive GEMMs on one stream may share a slot) */
+static bool gemm16p(const gemm_place *pl, int dt, int ta, int tb, size_t m, size_t n, size_t k, const uint16_t *a,
+                    size_t lda, size_t sa, size_t aext, const uint16_t *b, size_t ldb, size_t sb, size_t bext,
+                    float *c, size_t ldc, size_t sc, size_t batch, int beta, const pgk_epi *epi, const char *what)
+{
+    size_t wsz = pgk_gemm16_workspace_cu(ta, tb, m, n, k, batch, pl->cus);
+    void *ws = NULL;
+    if (wsz && !(ws = pgd_scratch(pl->slot, wsz))) {
+        pgd_set_err("%s: workspace allocation failed", what);
+        return false;
+    }
+    int tk = pl->timed ? pgd_tbegin(PGD_T_GEMM16) : -1;
+    int rc = pgk_gemm16_cu(dt, ta, tb, m, n, k, a, lda, sa, aext, b, ldb, sb, bext, c, ldc, sc, batch, beta, epi, ws,
+                           pl->cus, pl->st ? pl->st : pgd_stream());
+    pgd_tend(tk);
+    return pgd_check(rc, what);
+}
+
 static bool gemm16x(int dt, int ta, int tb, size_t m, size_t n, size_t k, const uint16_t *a, size_t lda, size_t sa,
                     size_t aext, const uint16_t *b, size_t ldb, size_t sb, size_t bext, float *c, size_t ldc,
                     size_t sc, size_t batch, int beta, const pgk_epi *epi, const char *what)
 {
-    size_t wsz = pgk_gemm16_workspace(ta, tb, m, n, k, batch);
-    void *ws = NULL;
-    if (wsz && !(ws = pgd_scratch(1, wsz))) {
-        pgd_set_err("%s: workspace allocation failed", what);
-        return false;
-    }
-    int tk = pgd_tbegin(PGD_T_GEMM16);
-    int rc = pgk_gemm16(dt, ta, tb, m, n, k, a, lda, sa, aext, b, ldb, sb, bext, c, ldc, sc, batch, beta, epi, ws,
-                        pgd_stream());
-    pgd_tend(tk);
-    return pgd_check(rc, what);
+    return gemm16p(&PLACE_MAIN, dt, ta, tb, m, n, k, a, lda, sa, aext, b, ldb, sb, bext, c, ldc, sc, batch, beta, epi,
+                   what);
 }
 
 static bool gemm16(int dt, int ta, int tb, size_t m, size_t n, size_t k, const uint16_t *a, size_t lda, size_t sa,
@@ -273,54 +293,85 @@ void pgm_matmul_backward(pg_node *n)
     uint16_t *g16 = stage16(dt, 0, g->dev, B * M, N, N, B * M, N8, 1, 0, &gbytes);
     if (!g16)
         return;
-    if (ga) {
-        /* dA[M, K] (+)= dC[M, N] . W[K, N]^T: both operands contiguous along
-         * the reduction (N); W padded to N8 zero columns when needed */
-        const uint16_t *wp = b->dev;
-        uint16_t *wpad = NULL;
-        size_t wbytes = 0, wb = s.bbat ? B : 1;
-        if (N8 != N)
-            wp = wpad = stage16(dt, dt, b->dev, K, N, N, K, N8, wb, K * N, &wbytes);
-        if (wp) {
-            if (s.abat || B == 1) {
-                gemm16(dt, 0, 0, M, K, N8, g16, N8, M * N8, M, wp, N8, s.bbat ? K * N8 : 0, K, ga->dev, K, M * K, B,
-                       ba, "dgrad");
-            } else {
-                /* unbatched A, batched B: dA accumulates over the batch */
-                for (size_t z = 0; z < B; z++)
-                    gemm16(dt, 0, 0, M, K, N8, g16 + z * M * N8, N8, 0, M, wp + z * K * N8, N8, 0, K, ga->dev, K, 0,
-                           1, z == 0 ? ba : 1, "dgrad");
+    /* dgrad operands: dA[M, K] (+)= dC[M, N] . W[K, N]^T, both contiguous
+     * along the reduction (N); W padded to N8 zero columns when needed */
+    const uint16_t *wp = b->dev;
+    uint16_t *wpad = NULL;
+    size_t wbytes = 0, wb = s.bbat ? B : 1;
+    if (ga && N8 != N)
+        wp = wpad = stage16(dt, dt, b->dev, K, N, N, K, N8, wb, K * N, &wbytes);
+    /* wgrad operands: dW[K, N] (+)= A[M, K]^T . dC[M, N], reduction over M
+     * with K and N contiguous; A padded to K8 zero columns when needed.
+     * When only A is batched the batch folds into the reduction (M_eff =
+     * B M) */
+    bool fold = s.abat && !s.bbat;
+    size_t Bw = fold ? 1 : B, Mw = fold ? B * M : M;
+    size_t a_rows = s.abat ? B * M : M;
+    const uint16_t *ap = a->dev;
+    uint16_t *apad = NULL;
+    size_t abytes = 0;
+    if (gb && K8 != K)
+        ap = apad = stage16(dt, dt, a->dev, a_rows, K, K, a_rows, K8, 1, 0, &abytes);
+    size_t lda_w = K8 != K ? K8 : K, sa_w = (s.abat && !fold) ? M * K8 : 0;
+    bool d_one = ga && wp && (s.abat || B == 1), w_one = gb && ap && (s.bbat || Bw == 1);
+
+    /* When each GEMM alone would leave CUs idle (the bmm grads of config 4:
+     * 128 blocks each), run the two side by side, each planned for its share
+     * of the chip: wgrad on the side stream, dgrad on the main one.  The
+     * planner's time estimates pick the split; without a clear win the two
+     * run one after the other on the whole chip. */
+    gemm_place pd = PLACE_MAIN, pw = PLACE_MAIN;
+    int tk = -1;
+    if (d_one && w_one) {
+        double td = pgk_gemm16_time(0, 0, M, K, N8, B, 0), tw = pgk_gemm16_time(1, 1, K, N, Mw, Bw, 0);
+        double best = 0.85 * (td + tw);
+        int best_cus = 0;
+        for (int cd = 32; cd <= 224; cd += 32) {
+            double a1 = pgk_gemm16_time(0, 0, M, K, N8, B, cd), a2 = pgk_gemm16_time(1, 1, K, N, Mw, Bw, 256 - cd);
+            double t = a1 > a2 ? a1 : a2;
+            if (t < best) {
+                best = t;
+                best_cus = cd;
             }
         }
-        if (wpad)
-            pgd_free(wpad, wbytes);
-    }
-    if (gb) {
-        /* dW[K, N] (+)= A[M, K]^T . dC[M, N]: reduction over M with K and N
-         * contiguous; A padded to K8 zero columns when needed.  When only
-         * A is batched the batch folds into the reduction (M_eff = B M) */
-        bool fold = s.abat && !s.bbat;
-        size_t Bw = fold ? 1 : B, Mw = fold ? B * M : M;
-        size_t a_rows = s.abat ? B * M : M;
-        const uint16_t *ap = a->dev;
-        uint16_t *apad = NULL;
-        size_t abytes = 0;
-        if (K8 != K)
-            ap = apad = stage16(dt, dt, a->dev, a_rows, K, K, a_rows, K8, 1, 0, &abytes);
-        if (ap) {
-            size_t sa = (s.abat && !fold) ? M * K8 : 0;
-            if (s.bbat || Bw == 1) {
-                gemm16(dt, 1, 1, K, N, Mw, ap, K8 != K ? K8 : K, sa, K8 != K ? K8 : K, g16, N8, Mw * N8, N8, gb->dev,
-                       N, s.bbat ? K * N : 0, Bw, bbeta, "wgrad");
-            } else {
-                for (size_t z = 0; z < Bw; z++)
-                    gemm16(dt, 1, 1, K, N, Mw, ap + z * sa, K8 != K ? K8 : K, 0, K8 != K ? K8 : K, g16 + z * Mw * N8,
-                           N8, 0, N8, gb->dev, N, 0, 1, z == 0 ? bbeta : 1, "wgrad");
+        if (best_cus) {
+            tk = pgd_tbegin(PGD_T_GEMM16); /* the pair is one interval */
+            pd.timed = pw.timed = false;
+            pgk_stream side = pgd_fork();
+            if (side) {
+                pd.cus = best_cus;
+                pw = (gemm_place){side, 5, 256 - best_cus, false};
             }
         }
-        if (apad)
-            pgd_free(apad, abytes);
     }
+    if (gb && ap) {
+        if (w_one) {
+            gemm16p(&pw, dt, 1, 1, K, N, Mw, ap, lda_w, sa_w, lda_w, g16, N8, Mw * N8, N8, gb->dev, N,
+                    s.bbat ? K * N : 0, Bw, bbeta, NULL, "wgrad");
+        } else {
+            for (size_t z = 0; z < Bw; z++)
+                gemm16(dt, 1, 1, K, N, Mw, ap + z * sa_w, lda_w, 0, lda_w, g16 + z * Mw * N8, N8, 0, N8, gb->dev, N,
+                       0, 1, z == 0 ? bbeta : 1, "wgrad");
+        }
+    }
+    if (ga && wp) {
+        if (d_one) {
+            gemm16p(&pd, dt, 0, 0, M, K, N8, g16, N8, M * N8, M, wp, N8, s.bbat ? K * N8 : 0, K, ga->dev, K, M * K, B,
+                    ba, NULL, "dgrad");
+        } else {
+            /* unbatched A, batched B: dA accumulates over the batch */
+            for (size_t z = 0; z < B; z++)
+                gemm16(dt, 0, 0, M, K, N8, g16 + z * M * N8, N8, 0, M, wp + z * K * N8, N8, 0, K, ga->dev, K, 0, 1,
+                       z == 0 ? ba : 1, "dgrad");
+        }
+    }
+    if (pw.st)
+        pgd_join();
+    pgd_tend(tk);
+    if (wpad)
+        pgd_free(wpad, wbytes);
+    if (apad)
+        pgd_free(apad, abytes);
     pgd_free(g16, gbytes);
 }
 

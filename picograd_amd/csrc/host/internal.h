@@ -24,6 +24,11 @@ bool pgd_ok(void);                 /* init on first use; false if no device */
 bool pgd_initialised(void);        /* pg_amd_init has succeeded (never inits) */
 size_t pgd_cached_blocks(void);    /* freed blocks held by the allocator's cache */
 pgk_stream pgd_stream(void);
+/* side stream: work launched on pgd_fork()'s stream runs after everything
+ * queued before the fork and before everything queued after pgd_join();
+ * NULL / false on a device error */
+pgk_stream pgd_fork(void);
+bool pgd_join(void);
 void *pgd_malloc(size_t nbytes);   /* cached, stream-ordered reuse */
 void pgd_free(void *p, size_t nbytes);
 bool pgd_h2d(void *dst, const void *src, size_t nbytes);  /* enqueued */
@@ -36,7 +41,7 @@ bool pgd_check(int status, const char *what);
 /* a scratch device buffer of at least nbytes, reused across calls on the
  * stream (grows, never shrinks) */
 void *pgd_scratch(int slot, size_t nbytes);
-#define PGD_SCRATCH_SLOTS 5
+#define PGD_SCRATCH_SLOTS 6 /* slot 5: a GEMM on the side stream */
 /* kernel timer (pg_amd_timer_*): kinds and bracket calls */
 enum {
     PGD_T_JIT_MAIN = 0, PGD_T_JIT_FIN = 1, PGD_T_GEMM16 = 2, PGD_T_SGD = 3, PGD_T_STAGE = 4,

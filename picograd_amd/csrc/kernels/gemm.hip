@@ -852,9 +852,14 @@ typedef struct {
     int sp;   // split-K factor, 1 = none
 } gemm_plan;
 
-static gemm_plan plan_gemm(size_t m, size_t n, size_t kin, size_t batch)
+// `cu_budget` is the number of CUs the launch may occupy (another launch
+// runs beside it on the rest), 0 for the whole chip.
+static constexpr int kCUs = 256;
+
+static gemm_plan plan_gemm(size_t m, size_t n, size_t kin, size_t batch, int cu_budget = 0, double *time = nullptr)
 {
-    const double cus = 256.0, rate[3] = {0.0, 2.6e12, 4.4e12}, bw = 5.0e12;
+    const double cus = cu_budget > 0 && cu_budget < kCUs ? (double)cu_budget : (double)kCUs;
+    const double rate[3] = {0.0, 2.6e12, 4.4e12}, bw = 5.0e12;
     gemm_plan best = {2, 1};
     double best_t = 1e300;
     for (int tile = 2; tile >= 1; --tile) {
@@ -877,6 +882,8 @@ static gemm_plan plan_gemm(size_t m, size_t n, size_t kin, size_t batch)
             }
         }
     }
+    if (time)
+        *time = best_t;
     return best;
 }
 
@@ -896,17 +903,38 @@ static size_t tail_ws(int ta, int tb, size_t m, size_t n, size_t k, size_t batch
     return (a + 64 + b) * sizeof(uint16_t);
 }
 
-extern "C" size_t pgk_gemm16_workspace(int ta, int tb, size_t m, size_t n, size_t k, size_t batch)
+extern "C" size_t pgk_gemm16_workspace_cu(int ta, int tb, size_t m, size_t n, size_t k, size_t batch, int cu_budget)
 {
-    const gemm_plan pl = plan_gemm(m, n, k_inkernel(ta, tb, k), batch);
+    const gemm_plan pl = plan_gemm(m, n, k_inkernel(ta, tb, k), batch, cu_budget);
     const size_t part = pl.sp > 1 ? (((size_t)pl.sp * m * n * sizeof(float) + 255) & ~(size_t)255) : 0;
     return part + tail_ws(ta, tb, m, n, k, batch);
+}
+
+extern "C" size_t pgk_gemm16_workspace(int ta, int tb, size_t m, size_t n, size_t k, size_t batch)
+{
+    return pgk_gemm16_workspace_cu(ta, tb, m, n, k, batch, 0);
+}
+
+extern "C" double pgk_gemm16_time(int ta, int tb, size_t m, size_t n, size_t k, size_t batch, int cu_budget)
+{
+    double t = 0.0;
+    plan_gemm(m, n, k_inkernel(ta, tb, k), batch, cu_budget, &t);
+    return t;
 }
 
 extern "C" int pgk_gemm16(int dtype, int ta, int tb, size_t m, size_t n, size_t k, const uint16_t *a, size_t lda,
                           size_t stride_a, size_t a_extent, const uint16_t *b, size_t ldb, size_t stride_b,
                           size_t b_extent, float *c, size_t ldc, size_t stride_c, size_t batch, int beta,
                           const pgk_epi *epi, void *ws, pgk_stream s)
+{
+    return pgk_gemm16_cu(dtype, ta, tb, m, n, k, a, lda, stride_a, a_extent, b, ldb, stride_b, b_extent, c, ldc,
+                         stride_c, batch, beta, epi, ws, 0, s);
+}
+
+extern "C" int pgk_gemm16_cu(int dtype, int ta, int tb, size_t m, size_t n, size_t k, const uint16_t *a, size_t lda,
+                             size_t stride_a, size_t a_extent, const uint16_t *b, size_t ldb, size_t stride_b,
+                             size_t b_extent, float *c, size_t ldc, size_t stride_c, size_t batch, int beta,
+                             const pgk_epi *epi, void *ws, int cu_budget, pgk_stream s)
 {
     if (!m || !n || !batch)
         return 0;
@@ -937,7 +965,7 @@ extern "C" int pgk_gemm16(int dtype, int ta, int tb, size_t m, size_t n, size_t 
             hipLaunchKernelGGL(k_bias_act, dim3(gmn), dim3(256), 0, st, c, ldc, (int)m, (int)n, *epi);
         return (int)hipGetLastError();
     }
-    const gemm_plan pl = plan_gemm(m, n, kmain, batch);
+    const gemm_plan pl = plan_gemm(m, n, kmain, batch, cu_budget);
     const int sp = pl.sp > 1 ? pl.sp : 0;
     // the epilogue rides on the GEMM when one launch of the forward layout
     // finishes C; otherwise it is a pass over C afterwards

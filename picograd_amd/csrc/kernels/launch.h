@@ -138,6 +138,15 @@ int pgk_gemm16(int dtype, int ta, int tb, size_t m, size_t n, size_t k, const ui
                size_t stride_a, size_t a_extent, const uint16_t *b, size_t ldb, size_t stride_b, size_t b_extent,
                float *c, size_t ldc, size_t stride_c, size_t batch, int beta, const pgk_epi *epi, void *ws,
                pgk_stream s);
+/* The same GEMM planned for `cu_budget` CUs (0: the whole chip), for a
+ * launch that runs beside another on the rest of the chip; its workspace
+ * size, and the planner's estimate of its time in seconds. */
+int pgk_gemm16_cu(int dtype, int ta, int tb, size_t m, size_t n, size_t k, const uint16_t *a, size_t lda,
+                  size_t stride_a, size_t a_extent, const uint16_t *b, size_t ldb, size_t stride_b, size_t b_extent,
+                  float *c, size_t ldc, size_t stride_c, size_t batch, int beta, const pgk_epi *epi, void *ws,
+                  int cu_budget, pgk_stream s);
+size_t pgk_gemm16_workspace_cu(int ta, int tb, size_t m, size_t n, size_t k, size_t batch, int cu_budget);
+double pgk_gemm16_time(int ta, int tb, size_t m, size_t n, size_t k, size_t batch, int cu_budget);
 
 /* MFMA rate probe: `blocks` x 512 threads, each wave 8 x iters bf16
  * 32x32x16 MFMAs, operands from registers (lds 0) or LDS (lds 1); sink
