@@ -1,64 +1,54 @@
-// f32 <-> f16/bf16 conversions on the raw bits, shared by the gfx950
-// kernels (device code only).  f32 -> 16-bit rounds to nearest even as the
-// reference's convert.h:15-104 does: bf16 = (x + 0x7FFF + lsb) >> 16 with
-// NaN -> quiet NaN; f16 per IEEE 754 including subnormals (where the
-// reference's f16 encoder rounds some subnormals differently, this one
-// keeps the IEEE result).
+// f32 <-> f16/bf16 conversions shared by the gfx950 kernels (device code
+// only).  f32 -> 16-bit rounds to nearest even as the reference's
+// convert.h:15-104 does: bf16 = (x + 0x7FFF + lsb) >> 16 with NaN -> quiet
+// NaN; f16 per IEEE 754 including subnormals (where the reference's f16
+// encoder rounds some subnormals differently, this one keeps the IEEE
+// result).  The encoders are gfx950's hardware converts with the NaN rule
+// applied on top; the decoders work on the raw bits.
 #ifndef PGK_CONVERT16_H
 #define PGK_CONVERT16_H
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-// f32 -> bf16: round to nearest even on the raw bits; a NaN becomes the
-// positive quiet NaN 0x7FC0 | bit 16 (the reference's convert.h rule).
+// f32 -> bf16 by the hardware convert (v_cvt_pk_bf16_f32): round to nearest
+// even, f32 subnormals kept (the kernels run in the default FP mode, which
+// does not flush them), so every non-NaN input gets the integer rule's
+// (x + 0x7FFF + lsb) >> 16.  A NaN becomes the positive quiet NaN
+// 0x7FC0 | bit 16 (the reference's convert.h rule), not the instruction's.
+__device__ __forceinline__ uint16_t bf16_nan(float f) { return (uint16_t)(0x7FC0u | ((__float_as_uint(f) >> 16) & 1u)); }
+
 __device__ __forceinline__ uint16_t f32_to_bf16(float f)
 {
-    uint32_t x = __float_as_uint(f);
-    if ((x & 0x7F800000u) == 0x7F800000u && (x & 0x7FFFFFu) != 0)
-        return (uint16_t)(0x7FC0u | ((x >> 16) & 1u));
-    return (uint16_t)((x + 0x7FFFu + ((x >> 16) & 1u)) >> 16);
+    const uint16_t h = __builtin_bit_cast(uint16_t, (__bf16)f);
+    return f != f ? bf16_nan(f) : h;
 }
 
-// f32 -> f16, IEEE round to nearest even including subnormals; NaN keeps
-// its top payload bits and is quieted.
+// two at once, a in the low half: one v_cvt_pk_bf16_f32
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2(float a, float b)
+{
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 h2 __attribute__((ext_vector_type(2)));
+    const f2 v = {a, b};
+    uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, h2));
+    h = a != a ? (h & 0xFFFF0000u) | bf16_nan(a) : h;
+    h = b != b ? (h & 0xFFFFu) | ((uint32_t)bf16_nan(b) << 16) : h;
+    return h;
+}
+
+// f32 -> f16 by the hardware convert (v_cvt_f16_f32): IEEE round to nearest
+// even including f16 subnormals and overflow to infinity.  A NaN keeps its
+// top 10 payload bits and is quieted, with payload 1 when those are all zero
+// (the reference's convert.h:22-28 rule: sign | 0x7C00 | man >> 13, | 1 when
+// that leaves no payload, | 0x200).
 __device__ __forceinline__ uint16_t f32_to_f16(float f)
 {
-    uint32_t x = __float_as_uint(f);
-    uint32_t sign = (x >> 16) & 0x8000u;
-    uint32_t ex = (x >> 23) & 0xFFu;
-    uint32_t man = x & 0x7FFFFFu;
-    if (ex == 255) {
-        if (man == 0)
-            return (uint16_t)(sign | 0x7C00u);
-        uint32_t q = sign | 0x7C00u | (man >> 13);
-        if ((q & 0x3FFu) == 0)
-            q |= 1u;
-        return (uint16_t)(q | 0x200u);
+    const uint16_t h = __builtin_bit_cast(uint16_t, (_Float16)f);
+    if (f != f) {
+        const uint32_t x = __float_as_uint(f), m = (x & 0x7FFFFFu) >> 13;
+        return (uint16_t)(((x >> 16) & 0x8000u) | 0x7E00u | m | (m == 0 ? 1u : 0u));
     }
-    int e = (int)ex - 112;
-    if (e >= 31)
-        return (uint16_t)(sign | 0x7C00u);
-    if (e <= 0) {
-        if (e < -10)
-            return (uint16_t)sign;
-        man |= 0x800000u;
-        uint32_t sh = (uint32_t)(1 - e) + 13u;
-        uint32_t keep = man >> sh;
-        uint32_t rem = man & ((1u << sh) - 1u);
-        uint32_t half = 1u << (sh - 1u);
-        if (rem > half || (rem == half && (keep & 1u)))
-            keep++;
-        return (uint16_t)(sign | keep);
-    }
-    uint32_t r = man + 0xFFFu + ((man >> 13) & 1u);
-    if (r & 0x800000u) {
-        r = 0;
-        e++;
-    }
-    if (e >= 31)
-        return (uint16_t)(sign | 0x7C00u);
-    return (uint16_t)(sign | ((uint32_t)e << 10) | (r >> 13));
+    return h;
 }
 
 // f16 -> f32 on the raw bits (exact; NaN payloads kept as they are)
@@ -88,6 +78,12 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_floa
 __device__ __forceinline__ uint16_t to16(int dtype, float f)
 {
     return dtype == 1 ? f32_to_f16(f) : f32_to_bf16(f);
+}
+
+// a and b as two 16-bit values of one word, a in the low half
+__device__ __forceinline__ uint32_t to16x2(int dtype, float a, float b)
+{
+    return dtype == 1 ? (uint32_t)f32_to_f16(a) | ((uint32_t)f32_to_f16(b) << 16) : f32x2_to_bf16x2(a, b);
 }
 
 __device__ __forceinline__ float from16(int dtype, uint16_t h)

@@ -8,6 +8,7 @@
 
 #include "launch.h"
 #include "convert16.h"
+#include "segtab.h"
 #include "pgmath.h"
 
 namespace {
@@ -351,10 +352,10 @@ __global__ void __launch_bounds__(kBlock) k_cast_to16(const float *__restrict__ 
         const float4 v0 = reinterpret_cast<const float4 *>(src)[2 * j];
         const float4 v1 = reinterpret_cast<const float4 *>(src)[2 * j + 1];
         uint4 o;
-        o.x = (uint32_t)to16(DT, v0.x) | ((uint32_t)to16(DT, v0.y) << 16);
-        o.y = (uint32_t)to16(DT, v0.z) | ((uint32_t)to16(DT, v0.w) << 16);
-        o.z = (uint32_t)to16(DT, v1.x) | ((uint32_t)to16(DT, v1.y) << 16);
-        o.w = (uint32_t)to16(DT, v1.z) | ((uint32_t)to16(DT, v1.w) << 16);
+        o.x = to16x2(DT, v0.x, v0.y);
+        o.y = to16x2(DT, v0.z, v0.w);
+        o.z = to16x2(DT, v1.x, v1.y);
+        o.w = to16x2(DT, v1.z, v1.w);
         reinterpret_cast<uint4 *>(dst)[j] = o;
     }
     for (size_t j = n8 * 8 + i; j < n; j += stride)
@@ -428,60 +429,73 @@ __device__ __forceinline__ void sgd_elem(float &p, float g, float &b, bool has_b
     p = p - lr * u;
 }
 
+// One block's chunk on the vector path.  FULL (the whole chunk in range)
+// and HAS_BUF are compile-time, so every load of the chunk is issued before
+// the first use: under a per-vector bound or buffer test the compiler
+// issues and waits for each group of loads in turn.
+template <bool FULL, bool HAS_BUF>
+__device__ __forceinline__ void sgd_vec(const pgk_sgd_seg &sg, size_t base, size_t n, float lr, float mu, float damp,
+                                        float wd, int nesterov)
+{
+    float4 p[kSgdVec], g[kSgdVec], b[kSgdVec];
+    size_t e[kSgdVec];
+#pragma unroll
+    for (int k = 0; k < kSgdVec; ++k) {
+        e[k] = base + 4 * ((size_t)threadIdx.x + (size_t)k * kBlock);
+        if (FULL || e[k] + 4 <= n) {
+            p[k] = reinterpret_cast<const float4 *>(sg.p + e[k])[0];
+            g[k] = reinterpret_cast<const float4 *>(sg.g + e[k])[0];
+            b[k] = HAS_BUF ? reinterpret_cast<const float4 *>(sg.buf + e[k])[0] : make_float4(0, 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kSgdVec; ++k) {
+        if (FULL || e[k] + 4 <= n) {
+            sgd_elem(p[k].x, g[k].x, b[k].x, HAS_BUF, lr, mu, damp, wd, nesterov);
+            sgd_elem(p[k].y, g[k].y, b[k].y, HAS_BUF, lr, mu, damp, wd, nesterov);
+            sgd_elem(p[k].z, g[k].z, b[k].z, HAS_BUF, lr, mu, damp, wd, nesterov);
+            sgd_elem(p[k].w, g[k].w, b[k].w, HAS_BUF, lr, mu, damp, wd, nesterov);
+            reinterpret_cast<float4 *>(sg.p + e[k])[0] = p[k];
+            if (HAS_BUF)
+                reinterpret_cast<float4 *>(sg.buf + e[k])[0] = b[k];
+            if (sg.shadow) {
+                reinterpret_cast<uint2 *>(sg.shadow + e[k])[0] =
+                    make_uint2(to16x2(sg.shadow_dtype, p[k].x, p[k].y), to16x2(sg.shadow_dtype, p[k].z, p[k].w));
+            }
+        } else {
+            for (size_t j = e[k]; j < n; ++j) { // the last 1-3 elements
+                float pj = sg.p[j], bj = HAS_BUF ? sg.buf[j] : 0.0f;
+                sgd_elem(pj, sg.g[j], bj, HAS_BUF, lr, mu, damp, wd, nesterov);
+                sg.p[j] = pj;
+                if (HAS_BUF)
+                    sg.buf[j] = bj;
+                if (sg.shadow)
+                    sg.shadow[j] = to16(sg.shadow_dtype, pj);
+            }
+        }
+    }
+}
+
 __global__ void __launch_bounds__(kBlock) k_sgd(sgd_table tab, float lr, float mu, float damp, float wd,
                                                 int nesterov)
 {
     const unsigned blk = blockIdx.x;
-    int si = 0;
-    for (int q = 1; q < tab.cnt; ++q)
-        si += blk >= tab.first[q] ? 1 : 0;
+    const int si = seg_of<PGK_SGD_MAX_SEG>(tab.first, blk);
     const pgk_sgd_seg sg = tab.seg[si];
     const size_t n = sg.n, base = (size_t)(blk - tab.first[si]) * kSgdChunk;
     const bool has_buf = sg.buf != nullptr;
     const bool aligned = ((((uintptr_t)sg.p) | ((uintptr_t)sg.g) | ((uintptr_t)sg.buf)) & 15) == 0 &&
                          (((uintptr_t)sg.shadow) & 7) == 0;
     if (aligned) {
-        float4 p[kSgdVec], g[kSgdVec], b[kSgdVec];
-        size_t e[kSgdVec];
-#pragma unroll
-        for (int k = 0; k < kSgdVec; ++k) {
-            e[k] = base + 4 * ((size_t)threadIdx.x + (size_t)k * kBlock);
-            if (e[k] + 4 <= n) {
-                p[k] = reinterpret_cast<const float4 *>(sg.p + e[k])[0];
-                g[k] = reinterpret_cast<const float4 *>(sg.g + e[k])[0];
-                b[k] = has_buf ? reinterpret_cast<const float4 *>(sg.buf + e[k])[0] : make_float4(0, 0, 0, 0);
-            }
-        }
-#pragma unroll
-        for (int k = 0; k < kSgdVec; ++k) {
-            if (e[k] + 4 <= n) {
-                sgd_elem(p[k].x, g[k].x, b[k].x, has_buf, lr, mu, damp, wd, nesterov);
-                sgd_elem(p[k].y, g[k].y, b[k].y, has_buf, lr, mu, damp, wd, nesterov);
-                sgd_elem(p[k].z, g[k].z, b[k].z, has_buf, lr, mu, damp, wd, nesterov);
-                sgd_elem(p[k].w, g[k].w, b[k].w, has_buf, lr, mu, damp, wd, nesterov);
-                reinterpret_cast<float4 *>(sg.p + e[k])[0] = p[k];
-                if (has_buf)
-                    reinterpret_cast<float4 *>(sg.buf + e[k])[0] = b[k];
-                if (sg.shadow) {
-                    ushort4 o;
-                    o.x = to16(sg.shadow_dtype, p[k].x);
-                    o.y = to16(sg.shadow_dtype, p[k].y);
-                    o.z = to16(sg.shadow_dtype, p[k].z);
-                    o.w = to16(sg.shadow_dtype, p[k].w);
-                    reinterpret_cast<ushort4 *>(sg.shadow + e[k])[0] = o;
-                }
-            } else {
-                for (size_t j = e[k]; j < n; ++j) { // the last 1-3 elements
-                    float pj = sg.p[j], bj = has_buf ? sg.buf[j] : 0.0f;
-                    sgd_elem(pj, sg.g[j], bj, has_buf, lr, mu, damp, wd, nesterov);
-                    sg.p[j] = pj;
-                    if (has_buf)
-                        sg.buf[j] = bj;
-                    if (sg.shadow)
-                        sg.shadow[j] = to16(sg.shadow_dtype, pj);
-                }
-            }
-        }
+        const bool full = base + kSgdChunk <= n;
+        if (full && has_buf)
+            sgd_vec<true, true>(sg, base, n, lr, mu, damp, wd, nesterov);
+        else if (full)
+            sgd_vec<true, false>(sg, base, n, lr, mu, damp, wd, nesterov);
+        else if (has_buf)
+            sgd_vec<false, true>(sg, base, n, lr, mu, damp, wd, nesterov);
+        else
+            sgd_vec<false, false>(sg, base, n, lr, mu, damp, wd, nesterov);
     } else {
         const size_t end = base + kSgdChunk < n ? base + kSgdChunk : n;
         for (size_t j = base + threadIdx.x; j < end; j += kBlock) {
@@ -559,7 +573,7 @@ __global__ void __launch_bounds__(kBlock) k_act_bwd16(int act, const float *__re
                 const float d1 = act ? gv[q + 1] * act_grad(act, zv[q + 1]) : gv[q + 1];
                 acc[q] += d0;
                 acc[q + 1] += d1;
-                w[q / 2] = (uint32_t)to16(dtype, d0) | ((uint32_t)to16(dtype, d1) << 16);
+                w[q / 2] = to16x2(dtype, d0, d1);
             }
             // columns past n hold g = 0, so they store zeros
             *reinterpret_cast<uint4 *>(d16 + r * ldd + c0) = make_uint4(w[0], w[1], w[2], w[3]);
@@ -607,9 +621,7 @@ constexpr size_t kUpChunk = (size_t)kBlock * 64;
 __global__ void __launch_bounds__(kBlock) k_upload(upload_table tab)
 {
     const unsigned b = blockIdx.x;
-    int s = 0;
-    for (int i = 1; i < tab.cnt; ++i)
-        s += b >= tab.first[i] ? 1 : 0;
+    const int s = seg_of<PGK_UPLOAD_MAX>(tab.first, b);
     const pgk_upload e = tab.e[s];
     const size_t base = (size_t)(b - tab.first[s]) * kUpChunk;
     const size_t end = base + kUpChunk < e.n ? base + kUpChunk : e.n;
@@ -690,7 +702,7 @@ extern "C" int pgk_upload_scatter(const pgk_upload *ents, int n, pgk_stream s)
         tab.first[q] = blocks;
         blocks += (unsigned)((ents[q].n + kUpChunk - 1) / kUpChunk);
     }
-    tab.first[n] = blocks;
+    seg_close<PGK_UPLOAD_MAX>(tab.first, n, blocks);
     tab.cnt = n;
     if (!blocks)
         return 0;
@@ -884,7 +896,7 @@ extern "C" int pgk_sgd_multi(const pgk_sgd_seg *segs, int nseg, float lr, float 
             if (blocks > 0x7fffffffu)
                 return (int)hipErrorInvalidValue;
         }
-        tab.first[cnt] = (unsigned)blocks;
+        seg_close<PGK_SGD_MAX_SEG>(tab.first, cnt, (unsigned)blocks);
         if (!blocks)
             continue;
         hipLaunchKernelGGL(k_sgd, dim3((unsigned)blocks), dim3(kBlock), 0, (hipStream_t)s, tab, lr, momentum,

@@ -514,8 +514,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1)
                         *reinterpret_cast<float4 *>(epi.z + off) = make_float4(zv[0], zv[1], zv[2], zv[3]);
                     if (epi.c16)
                         *reinterpret_cast<uint2 *>(epi.c16 + off) =
-                            make_uint2((uint32_t)to16(epi.dtype16, o[0]) | ((uint32_t)to16(epi.dtype16, o[1]) << 16),
-                                       (uint32_t)to16(epi.dtype16, o[2]) | ((uint32_t)to16(epi.dtype16, o[3]) << 16));
+                            make_uint2(to16x2(epi.dtype16, o[0], o[1]), to16x2(epi.dtype16, o[2], o[3]));
                 } else {
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {

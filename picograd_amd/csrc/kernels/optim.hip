@@ -11,21 +11,13 @@
 
 #include "launch.h"
 #include "convert16.h"
+#include "segtab.h"
 
 namespace {
 
 constexpr int kBlock = 256;
 
 inline int status() { return (int)hipGetLastError(); }
-
-// tensor index of block b: first[0] = 0 <= b < first[cnt]
-__device__ __forceinline__ int seg_of(const unsigned *first, int cnt, unsigned b)
-{
-    int s = 0;
-    for (int i = 1; i < cnt; ++i)
-        s += b >= first[i] ? 1 : 0;
-    return s;
-}
 
 // ---------------------------------------------------------------- Adam
 // adam.c:157-177 per element, in the order the reference's -O3 -ffast-math
@@ -71,7 +63,7 @@ __device__ __forceinline__ void adam_elem(float &p, float g, float &m, float &v,
 __global__ void __launch_bounds__(kBlock) k_adam(adam_table tab, pgk_adam_hyper h)
 {
     const unsigned b = blockIdx.x;
-    const int si = seg_of(tab.first, tab.cnt, b);
+    const int si = seg_of<PGK_ADAM_MAX_SEG>(tab.first, b);
     const pgk_adam_seg sg = tab.seg[si];
     const size_t base = (size_t)(b - tab.first[si]) * kAdamChunk;
     const size_t n = sg.n;
@@ -110,12 +102,8 @@ __global__ void __launch_bounds__(kBlock) k_adam(adam_table tab, pgk_adam_hyper 
                 if (ams)
                     *reinterpret_cast<float4 *>(VM + e[k]) = vm[k];
                 if (sg.shadow) {
-                    ushort4 o;
-                    o.x = to16(sg.shadow_dtype, p[k].x);
-                    o.y = to16(sg.shadow_dtype, p[k].y);
-                    o.z = to16(sg.shadow_dtype, p[k].z);
-                    o.w = to16(sg.shadow_dtype, p[k].w);
-                    *reinterpret_cast<ushort4 *>(sg.shadow + e[k]) = o;
+                    *reinterpret_cast<uint2 *>(sg.shadow + e[k]) =
+                        make_uint2(to16x2(sg.shadow_dtype, p[k].x, p[k].y), to16x2(sg.shadow_dtype, p[k].z, p[k].w));
                 }
             } else {
                 for (size_t j = e[k]; j < n; ++j) { // the last 1-3 elements
@@ -179,13 +167,31 @@ __global__ void __launch_bounds__(kBlock) k_sumsq(grad_table tab, double *__rest
 {
     __shared__ double sh[kBlock / 64];
     const unsigned b = blockIdx.x;
-    const int si = seg_of(tab.first, tab.cnt, b);
+    const int si = seg_of<PGK_GRAD_MAX_SEG>(tab.first, b);
     const pgk_grad_seg sg = tab.seg[si];
     const size_t base = (size_t)(b - tab.first[si]) * kSumChunk;
     const size_t n = sg.n;
     const float *__restrict__ G = sg.g;
     double acc = 0.0;
-    if ((((uintptr_t)G) & 15) == 0) {
+    if ((((uintptr_t)G) & 15) == 0 && base + kSumChunk <= n) {
+        // a whole chunk: every load issued before the first square (a load
+        // under a per-vector bound check is issued and waited for one at a
+        // time); the same per-thread order as the bounded path below
+        const float4 *__restrict__ G4 = reinterpret_cast<const float4 *>(G + base) + threadIdx.x;
+        float4 g[kSumVec];
+#pragma unroll
+        for (int k = 0; k < kSumVec; ++k)
+            g[k] = G4[k * kBlock];
+        __builtin_amdgcn_sched_barrier(0); // no square is moved between the loads
+#pragma unroll
+        for (int k = 0; k < kSumVec; ++k) {
+            const double x0 = g[k].x, x1 = g[k].y, x2 = g[k].z, x3 = g[k].w;
+            acc += x0 * x0;
+            acc += x1 * x1;
+            acc += x2 * x2;
+            acc += x3 * x3;
+        }
+    } else if ((((uintptr_t)G) & 15) == 0) {
         const size_t e0 = base + 4 * (size_t)threadIdx.x;
         float4 g[kSumVec];
 #pragma unroll
@@ -280,7 +286,7 @@ struct clamp_op {
 template <typename Op>
 __device__ __forceinline__ void grad_map(const grad_table &tab, unsigned b, Op op)
 {
-    const int si = seg_of(tab.first, tab.cnt, b);
+    const int si = seg_of<PGK_GRAD_MAX_SEG>(tab.first, b);
     const pgk_grad_seg sg = tab.seg[si];
     const size_t base = (size_t)(b - tab.first[si]) * kMapChunk;
     const size_t n = sg.n;
@@ -335,7 +341,7 @@ unsigned grad_table_fill(grad_table &tab, const pgk_grad_seg *segs, int cnt, siz
         tab.first[q] = blocks;
         blocks += (unsigned)((segs[q].n + chunk - 1) / chunk);
     }
-    tab.first[cnt] = blocks;
+    seg_close<PGK_GRAD_MAX_SEG>(tab.first, cnt, blocks);
     tab.cnt = cnt;
     return blocks;
 }
@@ -353,7 +359,7 @@ extern "C" int pgk_adam_multi(const pgk_adam_seg *segs, int nseg, const pgk_adam
             tab.first[q] = blocks;
             blocks += (unsigned)((segs[base + q].n + kAdamChunk - 1) / kAdamChunk);
         }
-        tab.first[cnt] = blocks;
+        seg_close<PGK_ADAM_MAX_SEG>(tab.first, cnt, blocks);
         tab.cnt = cnt;
         if (!blocks)
             continue;
