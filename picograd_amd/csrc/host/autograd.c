@@ -758,6 +758,19 @@ pg_node *pg_ag_matmul(pg_node *a, pg_node *b)
     return v ? attach(v, 2, (pg_node *[]){a, b}, pgm_matmul_backward, NULL, PG_AG_OP_MATMUL) : NULL;
 }
 
+/* the reduce node over a computed value v (v is the node's or freed) */
+static pg_node *reduce_attach(pg_node *a, size_t axis, bool keepdim, bool mean, pg_tensor *v)
+{
+    pga_red_ctx *cx = malloc(sizeof *cx);
+    if (!cx) {
+        pg_tensor_free(v);
+        return NULL;
+    }
+    cx->axis = axis;
+    cx->keepdim = keepdim;
+    return attach(v, 1, &a, bwd_reduce, cx, mean ? PG_AG_OP_MEAN : PG_AG_OP_SUM);
+}
+
 /* reduce.c:90-110 output shape: axis kept as 1 or removed; never 0-d */
 static pg_node *ag_reduce(pg_node *a, size_t axis, bool keepdim, bool mean)
 {
@@ -797,14 +810,7 @@ static pg_node *ag_reduce(pg_node *a, size_t axis, bool keepdim, bool mean)
         pg_tensor_free(v);
         return NULL;
     }
-    pga_red_ctx *cx = malloc(sizeof *cx);
-    if (!cx) {
-        pg_tensor_free(v);
-        return NULL;
-    }
-    cx->axis = axis;
-    cx->keepdim = keepdim;
-    return attach(v, 1, &a, bwd_reduce, cx, mean ? PG_AG_OP_MEAN : PG_AG_OP_SUM);
+    return reduce_attach(a, axis, keepdim, mean, v);
 }
 
 pg_node *pg_ag_sum(pg_node *a, size_t axis, bool keepdim) { return ag_reduce(a, axis, keepdim, false); }
@@ -817,6 +823,30 @@ static pg_node *reduce_all(pg_node *a, bool mean)
     if (!a || !a->value || a->value->ndim < 1) {
         pga_set_err("reduce_all: bad operand");
         return NULL;
+    }
+    const pg_tensor *t = a->value;
+    if (t->ndim == 2 && pgk_sum_all2_fits(t->shape[0], t->shape[1])) {
+        /* both nodes' values from one launch, the same sums in the same order */
+        if (!need_f32(t, "reduce"))
+            return NULL;
+        const size_t cols = t->shape[1];
+        pg_tensor *v1 = pgt_alloc(PG_DTYPE_F32, 1, (size_t[]){cols});
+        pg_tensor *v2 = v1 ? pgt_alloc(PG_DTYPE_F32, 1, (size_t[]){1}) : NULL;
+        if (!v2 || !pgd_check(pgk_sum_all2_f32((const float *)t->dev, (float *)v1->dev, (float *)v2->dev,
+                                               t->shape[0], cols, mean ? 1.0f / (float)cols : 1.0f, pgd_stream()),
+                              "reduce")) {
+            pg_tensor_free(v1);
+            pg_tensor_free(v2);
+            return NULL;
+        }
+        pg_node *n1 = reduce_attach(a, 0, false, false, v1);
+        if (!n1) {
+            pg_tensor_free(v2);
+            return NULL;
+        }
+        pg_node *out = reduce_attach(n1, 0, false, mean, v2);
+        pg_node_free(n1);
+        return out;
     }
     pg_node *cur = pg_node_retain(a);
     for (size_t d = a->value->ndim; d > 1; d--) {

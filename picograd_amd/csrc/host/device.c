@@ -269,7 +269,8 @@ void *pgd_scratch(int slot, size_t nbytes)
  * timer, and a free of a pending destination).  So a run of leaf creations
  * costs one kernel on the compute queue instead of one DMA each, with no
  * switch between the copy engine and the compute queue.  A slot is reused
- * once the last kernel that read it has finished (its event).  Larger
+ * once the last kernel that read it has finished (its event, recorded when
+ * the ring moves on from the slot).  Larger
  * copies go straight from pageable memory, which stages them before the
  * call returns. */
 #define PGD_STAGE_SLOTS 64
@@ -322,11 +323,22 @@ static bool up_flush(void)
         return true;
     const int n = g_up_n;
     g_up_n = 0;
-    bool ok = pgd_check(pgk_upload_scatter(g_up, n, (pgk_stream)g_stream), "upload");
+    return pgd_check(pgk_upload_scatter(g_up, n, (pgk_stream)g_stream), "upload");
+}
+
+/* leaves the current slot for the next: its event is recorded behind the
+ * last scatter that read it (one record per slot, not per batch), and the
+ * next slot is waited for when a scatter may still read it */
+static bool stage_next_slot(void)
+{
     g_stage_used[g_up_slot] = hip_ok(hipEventRecord(g_stage_ev[g_up_slot], g_stream), "hipEventRecord");
-    if (!g_stage_used[g_up_slot]) /* no event to wait on later: finish now */
-        ok = hip_ok(hipStreamSynchronize(g_stream), "hipStreamSynchronize") && ok;
-    return ok;
+    if (!g_stage_used[g_up_slot] && !hip_ok(hipStreamSynchronize(g_stream), "hipStreamSynchronize"))
+        return false; /* no event to wait on later: finish now */
+    g_up_slot = (g_up_slot + 1) % PGD_STAGE_SLOTS;
+    if (g_stage_used[g_up_slot] && !hip_ok(hipEventSynchronize(g_stage_ev[g_up_slot]), "hipEventSynchronize"))
+        return false;
+    g_stage_used[g_up_slot] = false;
+    return true;
 }
 
 /* a free of device memory a pending entry writes: queue the batch first,
@@ -356,12 +368,8 @@ bool pgd_h2d(void *dst, const void *src, size_t nbytes)
         up_flush_if_overlaps(dst, nbytes); /* a second write of the same bytes keeps its order */
         size_t off = (g_up_off + 15) & ~(size_t)15;
         if (off + nbytes > PGD_STAGE_BYTES || g_up_n == PGK_UPLOAD_MAX) {
-            if (!up_flush())
+            if (!up_flush() || !stage_next_slot())
                 return false;
-            g_up_slot = (g_up_slot + 1) % PGD_STAGE_SLOTS;
-            if (g_stage_used[g_up_slot] && !hip_ok(hipEventSynchronize(g_stage_ev[g_up_slot]), "hipEventSynchronize"))
-                return false;
-            g_stage_used[g_up_slot] = false;
             off = 0;
         }
         const size_t at = (size_t)g_up_slot * PGD_STAGE_BYTES + off;

@@ -322,6 +322,52 @@ __global__ void __launch_bounds__(kBlock) k_sum_axis_fin(const float *__restrict
     }
 }
 
+// Both reductions of a [rows, cols] reduce_all in one block, when each is a
+// single run (sum_axis_plan gives one slice for both): lane j adds column j
+// over the rows in row order (y1[j], as k_sum_axis_part with one slice),
+// then lane 0 adds y1 in order, times scale (y2).  The same additions in the
+// same order as the two k_sum_axis_part launches it replaces.
+constexpr int kSumAll2Max = 256;
+__global__ void __launch_bounds__(kSumAll2Max) k_sum_all2(const float *__restrict__ x, float *__restrict__ y1,
+                                                          float *__restrict__ y2, int rows, int cols, float scale)
+{
+    // the whole input goes through LDS first (every load of a lane issued
+    // at once; rows * cols <= 127 * 127 floats), so the serial column walks
+    // wait on LDS, not on memory
+    constexpr int kTile = 127 * 127, kPer = (kTile + kSumAll2Max - 1) / kSumAll2Max;
+    __shared__ float tile[kTile];
+    __shared__ float col[kSumAll2Max];
+    const int n = rows * cols, j = threadIdx.x;
+    float v[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const int i = j + k * kSumAll2Max;
+        v[k] = i < n ? x[i] : 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const int i = j + k * kSumAll2Max;
+        if (i < n)
+            tile[i] = v[k];
+    }
+    __syncthreads();
+    if (j < cols) {
+        float acc = 0.0f;
+#pragma unroll 8
+        for (int l = 0; l < rows; ++l)
+            acc += tile[l * cols + j];
+        col[j] = acc;
+        y1[j] = acc;
+    }
+    __syncthreads();
+    if (j == 0) {
+        float acc = 0.0f;
+        for (int l = 0; l < cols; ++l)
+            acc += col[l];
+        y2[0] = acc * scale;
+    }
+}
+
 // slices for a reduction: about 2^18 partial sums, runs of at least 64
 inline void sum_axis_plan(size_t outer, size_t len, size_t inner, size_t *slices, size_t *slice_len)
 {
@@ -628,6 +674,22 @@ __global__ void __launch_bounds__(kBlock) k_upload(upload_table tab)
     const unsigned char *__restrict__ src = (const unsigned char *)e.src;
     unsigned char *__restrict__ dst = (unsigned char *)e.dst;
     if ((((uintptr_t)src) | ((uintptr_t)dst)) % 16 == 0) {
+        // the source is host memory read over the bus: every 16-byte load
+        // of the chunk is issued before the first store, so a chunk costs
+        // one bus round trip rather than one per pass of the block
+        constexpr int kUpVec = (int)(kUpChunk / (16 * kBlock));
+        if (base + kUpChunk <= end) {
+            const uint4 *__restrict__ s4 = reinterpret_cast<const uint4 *>(src + base) + threadIdx.x;
+            uint4 *__restrict__ d4 = reinterpret_cast<uint4 *>(dst + base) + threadIdx.x;
+            uint4 v[kUpVec];
+#pragma unroll
+            for (int k = 0; k < kUpVec; ++k)
+                v[k] = s4[k * kBlock];
+#pragma unroll
+            for (int k = 0; k < kUpVec; ++k)
+                d4[k * kBlock] = v[k];
+            return;
+        }
         for (size_t j = base + 16 * (size_t)threadIdx.x; j + 16 <= end; j += 16 * (size_t)kBlock)
             *reinterpret_cast<uint4 *>(dst + j) = *reinterpret_cast<const uint4 *>(src + j);
         for (size_t j = (end & ~(size_t)15) + threadIdx.x; j < end; j += kBlock) // the last 0-15 bytes
@@ -837,6 +899,24 @@ extern "C" int pgk_sum_axis_f32(const float *x, float *y, size_t outer, size_t l
     if (slices > 1)
         hipLaunchKernelGGL(k_sum_axis_fin, dim3(grid_for(n)), dim3(kBlock), 0, (hipStream_t)s, part, y, n, slices,
                            scale);
+    return status();
+}
+
+extern "C" int pgk_sum_all2_fits(size_t rows, size_t cols)
+{
+    size_t s1, l1, s2, l2;
+    sum_axis_plan(1, rows, cols, &s1, &l1);
+    sum_axis_plan(1, cols, 1, &s2, &l2);
+    return rows && cols && rows * cols <= 127 * 127 && cols <= (size_t)kSumAll2Max && s1 == 1 && s2 == 1;
+}
+
+extern "C" int pgk_sum_all2_f32(const float *x, float *y1, float *y2, size_t rows, size_t cols, float scale,
+                                pgk_stream s)
+{
+    if (!pgk_sum_all2_fits(rows, cols))
+        return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_sum_all2, dim3(1), dim3(kSumAll2Max), 0, (hipStream_t)s, x, y1, y2, (int)rows, (int)cols,
+                       scale);
     return status();
 }
 

@@ -86,6 +86,14 @@ int pgk_expand_into_f32(float *dst, const float *src, const pgk_bcast *bc, float
 size_t pgk_sum_axis_workspace(size_t outer, size_t len, size_t inner);
 int pgk_sum_axis_f32(const float *x, float *y, size_t outer, size_t len, size_t inner,
                      float scale, void *ws, pgk_stream s);
+/* Both stages of reduce_all over a contiguous [rows, cols] in one launch:
+ * y1[cols] = column sums, y2[0] = scale * sum(y1), with the additions of
+ * two pgk_sum_axis_f32 calls in their order.  Only where each stage is a
+ * single run (pgk_sum_all2_fits: short axes, cols <= 256); otherwise
+ * hipErrorInvalidValue. */
+int pgk_sum_all2_fits(size_t rows, size_t cols);
+int pgk_sum_all2_f32(const float *x, float *y1, float *y2, size_t rows, size_t cols, float scale,
+                     pgk_stream s);
 
 /* dtype casts with the reference's RNE bit rules; dtype 1 = f16, 2 = bf16 */
 int pgk_cast_to16(int dtype, const float *src, uint16_t *dst, size_t n, pgk_stream s);
