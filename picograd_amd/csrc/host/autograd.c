@@ -297,11 +297,22 @@ typedef struct {
     lz_tensor out;
 } lz_op;
 
+/* reduce_all over a run's output, recorded with the run when it is small
+ * (pgj_small_reduce_fits): both reduction nodes' values come from the run's
+ * one-block kernel */
+typedef struct {
+    bool on;
+    int src; /* op index whose output is reduced */
+    lz_tensor r1, r2;
+    float scale;
+} lz_red;
+
 static struct {
     int nops, nin;
     lz_op op[LZ_MAX];
     lz_tensor in[LZ_MAX];
     size_t ndim, shape[PG_MAX_NDIM];
+    lz_red red;
     bool flushing;
 } g_lz;
 
@@ -412,12 +423,46 @@ static bool lz_run_eager(int k)
                      "binary");
 }
 
+/* the run as one block with the pending uploads (and the recorded
+ * reduction) folded in; false when it does not fit or fails to build, with
+ * nothing launched and the uploads still pending */
+static bool lz_run_small(pg_jit_graph *g, const int *ido)
+{
+    size_t numel = pg_shape_numel(g_lz.ndim, g_lz.shape);
+    if (numel > PGJ_SMALL_MAX)
+        return false;
+    pgk_upload up[PGK_UPLOAD_MAX];
+    int nup = pgd_upload_take(up, PGK_UPLOAD_MAX);
+    if (nup < 0)
+        return false;
+    if (!pgj_small_fits(numel, (size_t)nup, up) ||
+        (g_lz.red.on && !pgj_small_reduce_fits(g_lz.ndim, g_lz.shape))) {
+        for (int i = 0; i < nup; i++) /* back to the batch, in order */
+            pgd_upload_requeue(&up[i]);
+        return false;
+    }
+    (void)ido;
+    const void *ip[LZ_MAX];
+    void *op[LZ_MAX];
+    for (int j = 0; j < g_lz.nin; j++)
+        ip[j] = g_lz.in[j].dev;
+    for (int k = 0; k < g_lz.nops; k++)
+        op[k] = g_lz.op[k].out.dev;
+    bool ok = pgj_launch_small(g, g_lz.ndim, g_lz.shape, ip, (size_t)g_lz.nin, op, (size_t)g_lz.nops, up,
+                               (size_t)nup, g_lz.red.on ? g_lz.red.src : -1, g_lz.red.on ? g_lz.red.r1.dev : NULL,
+                               g_lz.red.on ? g_lz.red.r2.dev : NULL, g_lz.red.scale);
+    if (!ok)
+        for (int i = 0; i < nup; i++)
+            pgd_upload_requeue(&up[i]);
+    return ok;
+}
+
 void pga_lazy_flush(void)
 {
     if (!g_lz.nops || g_lz.flushing)
         return;
     g_lz.flushing = true;
-    bool ok = false;
+    bool ok = false, red_done = false;
     pg_jit_graph *g = pg_jit_graph_new();
     if (g) {
         pgj_graph_set_exact(g);
@@ -433,7 +478,10 @@ void pga_lazy_flush(void)
         }
         for (int k = 0; k < g_lz.nops && built; k++)
             pg_jit_mark_output(g, ido[k]);
-        pg_jit_exe *exe = built ? pg_jit_compile(g) : NULL;
+        if (built && lz_run_small(g, ido)) {
+            ok = red_done = true;
+        }
+        pg_jit_exe *exe = built && !ok ? pg_jit_compile(g) : NULL;
         if (exe) {
             pg_tensor tin[LZ_MAX], tout[LZ_MAX];
             const pg_tensor *pin[LZ_MAX];
@@ -451,9 +499,19 @@ void pga_lazy_flush(void)
         }
         pg_jit_graph_free(g);
     }
+    bool eager_ok = true;
     for (int k = 0; k < g_lz.nops && !ok; k++)
-        if (!lz_run_eager(k)) /* the device error is recorded; the rest are not run */
+        if (!(eager_ok = lz_run_eager(k))) /* the device error is recorded; the rest are not run */
             break;
+    if (g_lz.red.on) {
+        if (!red_done && eager_ok)
+            pgd_check(pgk_sum_all2_f32(g_lz.op[g_lz.red.src].out.dev, g_lz.red.r1.dev, g_lz.red.r2.dev,
+                                       g_lz.shape[0], g_lz.shape[1], g_lz.red.scale, pgd_stream()),
+                      "reduce");
+        pgt_ref_release(g_lz.red.r1.ref);
+        pgt_ref_release(g_lz.red.r2.ref);
+        g_lz.red.on = false;
+    }
     for (int j = 0; j < g_lz.nin; j++)
         pgt_ref_release(g_lz.in[j].ref);
     for (int k = 0; k < g_lz.nops; k++)
@@ -462,13 +520,41 @@ void pga_lazy_flush(void)
     g_lz.flushing = false;
 }
 
+/* reduce_all's two values from the pending run when t is one of its
+ * outputs and the run is small: the reduction is recorded and computed by
+ * the run's kernel.  False (nothing recorded) otherwise. */
+static bool lz_record_reduce_all(const pg_tensor *t, bool mean, pg_tensor **v1, pg_tensor **v2)
+{
+    if (!g_lz.nops || g_lz.red.on || g_lz.flushing || !pg_autograd_is_jit_enabled() || t->ndim != 2 ||
+        !pg_shape_equal(t->ndim, t->shape, g_lz.ndim, g_lz.shape) || !pgj_small_reduce_fits(t->ndim, t->shape) ||
+        pg_shape_numel(t->ndim, t->shape) > PGJ_SMALL_MAX)
+        return false;
+    int src = lz_find(t);
+    if (src >= 0 || src <= -LZ_MAX - 1)
+        return false;
+    const size_t cols = t->shape[1];
+    *v1 = pgt_alloc(PG_DTYPE_F32, 1, (size_t[]){cols});
+    *v2 = *v1 ? pgt_alloc(PG_DTYPE_F32, 1, (size_t[]){1}) : NULL;
+    if (!*v2) {
+        pg_tensor_free(*v1);
+        *v1 = NULL;
+        return false;
+    }
+    g_lz.red.src = -src - 1;
+    g_lz.red.scale = mean ? 1.0f / (float)cols : 1.0f;
+    lz_hold(&g_lz.red.r1, (*v1)->data_ref, (*v1)->dev, 1, (*v1)->shape);
+    lz_hold(&g_lz.red.r2, (*v2)->data_ref, (*v2)->dev, 1, (*v2)->shape);
+    g_lz.red.on = true;
+    return true;
+}
+
 /* records y = op(x...) into the run; NULL when the op must run eagerly
  * (nothing recorded then) */
 static pg_tensor *lz_record(int code, int nin, const pg_tensor *const *x, size_t nd, const size_t *shape)
 {
     if (code < 0 || !pg_autograd_is_jit_enabled() || g_lz.flushing)
         return NULL;
-    if (g_lz.nops && (g_lz.nops == LZ_MAX || !pg_shape_equal(nd, shape, g_lz.ndim, g_lz.shape)))
+    if (g_lz.nops && (g_lz.nops == LZ_MAX || g_lz.red.on || !pg_shape_equal(nd, shape, g_lz.ndim, g_lz.shape)))
         pga_lazy_flush();
     int src[2], fresh = 0;
     for (int i = 0; i < nin; i++) {
@@ -826,18 +912,28 @@ static pg_node *reduce_all(pg_node *a, bool mean)
     }
     const pg_tensor *t = a->value;
     if (t->ndim == 2 && pgk_sum_all2_fits(t->shape[0], t->shape[1])) {
-        /* both nodes' values from one launch, the same sums in the same order */
-        if (!need_f32(t, "reduce"))
+        /* both nodes' values from one launch, the same sums in the same
+         * order: the pending run's kernel when t is its output, else
+         * pgk_sum_all2_f32 */
+        if (!t->dev || t->dtype != PG_DTYPE_F32 || !pgt_is_contiguous(t)) {
+            pga_set_err("reduce: needs a contiguous f32 tensor");
             return NULL;
+        }
         const size_t cols = t->shape[1];
-        pg_tensor *v1 = pgt_alloc(PG_DTYPE_F32, 1, (size_t[]){cols});
-        pg_tensor *v2 = v1 ? pgt_alloc(PG_DTYPE_F32, 1, (size_t[]){1}) : NULL;
-        if (!v2 || !pgd_check(pgk_sum_all2_f32((const float *)t->dev, (float *)v1->dev, (float *)v2->dev,
-                                               t->shape[0], cols, mean ? 1.0f / (float)cols : 1.0f, pgd_stream()),
-                              "reduce")) {
-            pg_tensor_free(v1);
-            pg_tensor_free(v2);
-            return NULL;
+        pg_tensor *v1 = NULL, *v2 = NULL;
+        if (!lz_record_reduce_all(t, mean, &v1, &v2)) {
+            if (!need_f32(t, "reduce"))
+                return NULL;
+            v1 = pgt_alloc(PG_DTYPE_F32, 1, (size_t[]){cols});
+            v2 = v1 ? pgt_alloc(PG_DTYPE_F32, 1, (size_t[]){1}) : NULL;
+            if (!v2 || !pgd_check(pgk_sum_all2_f32((const float *)t->dev, (float *)v1->dev, (float *)v2->dev,
+                                                   t->shape[0], cols, mean ? 1.0f / (float)cols : 1.0f,
+                                                   pgd_stream()),
+                                  "reduce")) {
+                pg_tensor_free(v1);
+                pg_tensor_free(v2);
+                return NULL;
+            }
         }
         pg_node *n1 = reduce_attach(a, 0, false, false, v1);
         if (!n1) {

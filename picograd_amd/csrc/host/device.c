@@ -79,13 +79,14 @@ bool pgd_ok(void) { return pg_amd_init() == 0; }
 static bool up_flush(void);
 static void up_flush_if_overlaps(const void *p, size_t n);
 
-/* queues what is pending: the batched uploads, then the deferred forward
- * ops (which may read them) */
+/* queues what is pending: the deferred forward ops, whose kernel either
+ * performs the batched uploads itself (pgd_upload_take) or has them queued
+ * first (its launch calls pgd_stream, which comes back here and queues the
+ * batch while the run is flushing), then any uploads still pending */
 static bool flush_pending(void)
 {
-    bool ok = up_flush();
     pga_lazy_flush();
-    return ok;
+    return up_flush();
 }
 
 /* A second stream for work that runs beside the main stream's: pgd_fork
@@ -324,6 +325,23 @@ static bool up_flush(void)
     const int n = g_up_n;
     g_up_n = 0;
     return pgd_check(pgk_upload_scatter(g_up, n, (pgk_stream)g_stream), "upload");
+}
+
+int pgd_upload_take(pgk_upload *out, int max)
+{
+    if (!g_up_n)
+        return 0;
+    if (g_up_n > max)
+        return -1;
+    const int n = g_up_n;
+    memcpy(out, g_up, (size_t)n * sizeof *out);
+    g_up_n = 0;
+    return n;
+}
+
+void pgd_upload_requeue(const pgk_upload *e)
+{
+    g_up[g_up_n++] = *e;
 }
 
 /* leaves the current slot for the next: its event is recorded behind the

@@ -35,6 +35,14 @@ bool pgd_h2d(void *dst, const void *src, size_t nbytes);  /* enqueued */
 bool pgd_d2h(void *dst, const void *src, size_t nbytes);  /* waits */
 bool pgd_d2d(void *dst, const void *src, size_t nbytes);  /* enqueued */
 bool pgd_sync(void);
+/* hands the pending batch of small uploads (see pgd_h2d) to a caller whose
+ * kernel performs them: up to max entries are moved to out and no longer
+ * pending; 0 when nothing is pending, -1 (nothing moved) when more than max
+ * are.  The caller launches on pgd_stream() before queueing anything else. */
+int pgd_upload_take(pgk_upload *out, int max);
+/* puts a taken entry back at the end of the batch (call in the order taken,
+ * before anything else is uploaded) */
+void pgd_upload_requeue(const pgk_upload *e);
 void pgd_set_err(const char *fmt, ...);
 /* records a launcher status; false (and last error set) when non-zero */
 bool pgd_check(int status, const char *what);
@@ -144,6 +152,20 @@ enum { PGJ_OP_GELU_GRAD = 100, PGJ_OP_SIGN = 101, PGJ_OP_ERF_GRAD = 102 };
 bool pgj_launch(pg_jit_graph *g, size_t loop_ndim, const size_t *loop_shape,
                 const void *const *inputs, size_t ninputs, void *const *outputs,
                 size_t noutputs);
+/* A small run as one block (PGJ_SMALL_MAX loop elements at most): the block
+ * first performs the given uploads (at most PGJ_SMALL_UPLOAD_BYTES, every
+ * address and size a multiple of 16; pgj_small_fits), then the run, then,
+ * for red_out >= 0, reduce_all's two stages over output red_out of a 2-D
+ * loop shape (pgj_small_reduce_fits): r1[cols] its column sums and
+ * r2[0] = scale * sum(r1), the additions of pgk_sum_all2_f32 in its order. */
+#define PGJ_SMALL_MAX 16384
+#define PGJ_SMALL_UPLOAD_BYTES ((size_t)256 << 10)
+bool pgj_small_fits(size_t numel, size_t nup, const pgk_upload *up);
+bool pgj_small_reduce_fits(size_t loop_ndim, const size_t *loop_shape);
+bool pgj_launch_small(pg_jit_graph *g, size_t loop_ndim, const size_t *loop_shape,
+                      const void *const *inputs, size_t ninputs, void *const *outputs,
+                      size_t noutputs, const pgk_upload *up, size_t nup, int red_out, float *r1,
+                      float *r2, float scale);
 extern size_t pgj_stat_compiles, pgj_stat_hits;
 
 #endif

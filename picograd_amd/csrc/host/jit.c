@@ -73,6 +73,8 @@ typedef struct centry {
     size_t loop_shape[PG_MAX_NDIM];
     hipModule_t mod;
     hipFunction_t fmain, ffin;
+    int variant;     /* PGJ_VAR_MAIN, PGJ_VAR_SMALL or PGJ_VAR_SMALL + 1 + reduced output */
+    size_t nin, nout; /* the kernel argument block holds max(1, n) pointers of each */
     /* launch plan */
     unsigned grid_x, grid_y, fin_grid;
     int has_red;
@@ -81,6 +83,23 @@ typedef struct centry {
     size_t part_total;
     struct centry *next;
 } centry;
+
+/* kernel variants of one graph: the grid-stride (or [R x C] tiled) kernel,
+ * and the one-block kernel of a small run that also performs the pending
+ * uploads and, optionally, the two-stage column/total reduction of one of
+ * its outputs (PGJ_VAR_SMALL + 1 + that output's index) */
+enum { PGJ_VAR_MAIN = 0, PGJ_VAR_SMALL = 1 };
+#define PGJ_SMALL_THREADS 1024
+#define PGJ_SMALL_UPLOADS 4
+
+/* the small kernel's argument block after its in[NI] and out[NO] pointers
+ * (the generated struct asserts the same layout) */
+typedef struct {
+    pgk_upload up[PGJ_SMALL_UPLOADS];
+    unsigned nup, up_pieces;
+    float *r1, *r2;
+    float scale;
+} small_tail;
 
 struct pg_jit_exe {
     centry *e;
@@ -813,8 +832,12 @@ static char *gen_source(const pg_jit_graph *g, const plan_t *P, const bool *reac
     sb_add(&b, "%s\n", pgk_math_source);
     sb_add(&b, "typedef %s IDX;\n", wide ? "unsigned long long" : "unsigned int");
     sb_add(&b, "typedef float pgf4 __attribute__((ext_vector_type(4)));\n");
-    sb_add(&b, "struct PgArgs { const float *in[%d]; float *out[%d]; float *part[%d]; };\n", MAXIO * 2, MAXIO * 2,
-           MAXIO * 2);
+    /* exactly the pointers this kernel takes (the host packs the same) */
+    const int ni = P->nin ? P->nin : 1, no = P->nout ? P->nout : 1;
+    if (red)
+        sb_add(&b, "struct PgArgs { const float *in[%d]; float *out[%d]; float *part[%d]; };\n", ni, no, no);
+    else
+        sb_add(&b, "struct PgArgs { const float *in[%d]; float *out[%d]; };\n", ni, no);
     if (!red) {
         /* grid-stride over the flat loop: two strides per iteration, both
          * copies' loads issued before either copy's math */
@@ -928,6 +951,95 @@ static char *gen_source(const pg_jit_graph *g, const plan_t *P, const bool *reac
         else
             sb_add(&b, "      *(%s *)(a.out[%d] + c) = t; }\n", T, o);
         sb_add(&b, "    __syncthreads(); }\n");
+    }
+    sb_add(&b, "}\n");
+    return b.s;
+}
+
+bool pgj_small_reduce_fits(size_t lnd, const size_t *ls)
+{
+    return lnd == 2 && pgk_sum_all2_fits(ls[0], ls[1]);
+}
+
+/* The one-block kernel of a small run (PGJ_SMALL_THREADS lanes):
+ *  1. the uploads handed over by the device layer: 16-byte pieces of up to
+ *     PGJ_SMALL_UPLOADS entries, four pieces per lane in flight (the source
+ *     is host memory read over the bus), then a barrier, after which every
+ *     lane sees the uploaded inputs;
+ *  2. the run itself, the grid-stride body over one block;
+ *  3. with red_out >= 0, reduce_all's two stages over that output, as
+ *     k_sum_all2: the output staged in LDS, lane j adds column j over the
+ *     rows in order, lane 0 adds the column sums in order and scales. */
+static char *gen_source_small(const pg_jit_graph *g, const plan_t *P, const bool *reach, int red_out, size_t lnd,
+                              const size_t *ls)
+{
+    sbuf b = {0};
+    const int ni = P->nin ? P->nin : 1, no = P->nout ? P->nout : 1;
+    const int vec = P->vec, T = PGJ_SMALL_THREADS;
+    sb_add(&b, "// picograd-amd fused elementwise kernel, one-block run (generated)\n");
+    sb_add(&b, "%s\n", pgk_math_source);
+    sb_add(&b, "typedef unsigned int IDX;\n");
+    sb_add(&b, "typedef float pgf4 __attribute__((ext_vector_type(4)));\n");
+    sb_add(&b, "typedef unsigned int pgu4 __attribute__((ext_vector_type(4)));\n");
+    sb_add(&b, "struct PgUp { unsigned char *dst; const unsigned char *src; unsigned long long n; };\n");
+    sb_add(&b, "struct PgArgs { const float *in[%d]; float *out[%d]; PgUp up[%d]; unsigned nup, up_pieces;"
+               " float *r1, *r2; float scale; };\n", ni, no, PGJ_SMALL_UPLOADS);
+    sb_add(&b, "static_assert(sizeof(PgArgs) == %zu, \"argument block layout\");\n",
+           (size_t)(ni + no) * sizeof(void *) + sizeof(small_tail));
+    sb_add(&b, "extern \"C\" __global__ void __launch_bounds__(%d) pgjit_small(PgArgs a) {\n", T);
+    if (g->exact)
+        sb_add(&b, "#pragma clang fp contract(off)\n");
+    /* 1. uploads */
+    sb_add(&b, "  if (a.up_pieces) {\n");
+    sb_add(&b, "    const unsigned P = a.up_pieces;\n");
+    sb_add(&b, "    unsigned base[%d]; unsigned acc = 0;\n", PGJ_SMALL_UPLOADS);
+    sb_add(&b, "#pragma unroll\n    for (int e = 0; e < %d; ++e) { base[e] = acc; acc += e < (int)a.nup ?"
+               " (unsigned)(a.up[e].n / 16u) : 0u; }\n", PGJ_SMALL_UPLOADS);
+    sb_add(&b, "    for (unsigned p0 = threadIdx.x; p0 < P; p0 += 4u * %du) {\n", T);
+    sb_add(&b, "      pgu4 v[4]; unsigned q[4]; int en[4];\n");
+    sb_add(&b, "#pragma unroll\n      for (int k = 0; k < 4; ++k) {\n");
+    sb_add(&b, "        const unsigned p = p0 + (unsigned)k * %du; q[k] = p < P ? p : P - 1u;\n", T);
+    sb_add(&b, "        int e = 0;\n#pragma unroll\n        for (int j = 1; j < %d; ++j) e += (j < (int)a.nup && q[k] >= base[j]) ? 1 : 0;\n",
+           PGJ_SMALL_UPLOADS);
+    sb_add(&b, "        en[k] = e; v[k] = ((const pgu4 *)a.up[e].src)[q[k] - base[e]];\n      }\n");
+    sb_add(&b, "#pragma unroll\n      for (int k = 0; k < 4; ++k)\n");
+    sb_add(&b, "        if (p0 + (unsigned)k * %du < P) ((pgu4 *)a.up[en[k]].dst)[q[k] - base[en[k]]] = v[k];\n", T);
+    sb_add(&b, "    }\n    __syncthreads();\n  }\n");
+    /* 2. the run */
+    emit_prologue(&b, P);
+    sb_add(&b, "  {\n  const IDX N = (IDX)%lldu;\n", (long long)P->numel);
+    sb_add(&b, "  const IDX step = %du * %du;\n", T, vec);
+    sb_add(&b, "  IDX i = (IDX)threadIdx.x * %du;\n", vec);
+    sb_add(&b, "  for (; i + step < N; i += 2u * step) {\n");
+    sb_add(&b, "    const IDX i0 = i, i1 = i + step;\n");
+    emit_loads(&b, P, vec, "i0", 0);
+    emit_loads(&b, P, vec, "i1", 1);
+    emit_compute(&b, g, reach, vec, 0);
+    emit_compute(&b, g, reach, vec, 1);
+    emit_stores(&b, P, vec, "i0", 0);
+    emit_stores(&b, P, vec, "i1", 1);
+    sb_add(&b, "  }\n  if (i < N) {\n    const IDX i0 = i;\n");
+    emit_loads(&b, P, vec, "i0", 0);
+    emit_compute(&b, g, reach, vec, 0);
+    emit_stores(&b, P, vec, "i0", 0);
+    sb_add(&b, "  }\n  }\n");
+    /* 3. the reduction */
+    if (red_out >= 0 && lnd == 2) {
+        const long long R = (long long)ls[0], C = (long long)ls[1];
+        sb_add(&b, "  __syncthreads();\n");
+        sb_add(&b, "  __shared__ float tile[%lld];\n  __shared__ float col[%lld];\n", R * C, C);
+        sb_add(&b, "  {\n    const float *__restrict__ y = a.out[%d];\n", red_out);
+        sb_add(&b, "    for (int i0 = threadIdx.x; i0 < %lld; i0 += 4 * %d) {\n      float v[4];\n", R * C, T);
+        sb_add(&b, "#pragma unroll\n      for (int k = 0; k < 4; ++k) { const int i = i0 + k * %d; v[k] = y[i < %lld ? i : %lld]; }\n",
+               T, R * C, R * C - 1);
+        sb_add(&b, "#pragma unroll\n      for (int k = 0; k < 4; ++k) { const int i = i0 + k * %d; if (i < %lld) tile[i] = v[k]; }\n    }\n  }\n",
+               T, R * C);
+        sb_add(&b, "  __syncthreads();\n");
+        sb_add(&b, "  if (threadIdx.x < %lldu) {\n    float acc = 0.0f;\n", C);
+        sb_add(&b, "#pragma unroll 8\n    for (int l = 0; l < %lld; ++l) acc += tile[l * %lld + (int)threadIdx.x];\n", R, C);
+        sb_add(&b, "    col[threadIdx.x] = acc;\n    a.r1[threadIdx.x] = acc;\n  }\n  __syncthreads();\n");
+        sb_add(&b, "  if (threadIdx.x == 0) {\n    float acc = 0.0f;\n");
+        sb_add(&b, "    for (int l = 0; l < %lld; ++l) acc += col[l];\n    a.r2[0] = acc * a.scale;\n  }\n", C);
     }
     sb_add(&b, "}\n");
     return b.s;
@@ -1055,16 +1167,17 @@ static void entry_free(centry *e)
 }
 
 /* finds or builds the kernel for (g, loop shape) */
-static centry *get_entry(const pg_jit_graph *g, size_t lnd, const size_t *ls, bool *owned)
+static centry *get_entry(const pg_jit_graph *g, size_t lnd, const size_t *ls, int variant, bool *owned)
 {
     uint64_t h = pg_jit_graph_hash(g);
     h = fnv(&lnd, sizeof lnd, h);
     h = fnv(ls, lnd * sizeof(size_t), h);
+    h = fnv(&variant, sizeof variant, h);
     *owned = false;
     if (g_cache_on) {
         for (centry *e = g_cache; e; e = e->next)
-            if (e->hash == h && e->loop_ndim == lnd && !memcmp(e->loop_shape, ls, lnd * sizeof(size_t)) &&
-                graph_equal(g, e->g)) {
+            if (e->hash == h && e->variant == variant && e->loop_ndim == lnd &&
+                !memcmp(e->loop_shape, ls, lnd * sizeof(size_t)) && graph_equal(g, e->g)) {
                 pgj_stat_hits++;
                 return e;
             }
@@ -1093,7 +1206,13 @@ static centry *get_entry(const pg_jit_graph *g, size_t lnd, const size_t *ls, bo
         red |= P.out_red[o] != 0;
     if (!red)
         P.R = 0;
-    char *src = gen_source(g, &P, reach);
+    if (variant != PGJ_VAR_MAIN && (red || P.numel > PGJ_SMALL_MAX)) {
+        free(reach);
+        jset_err("run too large or reduced: no one-block kernel");
+        return NULL;
+    }
+    char *src = variant == PGJ_VAR_MAIN ? gen_source(g, &P, reach)
+                                        : gen_source_small(g, &P, reach, variant - PGJ_VAR_SMALL - 1, lnd, ls);
     free(reach);
     if (!src) {
         jset_err("codegen failed");
@@ -1108,11 +1227,16 @@ static centry *get_entry(const pg_jit_graph *g, size_t lnd, const size_t *ls, bo
         return NULL;
     }
     e->hash = h;
+    e->variant = variant;
+    e->nin = g->nin;
+    e->nout = g->nout;
     e->loop_ndim = lnd;
     memcpy(e->loop_shape, ls, lnd * sizeof(size_t));
     bool ok = compile_source(src, &e->mod);
     free(src);
-    if (!ok || hipModuleGetFunction(&e->fmain, e->mod, "pgjit_main") != hipSuccess ||
+    if (!ok ||
+        hipModuleGetFunction(&e->fmain, e->mod, variant == PGJ_VAR_MAIN ? "pgjit_main" : "pgjit_small") !=
+            hipSuccess ||
         (red && hipModuleGetFunction(&e->ffin, e->mod, "pgjit_fin") != hipSuccess)) {
         if (ok)
             jset_err("kernel symbol missing");
@@ -1120,7 +1244,9 @@ static centry *get_entry(const pg_jit_graph *g, size_t lnd, const size_t *ls, bo
         return NULL;
     }
     e->has_red = red;
-    if (!red) {
+    if (variant != PGJ_VAR_MAIN) {
+        e->grid_x = e->grid_y = 1;
+    } else if (!red) {
         int64_t items = (P.numel + P.vec - 1) / P.vec;
         int64_t blocks = (items + 255) / 256;
         if (blocks > 256 * 16)
@@ -1170,20 +1296,28 @@ static centry *get_entry(const pg_jit_graph *g, size_t lnd, const size_t *ls, bo
     return e;
 }
 
+/* The kernel's argument block: in[max(1, nin)], out[max(1, nout)], then
+ * part[max(1, nout)] for a reduced kernel or the small kernel's tail: only
+ * the bytes the kernel declares are passed, not a fixed maximum. */
 typedef struct {
-    const float *in[MAXIO * 2];
-    float *out[MAXIO * 2];
-    float *part[MAXIO * 2];
+    void *p[MAXIO * 6];
+    small_tail tail; /* follows p[0 .. k) in the small kernel's block (see pack_small) */
 } kargs;
+
+static size_t pack_ptrs(void **p, const void *const *inputs, size_t nin, void *const *outputs, size_t nout)
+{
+    size_t k = 0;
+    for (size_t i = 0; i < (nin ? nin : 1); i++)
+        p[k++] = i < nin ? (void *)inputs[i] : NULL;
+    for (size_t i = 0; i < (nout ? nout : 1); i++)
+        p[k++] = i < nout ? outputs[i] : NULL;
+    return k;
+}
 
 static bool launch_entry(centry *e, const void *const *inputs, size_t nin, void *const *outputs, size_t nout)
 {
     kargs a;
-    memset(&a, 0, sizeof a);
-    for (size_t i = 0; i < nin; i++)
-        a.in[i] = inputs[i];
-    for (size_t i = 0; i < nout; i++)
-        a.out[i] = outputs[i];
+    size_t k = pack_ptrs(a.p, inputs, nin, outputs, nout);
     hipStream_t s = (hipStream_t)pgd_stream();
     if (e->has_red) {
         float *part = pgd_scratch(0, e->part_total * sizeof(float));
@@ -1191,16 +1325,16 @@ static bool launch_entry(centry *e, const void *const *inputs, size_t nin, void 
             jset_err("scratch alloc failed");
             return false;
         }
-        for (size_t o = 0; o < nout; o++)
-            a.part[o] = e->part_floats[o] ? part + e->part_off[o] : NULL;
+        for (size_t o = 0; o < (nout ? nout : 1); o++)
+            a.p[k++] = o < nout && e->part_floats[o] ? part + e->part_off[o] : NULL;
     }
-    void *params[] = {&a};
+    void *params[] = {a.p};
     int tk = pgd_tbegin(PGD_T_JIT_MAIN);
     hipError_t err = hipModuleLaunchKernel(e->fmain, e->grid_x, e->grid_y, 1, 256, 1, 1, 0, s, params, NULL);
     pgd_tend(tk);
     if (err == hipSuccess && e->has_red) {
         unsigned nblk = e->grid_y;
-        void *fparams[] = {&a, &nblk};
+        void *fparams[] = {a.p, &nblk};
         tk = pgd_tbegin(PGD_T_JIT_FIN);
         err = hipModuleLaunchKernel(e->ffin, e->fin_grid, 1, 1, 256, 1, 1, 0, s, fparams, NULL);
         pgd_tend(tk);
@@ -1220,13 +1354,75 @@ bool pgj_launch(pg_jit_graph *g, size_t lnd, const size_t *ls, const void *const
         return false;
     }
     bool owned = false;
-    centry *e = get_entry(g, lnd, ls, &owned);
+    centry *e = get_entry(g, lnd, ls, PGJ_VAR_MAIN, &owned);
     if (!e)
         return false;
     bool ok = launch_entry(e, inputs, nin, outputs, nout);
     if (owned)
         entry_free(e);
     return ok;
+}
+
+bool pgj_small_fits(size_t numel, size_t nup, const pgk_upload *up)
+{
+    if (numel > PGJ_SMALL_MAX || nup > PGJ_SMALL_UPLOADS)
+        return false;
+    size_t bytes = 0;
+    for (size_t i = 0; i < nup; i++) {
+        if ((((uintptr_t)up[i].dst) | ((uintptr_t)up[i].src) | up[i].n) & 15)
+            return false;
+        bytes += up[i].n;
+    }
+    return bytes <= PGJ_SMALL_UPLOAD_BYTES;
+}
+
+bool pgj_launch_small(pg_jit_graph *g, size_t lnd, const size_t *ls, const void *const *inputs, size_t nin,
+                      void *const *outputs, size_t nout, const pgk_upload *up, size_t nup, int red_out, float *r1,
+                      float *r2, float scale)
+{
+    if (!g || nin != g->nin || nout != g->nout || (red_out >= 0 && (size_t)red_out >= nout)) {
+        jset_err("pgj_launch_small: argument mismatch");
+        return false;
+    }
+    size_t numel = pg_shape_numel(lnd, ls);
+    if (!pgj_small_fits(numel, nup, up) || (red_out >= 0 && !pgj_small_reduce_fits(lnd, ls))) {
+        jset_err("pgj_launch_small: run does not fit one block");
+        return false;
+    }
+    bool owned = false;
+    centry *e = get_entry(g, lnd, ls, PGJ_VAR_SMALL + 1 + red_out, &owned);
+    if (!e)
+        return false;
+    kargs a;
+    size_t k = pack_ptrs(a.p, inputs, nin, outputs, nout);
+    small_tail t;
+    memset(&t, 0, sizeof t);
+    size_t pieces = 0;
+    for (size_t i = 0; i < nup; i++) {
+        t.up[i] = up[i];
+        pieces += up[i].n / 16;
+    }
+    t.nup = (unsigned)nup;
+    t.up_pieces = (unsigned)pieces;
+    t.r1 = r1;
+    t.r2 = r2;
+    t.scale = scale;
+    /* the tail follows the pointers in one block (pointer-aligned) */
+    unsigned char blockbuf[sizeof a.p + sizeof t];
+    memcpy(blockbuf, a.p, k * sizeof(void *));
+    memcpy(blockbuf + k * sizeof(void *), &t, sizeof t);
+    void *params[] = {blockbuf};
+    hipStream_t s = (hipStream_t)pgd_stream();
+    int tk = pgd_tbegin(PGD_T_JIT_MAIN);
+    hipError_t err = hipModuleLaunchKernel(e->fmain, 1, 1, 1, PGJ_SMALL_THREADS, 1, 1, 0, s, params, NULL);
+    pgd_tend(tk);
+    if (owned)
+        entry_free(e);
+    if (err != hipSuccess) {
+        jset_err("hipModuleLaunchKernel: %s", hipGetErrorString(err));
+        return false;
+    }
+    return true;
 }
 
 /* ---------------------------------------------------------------- public API */
@@ -1254,7 +1450,7 @@ pg_jit_exe *pg_jit_compile(pg_jit_graph *g)
         }
     }
     bool owned = false;
-    centry *e = get_entry(g, o0->ndim, o0->shape, &owned);
+    centry *e = get_entry(g, o0->ndim, o0->shape, PGJ_VAR_MAIN, &owned);
     if (!e)
         return NULL;
     pg_jit_exe *x = calloc(1, sizeof *x);
