@@ -155,3 +155,62 @@ def test_backward_through_deferred_values(lib, oracle):
     assert abs(float(lib.value(loss)[0]) - want_loss) <= 1e-3
     for n in (loss, t3, na, nb, nc):
         lib.pg_node_free(n)
+
+
+@pytest.mark.parametrize("shape", [(64, 64), (37, 63), (127, 127), (1, 100), (100, 1), (130, 64)])
+@pytest.mark.parametrize("mean", [False, True])
+def test_small_runs_fold_uploads_and_reduce_all(lib, shape, mean):
+    """A small run ending in sum_all / mean_all (config 1's loop): with the
+    JIT on, one block performs the leaves' uploads, the run and both
+    reduction stages; the values equal the eager path's (JIT off: upload
+    scatter, one kernel per op, pgk_sum_all2_f32) bit for bit.  (37, 63)
+    has leaves that are not whole 16-byte pieces, (127, 127) the largest
+    folded reduction, (130, 64) a reduction that does not fold (its row
+    axis is reduced in two stages)."""
+    rng = np.random.default_rng(shape[0] * 1000 + shape[1])
+    a, b, c = (rng.uniform(-1, 1, shape).astype(np.float32) for _ in range(3))
+    red = "mean_all" if mean else "sum_all"
+
+    def build(L):
+        na, nb, nc = L.var(a), L.var(b), L.var(c)
+        t = L.op("tanh", L.op("relu", L.op("mul", L.op("add", na, nb), nc)))
+        loss = L.op(red, t)
+        direct = L.op(red, nc)  # a leaf: no run to fold into
+        return [loss, t, direct], [na, nb, nc, t, loss, direct]
+
+    d, e = run_both(lib, build)
+    for u, v in zip(d, e):
+        assert np.array_equal(bits(u), bits(v))
+
+
+@pytest.mark.parametrize("nleaves,side", [(5, 32), (4, 127)])
+def test_small_run_with_uploads_it_cannot_fold(lib, nleaves, side):
+    """More pending uploads than the one-block kernel takes (5 > 4), or more
+    bytes (4 x 127 x 127 floats > 256 KiB): the uploads go back to the batch
+    in order and the run still equals the eager path, as does the mse
+    tail's mean_all and the grads of a backward through it."""
+    rng = np.random.default_rng(nleaves * side)
+    leaves = [rng.standard_normal((side, side)).astype(np.float32) for _ in range(nleaves)]
+    target = rng.standard_normal((side, side)).astype(np.float32)
+
+    grads = {}
+
+    def build(L):
+        ns = [L.var(v) for v in leaves]
+        acc = ns[0]
+        made = list(ns)
+        for n in ns[1:]:
+            m = L.op("mul", acc, n)
+            acc = L.op("add", m, n)
+            made += [m, acc]
+        nt = L.var(target, requires_grad=False)
+        loss = L.op("mse", acc, nt, True)
+        L.pg_backward(loss)
+        grads[bool(L.pg_autograd_is_jit_enabled())] = [L.grad(n) for n in ns]
+        return [loss, acc], made + [nt, loss]
+
+    d, e = run_both(lib, build)
+    for u, v in zip(d, e):
+        assert np.array_equal(bits(u), bits(v))
+    for u, v in zip(grads[True], grads[False]):  # fused backward against eager: f32 reassociation only
+        assert np.max(np.abs(u - v)) <= 1e-5 * max(1.0, float(np.max(np.abs(v))))
