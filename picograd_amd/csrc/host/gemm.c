@@ -337,6 +337,24 @@ void pgm_matmul_backward(pg_node *n)
         if (best_cus) {
             tk = pgd_tbegin(PGD_T_GEMM16); /* the pair is one interval */
             pd.timed = pw.timed = false;
+            /* one launch holding both when it can (no second stream to
+             * fork and join), else the two on two streams */
+            pgk_gemm_desc dd = {M, K, N8, g16, N8, M * N8, M, wp, N8, s.bbat ? K * N8 : 0, K, ga->dev, K, M * K, B, ba};
+            pgk_gemm_desc dw = {K, N, Mw, ap, lda_w, sa_w, lda_w, g16, N8, Mw * N8, N8, gb->dev, N,
+                                s.bbat ? K * N : 0, Bw, bbeta};
+            size_t offw = 0, wsz = pgk_gemm16_pair_dw_workspace(&dd, &dw, best_cus, &offw);
+            void *ws = wsz ? pgd_scratch(1, wsz) : NULL;
+            int rc = wsz && !ws ? PGK_GEMM_NOT_PAIRED : pgk_gemm16_pair_dw(dt, &dd, &dw, best_cus, ws, pgd_stream());
+            if (rc != PGK_GEMM_NOT_PAIRED) {
+                pgd_check(rc, "dgrad + wgrad");
+                pgd_tend(tk);
+                if (wpad)
+                    pgd_free(wpad, wbytes);
+                if (apad)
+                    pgd_free(apad, abytes);
+                pgd_free(g16, gbytes);
+                return;
+            }
             pgk_stream side = pgd_fork();
             if (side) {
                 pd.cus = best_cus;

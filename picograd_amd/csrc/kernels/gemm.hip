@@ -257,12 +257,48 @@ struct TileMN {
     }
 };
 
-template <int BM, int BN, int WGM, int WGN, bool TA, bool TB, bool F16, bool EPI, int KB, int S>
-__global__ void __launch_bounds__(64 * WGM * WGN, 1)
-    k_gemm16(const uint16_t *__restrict__ A, size_t lda, size_t sA, int a_extent, const uint16_t *__restrict__ B,
-             size_t ldb, size_t sB, int b_extent, float *__restrict__ C, size_t ldc, size_t sC, int M, int N, int K,
-             int beta, int tiles_m, int tiles_n, pgk_epi epi, int k_total, int kz_step, int fast_ok)
+// A GEMM launch's arguments (one problem; a paired launch takes two).
+struct gemm_kargs {
+    const uint16_t *A;
+    size_t lda, sA;
+    int a_extent;
+    const uint16_t *B;
+    size_t ldb, sB;
+    int b_extent;
+    float *C;
+    size_t ldc, sC;
+    int M, N, K, beta, tiles_m, tiles_n;
+    pgk_epi epi;
+    int k_total, kz_step, fast_ok;
+};
+
+// one kernel configuration: block tile BM x BN on WGM x WGN waves, operand
+// layouts TA / TB, f16 or bf16, fused epilogue, k-tile depth KB, S stages
+template <int BM_, int BN_, int WGM_, int WGN_, bool TA_, bool TB_, bool F16_, bool EPI_, int KB_, int S_>
+struct gcfg {
+    static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_, KB = KB_, S = S_;
+    static constexpr bool TA = TA_, TB = TB_, F16 = F16_, EPI = EPI_;
+    static constexpr int NT = 64 * WGM * WGN;
+    static constexpr int LDS_U4 = S * (BM * KB / 8 + BN * KB / 8); // uint4 of LDS
+};
+
+// One block tile of problem g: tile pid of the nb tiles of batch entry (or
+// split-K slice) z, with the LDS ring at lds.  remap: block ids were dealt
+// to the 8 XCDs round-robin with pid % 8 naming the XCD.
+template <class CF>
+__device__ __forceinline__ void gemm16_block(const gemm_kargs &g, int pid, int nb, bool remap, int z,
+                                             LDS uint4 *const lds)
 {
+    constexpr int BM = CF::BM, BN = CF::BN, WGM = CF::WGM, WGN = CF::WGN, KB = CF::KB, S = CF::S;
+    constexpr bool TA = CF::TA, TB = CF::TB, F16 = CF::F16, EPI = CF::EPI;
+    const uint16_t *__restrict__ A = g.A;
+    const uint16_t *__restrict__ B = g.B;
+    float *__restrict__ C = g.C;
+    const size_t lda = g.lda, sA = g.sA, ldb = g.ldb, sB = g.sB, ldc = g.ldc, sC = g.sC;
+    const int a_extent = g.a_extent, b_extent = g.b_extent, M = g.M, N = g.N, K = g.K, beta = g.beta;
+    const int tiles_m = g.tiles_m, tiles_n = g.tiles_n, k_total = g.k_total, kz_step = g.kz_step;
+    const int fast_ok = g.fast_ok;
+    const pgk_epi &epi = g.epi;
     constexpr int NT = 64 * WGM * WGN;
     constexpr int WM = BM / WGM, WN = BN / WGN;
     constexpr int FM = WM / 32, FN = WN / 32;
@@ -271,15 +307,12 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1)
     // S-stage ring of A and B tiles in one LDS block; the k-loop below is
     // unrolled by S, so every stage index is a compile-time constant
     constexpr int SA = BM * KB / 8, SB = BN * KB / 8; // uint4 per stage
-    __shared__ uint4 smem[S * (SA + SB)];
-    LDS uint4 *const lds = (LDS uint4 *)smem;
     auto stA = [&](int st) { return lds + st * SA; };
     auto stB = [&](int st) { return lds + S * SA + st * SB; };
 
     // tile order: XCD-aware (block ids dealt round-robin to the 8 XCDs are
     // regrouped so consecutive ids share an XCD), then 8 tile-rows at a time
-    int nb = gridDim.x, pid = blockIdx.x;
-    if ((nb & 7) == 0)
+    if (remap && (nb & 7) == 0)
         pid = (pid & 7) * (nb >> 3) + (pid >> 3);
     const int GM = 8;
     const int per_group = GM * tiles_n;
@@ -289,9 +322,9 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1)
     const int in_group = pid - group * per_group;
     const int m0 = (first_m + in_group % gsz) * BM, n0 = (in_group / gsz) * BN;
 
-    const uint16_t *Ab = A + (size_t)blockIdx.z * sA;
-    const uint16_t *Bb = B + (size_t)blockIdx.z * sB;
-    float *Cb = C + (size_t)blockIdx.z * sC;
+    const uint16_t *Ab = A + (size_t)z * sA;
+    const uint16_t *Bb = B + (size_t)z * sB;
+    float *Cb = C + (size_t)z * sC;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WGN, wn = wave % WGN;
@@ -309,7 +342,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1)
     // valid reduction length of this batch entry: K, or for split-K slice z
     // the rest of k_total from z * kz_step; the last partial tile reads
     // zeros past it (kend % 8 == 0)
-    const int krem = k_total - (int)blockIdx.z * kz_step;
+    const int krem = k_total - z * kz_step;
     const int kend = krem < K ? krem : K;
     const int KT = (kend + KB - 1) / KB;
     // S-stage ring, tile t in stage t % S.  Between two barriers the
@@ -551,6 +584,30 @@ __global__ void __launch_bounds__(64 * WGM * WGN, 1)
     }
 }
 
+template <class CF>
+__global__ void __launch_bounds__(CF::NT, 1) k_gemm16(gemm_kargs g)
+{
+    __shared__ uint4 smem[CF::LDS_U4];
+    gemm16_block<CF>(g, (int)blockIdx.x, (int)gridDim.x, true, (int)blockIdx.z, (LDS uint4 *)smem);
+}
+
+// Two problems in one launch (the dgrad and wgrad of one matmul when each
+// alone leaves CUs idle): blocks [0, n1) take problem 1 (tile b % nb1 of
+// slice / batch entry b / nb1), the rest problem 2; one LDS ring, sized for
+// the larger configuration.  Both configurations have the same thread
+// count.  Problem 2's tiles are regrouped by XCD only when n1 % 8 == 0.
+template <class C1, class C2>
+__global__ void __launch_bounds__(C1::NT, 1) k_gemm16_pair(gemm_kargs g1, gemm_kargs g2, int nb1, int n1, int nb2)
+{
+    static_assert(C1::NT == C2::NT, "one block size");
+    __shared__ uint4 smem[C1::LDS_U4 > C2::LDS_U4 ? C1::LDS_U4 : C2::LDS_U4];
+    const int b = (int)blockIdx.x;
+    if (b < n1)
+        gemm16_block<C1>(g1, b % nb1, nb1, true, b / nb1, (LDS uint4 *)smem);
+    else
+        gemm16_block<C2>(g2, (b - n1) % nb2, nb2, (n1 & 7) == 0, (b - n1) / nb2, (LDS uint4 *)smem);
+}
+
 // the same epilogue as a pass over a finished C (split-K or k-tail runs)
 __global__ void __launch_bounds__(256) k_bias_act(float *__restrict__ c, size_t ldc, int m, int n, pgk_epi epi)
 {
@@ -592,17 +649,53 @@ __global__ void __launch_bounds__(256) k_pack_slab(int mn_major, const uint16_t 
     }
 }
 
-// split-K finish: C = (beta ? C : 0) + sum over the `splits` partial
+// split-K finish of up to two problems (grid z picks one; a problem with
+// splits = 0 is absent): C = (beta ? C : 0) + sum over the `splits` partial
 // products (each m x n, dense), added in split order.  With n and ldc
 // allowing 16-byte accesses, rows run along grid y (stride gridDim.y) and
 // columns along x, four per thread; otherwise (narrow outputs such as
 // n = 10) one element per thread over the flattened m x n, indexed with a
 // 32-bit division when m n fits
-__global__ void __launch_bounds__(256) k_splitk_sum(const float *__restrict__ part, int splits, int m, int n,
-                                                    float *__restrict__ c, size_t ldc, int beta, int v4)
+struct splitk_desc {
+    const float *part;
+    int splits, m, n;
+    float *c;
+    size_t ldc;
+    int beta, v4;
+};
+
+splitk_desc splitk_of(const float *part, int splits, size_t m, size_t n, float *c, size_t ldc, int beta)
 {
+    const int v4 = ((n | (ldc & 3)) & 3) == 0 && (((uintptr_t)c | (uintptr_t)part) & 15) == 0;
+    return splitk_desc{part, splits, (int)m, (int)n, c, ldc, beta, v4};
+}
+
+dim3 splitk_grid(const splitk_desc &a, const splitk_desc &b)
+{
+    unsigned gx = 1, gy = 1;
+    for (const splitk_desc *d : {&a, &b}) {
+        if (!d->splits)
+            continue;
+        const size_t mn = (size_t)d->m * d->n;
+        const unsigned x = d->v4 ? (unsigned)((d->n / 4 + 255) / 256) : (unsigned)((mn + 255) / 256 < 2048 ? (mn + 255) / 256 : 2048);
+        const unsigned y = d->v4 ? (unsigned)(d->m < 65535 ? d->m : 65535) : 1u;
+        gx = x > gx ? x : gx;
+        gy = y > gy ? y : gy;
+    }
+    return dim3(gx, gy, &a == &b || !b.splits ? 1u : 2u);
+}
+
+__global__ void __launch_bounds__(256) k_splitk_sum(splitk_desc d0, splitk_desc d1)
+{
+    const splitk_desc &d = blockIdx.z ? d1 : d0;
+    if (!d.splits)
+        return;
+    const float *__restrict__ part = d.part;
+    float *__restrict__ c = d.c;
+    const int m = d.m, n = d.n, splits = d.splits, beta = d.beta;
+    const size_t ldc = d.ldc;
     const size_t mn = (size_t)m * n;
-    if (v4) {
+    if (d.v4) {
         const int j = blockIdx.x * blockDim.x + threadIdx.x;
         if (j >= n >> 2)
             return;
@@ -616,6 +709,8 @@ __global__ void __launch_bounds__(256) k_splitk_sum(const float *__restrict__ pa
         }
         return;
     }
+    if (blockIdx.y)
+        return;
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < mn; i += (size_t)gridDim.x * blockDim.x) {
         size_t r, col;
         if (mn <= 0xffffffffu) {
@@ -717,34 +812,75 @@ struct gemm_args {
     int k_total = 0, kz_step = 0;
 };
 
+template <class CF>
+gemm_kargs make_kargs(const gemm_args &g, const pgk_epi &epi)
+{
+    gemm_kargs k;
+    k.A = g.a, k.lda = g.lda, k.sA = g.sa, k.a_extent = g.a_extent;
+    k.B = g.b, k.ldb = g.ldb, k.sB = g.sb, k.b_extent = g.b_extent;
+    k.C = g.c, k.ldc = g.ldc, k.sC = g.sc;
+    k.M = g.m, k.N = g.n, k.K = g.k, k.beta = g.beta;
+    k.tiles_m = (g.m + CF::BM - 1) / CF::BM, k.tiles_n = (g.n + CF::BN - 1) / CF::BN;
+    k.epi = epi;
+    k.k_total = g.k_total ? g.k_total : g.k, k.kz_step = g.kz_step;
+    k.fast_ok = (int)(g.lda < ((size_t)1 << 26) && g.ldb < ((size_t)1 << 26));
+    return k;
+}
+
 template <int BM, int BN, int WGM, int WGN, bool TA, bool TB, bool F16, bool EPI, int KB = 64, int S = 2>
 int launch_tile(const gemm_args &g, const pgk_epi &epi, hipStream_t s)
 {
-    const int tm = (g.m + BM - 1) / BM, tn = (g.n + BN - 1) / BN;
-    hipLaunchKernelGGL((k_gemm16<BM, BN, WGM, WGN, TA, TB, F16, EPI, KB, S>), dim3((unsigned)(tm * tn), 1, g.batch),
-                       dim3(64 * WGM * WGN), 0, s, g.a, g.lda, g.sa, g.a_extent, g.b, g.ldb, g.sb, g.b_extent, g.c,
-                       g.ldc, g.sc, g.m, g.n, g.k, g.beta, tm, tn, epi, g.k_total ? g.k_total : g.k, g.kz_step,
-                       (int)(g.lda < ((size_t)1 << 26) && g.ldb < ((size_t)1 << 26)));
+    using CF = gcfg<BM, BN, WGM, WGN, TA, TB, F16, EPI, KB, S>;
+    const gemm_kargs k = make_kargs<CF>(g, epi);
+    hipLaunchKernelGGL(k_gemm16<CF>, dim3((unsigned)(k.tiles_m * k.tiles_n), 1, g.batch), dim3(CF::NT), 0, s, k);
     return (int)hipGetLastError();
+}
+
+// the configuration launch_layout picks: 256 x 256 tiles (eight waves, each
+// 128 x 64) whenever they still give most CUs a tile, else 128 x 128 (four
+// waves, each 64 x 64; k-tiles of 64, two stages).  Big tiles take k-tiles
+// of 32 in a four-stage ring (128 KiB of LDS), except with both operands
+// K-contiguous: there a k-tile of 32 covers half of each 128-byte row
+// segment per load, and k-tiles of 64 in two stages measure faster
+inline bool use_big_tile(const gemm_args &g)
+{
+    const size_t big = (size_t)((g.m + 255) / 256) * ((g.n + 255) / 256) * g.batch;
+    return g.tile == 2 || (g.tile == 0 && big >= 128);
+}
+
+template <bool TA, bool TB, bool F16, bool EPI, bool BIG>
+using layout_cfg = typename std::conditional<
+    BIG,
+    typename std::conditional<!TA && !TB, gcfg<256, 256, 2, 4, TA, TB, F16, EPI, 64, 2>,
+                              gcfg<256, 256, 2, 4, TA, TB, F16, EPI, 32, 4>>::type,
+    gcfg<128, 128, 2, 2, TA, TB, F16, EPI, 64, 2>>::type;
+
+template <class CF>
+int launch_cfg(const gemm_args &g, const pgk_epi &epi, hipStream_t s)
+{
+    return launch_tile<CF::BM, CF::BN, CF::WGM, CF::WGN, CF::TA, CF::TB, CF::F16, CF::EPI, CF::KB, CF::S>(g, epi, s);
 }
 
 template <bool TA, bool TB, bool F16, bool EPI = false>
 int launch_layout(const gemm_args &g, hipStream_t s, const pgk_epi &epi = pgk_epi{})
 {
-    // 256 x 256 tiles (eight waves, each 128 x 64) whenever they still give
-    // most CUs a tile; else 128 x 128 (four waves, each 64 x 64; k-tiles of
-    // 64, two stages).  Big tiles take k-tiles of 32 in a four-stage ring
-    // (128 KiB of LDS), except with both operands K-contiguous: there a
-    // k-tile of 32 covers half of each 128-byte row segment per load, and
-    // k-tiles of 64 in two stages measure faster
-    const size_t big = (size_t)((g.m + 255) / 256) * ((g.n + 255) / 256) * g.batch;
-    if (g.tile == 2 || (g.tile == 0 && big >= 128)) {
-        if constexpr (!TA && !TB)
-            return launch_tile<256, 256, 2, 4, TA, TB, F16, EPI, 64, 2>(g, epi, s);
-        else
-            return launch_tile<256, 256, 2, 4, TA, TB, F16, EPI, 32, 4>(g, epi, s);
-    }
-    return launch_tile<128, 128, 2, 2, TA, TB, F16, EPI>(g, epi, s);
+    if (use_big_tile(g))
+        return launch_cfg<layout_cfg<TA, TB, F16, EPI, true>>(g, epi, s);
+    return launch_cfg<layout_cfg<TA, TB, F16, EPI, false>>(g, epi, s);
+}
+
+// dgrad (both operands K-contiguous) and wgrad (both MN-contiguous) of one
+// matmul in one launch; both on the same tile size
+template <bool F16, bool BIG>
+int launch_pair_dw(const gemm_args &gd, const gemm_args &gw, hipStream_t s)
+{
+    using CD = layout_cfg<false, false, F16, false, BIG>;
+    using CW = layout_cfg<true, true, F16, false, BIG>;
+    const gemm_kargs kd = make_kargs<CD>(gd, pgk_epi{}), kw = make_kargs<CW>(gw, pgk_epi{});
+    const int nb1 = kd.tiles_m * kd.tiles_n, nb2 = kw.tiles_m * kw.tiles_n;
+    const int n1 = nb1 * (int)gd.batch, n2 = nb2 * (int)gw.batch;
+    hipLaunchKernelGGL((k_gemm16_pair<CD, CW>), dim3((unsigned)(n1 + n2)), dim3(CD::NT), 0, s, kd, kw, nb1, n1, nb2);
+    return (int)hipGetLastError();
 }
 
 int launch_any(int f16, int ta, int tb, const gemm_args &g, hipStream_t s)
@@ -902,6 +1038,24 @@ static size_t tail_ws(int ta, int tb, size_t m, size_t n, size_t k, size_t batch
     return (a + 64 + b) * sizeof(uint16_t);
 }
 
+// the checks of pgk_gemm16_cu's operands
+int check_gemm_args(int ta, int tb, size_t m, size_t n, size_t k, const uint16_t *a, size_t lda, size_t stride_a,
+                    size_t a_extent, const uint16_t *b, size_t ldb, size_t stride_b, size_t b_extent, size_t batch)
+{
+    // k leaves headroom for the k offsets of the tiles the kernel loads
+    // past the end (from the zero page) to stay within int
+    if (m > 0x7fffffff || n > 0x7fffffff || k > 0x7fff0000 || batch > 65535)
+        return (int)hipErrorInvalidValue;
+    // 16-byte global loads: aligned bases, leading dims and batch strides
+    if ((((uintptr_t)a | (uintptr_t)b) & 15) || (lda & 7) || (ldb & 7) || (stride_a & 7) || (stride_b & 7))
+        return (int)hipErrorInvalidValue;
+    // the clamped loads stay inside [0, extent) of each operand
+    if (!a_extent || !b_extent || (ta && ((a_extent & 7) || a_extent < m)) || (tb && ((b_extent & 7) || b_extent < n)) ||
+        (!ta && a_extent < m) || (!tb && b_extent < n) || a_extent > 0x7fffffff || b_extent > 0x7fffffff)
+        return (int)hipErrorInvalidValue;
+    return 0;
+}
+
 extern "C" size_t pgk_gemm16_workspace_cu(int ta, int tb, size_t m, size_t n, size_t k, size_t batch, int cu_budget)
 {
     const gemm_plan pl = plan_gemm(m, n, k_inkernel(ta, tb, k), batch, cu_budget);
@@ -940,17 +1094,9 @@ extern "C" int pgk_gemm16_cu(int dtype, int ta, int tb, size_t m, size_t n, size
     const bool has_epi = epi && (epi->bias || epi->act != PGK_ACT_NONE || epi->z || epi->c16);
     if (has_epi && (beta || batch != 1 || (epi->c16 && epi->dtype16 != 1 && epi->dtype16 != 2)))
         return (int)hipErrorInvalidValue;
-    // k leaves headroom for the k offsets of the tiles the kernel loads
-    // past the end (from the zero page) to stay within int
-    if (m > 0x7fffffff || n > 0x7fffffff || k > 0x7fff0000 || batch > 65535)
-        return (int)hipErrorInvalidValue;
-    // 16-byte global loads: aligned bases, leading dims and batch strides
-    if ((((uintptr_t)a | (uintptr_t)b) & 15) || (lda & 7) || (ldb & 7) || (stride_a & 7) || (stride_b & 7))
-        return (int)hipErrorInvalidValue;
-    // the clamped loads stay inside [0, extent) of each operand
-    if (!a_extent || !b_extent || (ta && ((a_extent & 7) || a_extent < m)) || (tb && ((b_extent & 7) || b_extent < n)) ||
-        (!ta && a_extent < m) || (!tb && b_extent < n) || a_extent > 0x7fffffff || b_extent > 0x7fffffff)
-        return (int)hipErrorInvalidValue;
+    const int bad = check_gemm_args(ta, tb, m, n, k, a, lda, stride_a, a_extent, b, ldb, stride_b, b_extent, batch);
+    if (bad)
+        return bad;
     hipStream_t st = (hipStream_t)s;
     const int f16 = dtype == 1;
     const size_t kmain = k_inkernel(ta, tb, k), ktail = k - kmain;
@@ -988,11 +1134,8 @@ extern "C" int pgk_gemm16_cu(int dtype, int ta, int tb, size_t m, size_t n, size
         rc = launch_any(f16, ta, tb, g, st);
         if (rc)
             return rc;
-        {
-            const bool v4 = ((n | (ldc & 3)) & 3) == 0 && (((uintptr_t)c | (uintptr_t)part) & 15) == 0;
-            const dim3 grid = v4 ? dim3((unsigned)((n / 4 + 255) / 256), (unsigned)(m < 65535 ? m : 65535)) : dim3(gmn);
-            hipLaunchKernelGGL(k_splitk_sum, grid, dim3(256), 0, st, part, sp, (int)m, (int)n, c, ldc, beta, (int)v4);
-        }
+        const splitk_desc sd = splitk_of(part, sp, m, n, c, ldc, beta);
+        hipLaunchKernelGGL(k_splitk_sum, splitk_grid(sd, sd), dim3(256), 0, st, sd, sd);
         rc = (int)hipGetLastError();
         if (rc)
             return rc;
@@ -1034,6 +1177,64 @@ extern "C" int pgk_gemm16_cu(int dtype, int ta, int tb, size_t m, size_t n, size
         return (int)hipGetLastError();
     }
     return 0;
+}
+
+extern "C" size_t pgk_gemm16_pair_dw_workspace(const pgk_gemm_desc *d, const pgk_gemm_desc *w, int cu_d, size_t *off_w)
+{
+    const size_t wd = pgk_gemm16_workspace_cu(0, 0, d->m, d->n, d->k, d->batch, cu_d);
+    *off_w = (wd + 255) & ~(size_t)255;
+    return *off_w + pgk_gemm16_workspace_cu(1, 1, w->m, w->n, w->k, w->batch, kCUs - cu_d);
+}
+
+extern "C" int pgk_gemm16_pair_dw(int dtype, const pgk_gemm_desc *d, const pgk_gemm_desc *w, int cu_d, void *ws,
+                                  pgk_stream s)
+{
+    if (cu_d <= 0 || cu_d >= kCUs || !d->m || !d->n || !d->batch || !w->m || !w->n || !w->batch || !d->k || !w->k)
+        return PGK_GEMM_NOT_PAIRED;
+    int bad = check_gemm_args(0, 0, d->m, d->n, d->k, d->a, d->lda, d->stride_a, d->a_extent, d->b, d->ldb,
+                              d->stride_b, d->b_extent, d->batch);
+    if (!bad)
+        bad = check_gemm_args(1, 1, w->m, w->n, w->k, w->a, w->lda, w->stride_a, w->a_extent, w->b, w->ldb,
+                              w->stride_b, w->b_extent, w->batch);
+    if (bad)
+        return bad;
+    // one launch covers each problem: no k tail, one tile size for both
+    if (k_inkernel(0, 0, d->k) != d->k || k_inkernel(1, 1, w->k) != w->k)
+        return PGK_GEMM_NOT_PAIRED;
+    const gemm_plan pd = plan_gemm(d->m, d->n, d->k, d->batch, cu_d), pw = plan_gemm(w->m, w->n, w->k, w->batch,
+                                                                                      kCUs - cu_d);
+    if (pd.tile != pw.tile)
+        return PGK_GEMM_NOT_PAIRED;
+    size_t off_w = 0;
+    pgk_gemm16_pair_dw_workspace(d, w, cu_d, &off_w);
+    if ((pd.sp > 1 || pw.sp > 1) && !ws)
+        return (int)hipErrorInvalidValue;
+    // a split problem writes its slices' partials to its workspace part;
+    // one summing launch then adds both problems' slices in order
+    auto args = [&](const pgk_gemm_desc *x, int ta, int tb, const gemm_plan &pl, float *part) {
+        gemm_args g = {x->a, x->lda, x->stride_a, (int)x->a_extent, x->b, x->ldb, x->stride_b, (int)x->b_extent,
+                       x->c, x->ldc, x->stride_c, (int)x->m, (int)x->n, (int)x->k, x->beta, (unsigned)x->batch,
+                       pl.tile};
+        if (pl.sp > 1) {
+            const size_t ks = ((x->k + pl.sp - 1) / pl.sp + BK - 1) / BK * BK;
+            g.sa = ta ? ks * x->lda : ks, g.sb = tb ? ks * x->ldb : ks;
+            g.c = part, g.ldc = x->n, g.sc = x->m * x->n, g.k = (int)ks, g.beta = 0, g.batch = (unsigned)pl.sp;
+            g.k_total = (int)x->k, g.kz_step = (int)ks;
+        }
+        return g;
+    };
+    float *part_d = (float *)ws, *part_w = (float *)((char *)ws + off_w);
+    const gemm_args gd = args(d, 0, 0, pd, part_d), gw = args(w, 1, 1, pw, part_w);
+    hipStream_t st = (hipStream_t)s;
+    const bool big = pd.tile == 2;
+    int rc = dtype == 1 ? (big ? launch_pair_dw<true, true>(gd, gw, st) : launch_pair_dw<true, false>(gd, gw, st))
+                        : (big ? launch_pair_dw<false, true>(gd, gw, st) : launch_pair_dw<false, false>(gd, gw, st));
+    if (rc || (pd.sp <= 1 && pw.sp <= 1))
+        return rc;
+    const splitk_desc s1 = pd.sp > 1 ? splitk_of(part_d, pd.sp, d->m, d->n, d->c, d->ldc, d->beta) : splitk_desc{};
+    const splitk_desc s2 = pw.sp > 1 ? splitk_of(part_w, pw.sp, w->m, w->n, w->c, w->ldc, w->beta) : splitk_desc{};
+    hipLaunchKernelGGL(k_splitk_sum, splitk_grid(s1, s2), dim3(256), 0, st, s1, s2);
+    return (int)hipGetLastError();
 }
 
 extern "C" int pgk_gemm_f32(int ta, int tb, size_t m, size_t n, size_t k, const float *a, size_t lda,

@@ -155,6 +155,29 @@ int pgk_gemm16_cu(int dtype, int ta, int tb, size_t m, size_t n, size_t k, const
                   int cu_budget, pgk_stream s);
 size_t pgk_gemm16_workspace_cu(int ta, int tb, size_t m, size_t n, size_t k, size_t batch, int cu_budget);
 double pgk_gemm16_time(int ta, int tb, size_t m, size_t n, size_t k, size_t batch, int cu_budget);
+/* One GEMM problem of pgk_gemm16's parameters */
+typedef struct {
+    size_t m, n, k;
+    const uint16_t *a;
+    size_t lda, stride_a, a_extent;
+    const uint16_t *b;
+    size_t ldb, stride_b, b_extent;
+    float *c;
+    size_t ldc, stride_c, batch;
+    int beta;
+} pgk_gemm_desc;
+/* A matmul's dgrad d (both operands K-contiguous: ta = tb = 0) and wgrad w
+ * (both MN-contiguous: ta = tb = 1) in ONE launch, d planned for cu_d CUs
+ * and w for the rest, each split along k as its plan says (one more launch
+ * then adds both problems' slices): the two run side by side with no second
+ * stream.
+ * PGK_GEMM_NOT_PAIRED (nothing launched) when one launch cannot hold the
+ * pair: a k that needs a zero-padded tail launch, or the plans choose
+ * different tile sizes.  ws: pgk_gemm16_pair_dw_workspace bytes. */
+#define PGK_GEMM_NOT_PAIRED (-1)
+size_t pgk_gemm16_pair_dw_workspace(const pgk_gemm_desc *d, const pgk_gemm_desc *w, int cu_d, size_t *off_w);
+int pgk_gemm16_pair_dw(int dtype, const pgk_gemm_desc *d, const pgk_gemm_desc *w, int cu_d, void *ws,
+                       pgk_stream s);
 
 /* MFMA rate probe: `blocks` x 512 threads, each wave 8 x iters bf16
  * 32x32x16 MFMAs, operands from registers (lds 0) or LDS (lds 1); sink
