@@ -574,10 +574,29 @@ __device__ __forceinline__ float act_grad(int act, float z)
     return 1.0f;
 }
 
-__global__ void __launch_bounds__(kBlock) k_act_bwd16(int act, const float *__restrict__ g,
-                                                      const float *__restrict__ z, size_t m, size_t n,
-                                                      uint16_t *__restrict__ d16, size_t ldd, int dtype,
-                                                      float *__restrict__ part, size_t rpb)
+// one row of lane (cx, ry)'s eight columns: the products, their 16-bit
+// store and the column sums (in row order)
+template <int ACT>
+__device__ __forceinline__ void act_bwd_row(const float (&gv)[8], const float (&zv)[8], float (&acc)[8],
+                                            uint16_t *__restrict__ dst, int dtype)
+{
+    uint32_t w[4];
+#pragma unroll
+    for (int q = 0; q < 8; q += 2) {
+        const float d0 = ACT ? gv[q] * act_grad(ACT, zv[q]) : gv[q];
+        const float d1 = ACT ? gv[q + 1] * act_grad(ACT, zv[q + 1]) : gv[q + 1];
+        acc[q] += d0;
+        acc[q + 1] += d1;
+        w[q / 2] = to16x2(dtype, d0, d1);
+    }
+    // columns past n hold g = 0, so they store zeros
+    *reinterpret_cast<uint4 *>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+template <int ACT>
+__global__ void __launch_bounds__(kBlock) k_act_bwd16(const float *__restrict__ g, const float *__restrict__ z,
+                                                      size_t m, size_t n, uint16_t *__restrict__ d16, size_t ldd,
+                                                      int dtype, float *__restrict__ part, size_t rpb)
 {
     __shared__ float red[16][129];
     const int cx = threadIdx.x & 15, ry = threadIdx.x >> 4;
@@ -589,40 +608,49 @@ __global__ void __launch_bounds__(kBlock) k_act_bwd16(int act, const float *__re
     for (int q = 0; q < 8; ++q)
         acc[q] = 0.0f;
     if (c0 < ldd) {
-#pragma unroll 2
-        for (size_t r = rb + ry; r < re; r += 16) {
+        size_t r = rb + ry;
+        if (vec) {
+            // four of the lane's rows per pass, every load of the pass
+            // issued before the first product
+            constexpr int R = 4;
+            for (; r + 16 * (R - 1) < re; r += 16 * R) {
+                float4 gq[R][2], zq[R][2];
+#pragma unroll
+                for (int u = 0; u < R; ++u) {
+                    const size_t off = (r + 16 * u) * n + c0;
+                    gq[u][0] = *reinterpret_cast<const float4 *>(g + off);
+                    gq[u][1] = *reinterpret_cast<const float4 *>(g + off + 4);
+                    if (ACT) {
+                        zq[u][0] = *reinterpret_cast<const float4 *>(z + off);
+                        zq[u][1] = *reinterpret_cast<const float4 *>(z + off + 4);
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < R; ++u) {
+                    const float gv[8] = {gq[u][0].x, gq[u][0].y, gq[u][0].z, gq[u][0].w,
+                                         gq[u][1].x, gq[u][1].y, gq[u][1].z, gq[u][1].w};
+                    float zv[8] = {};
+                    if (ACT) {
+                        const float zt[8] = {zq[u][0].x, zq[u][0].y, zq[u][0].z, zq[u][0].w,
+                                             zq[u][1].x, zq[u][1].y, zq[u][1].z, zq[u][1].w};
+#pragma unroll
+                        for (int q = 0; q < 8; ++q)
+                            zv[q] = zt[q];
+                    }
+                    act_bwd_row<ACT>(gv, zv, acc, d16 + (r + 16 * u) * ldd + c0, dtype);
+                }
+            }
+        }
+        for (; r < re; r += 16) {
             float gv[8], zv[8];
             const size_t off = r * n + c0;
-            if (vec) {
-                const float4 g0 = *reinterpret_cast<const float4 *>(g + off);
-                const float4 g1 = *reinterpret_cast<const float4 *>(g + off + 4);
-                gv[0] = g0.x, gv[1] = g0.y, gv[2] = g0.z, gv[3] = g0.w;
-                gv[4] = g1.x, gv[5] = g1.y, gv[6] = g1.z, gv[7] = g1.w;
-                if (act) {
-                    const float4 z0 = *reinterpret_cast<const float4 *>(z + off);
-                    const float4 z1 = *reinterpret_cast<const float4 *>(z + off + 4);
-                    zv[0] = z0.x, zv[1] = z0.y, zv[2] = z0.z, zv[3] = z0.w;
-                    zv[4] = z1.x, zv[5] = z1.y, zv[6] = z1.z, zv[7] = z1.w;
-                }
-            } else {
 #pragma unroll
-                for (int q = 0; q < 8; ++q) {
-                    const bool in = c0 + q < n;
-                    gv[q] = in ? g[off + q] : 0.0f;
-                    zv[q] = (in && act) ? z[off + q] : 0.0f;
-                }
+            for (int q = 0; q < 8; ++q) {
+                const bool in = c0 + q < n;
+                gv[q] = in ? g[off + q] : 0.0f;
+                zv[q] = (in && ACT) ? z[off + q] : 0.0f;
             }
-            uint32_t w[4];
-#pragma unroll
-            for (int q = 0; q < 8; q += 2) {
-                const float d0 = act ? gv[q] * act_grad(act, zv[q]) : gv[q];
-                const float d1 = act ? gv[q + 1] * act_grad(act, zv[q + 1]) : gv[q + 1];
-                acc[q] += d0;
-                acc[q + 1] += d1;
-                w[q / 2] = to16x2(dtype, d0, d1);
-            }
-            // columns past n hold g = 0, so they store zeros
-            *reinterpret_cast<uint4 *>(d16 + r * ldd + c0) = make_uint4(w[0], w[1], w[2], w[3]);
+            act_bwd_row<ACT>(gv, zv, acc, d16 + r * ldd + c0, dtype);
         }
     }
     if (part) {
@@ -1023,8 +1051,13 @@ extern "C" int pgk_act_bwd16(int act, const float *g, const float *z, size_t m, 
         return (int)hipErrorInvalidValue;
     const unsigned gx = (unsigned)((ldd + 127) / 128);
     float *part = db ? (float *)ws : nullptr;
-    hipLaunchKernelGGL(k_act_bwd16, dim3(gx, (unsigned)nrb), dim3(kBlock), 0, (hipStream_t)s, act, g, z, m, n, d16,
-                       ldd, dtype, part, rpb);
+    const dim3 grid(gx, (unsigned)nrb);
+    if (act == 0)
+        hipLaunchKernelGGL(k_act_bwd16<0>, grid, dim3(kBlock), 0, (hipStream_t)s, g, z, m, n, d16, ldd, dtype, part, rpb);
+    else if (act == 1)
+        hipLaunchKernelGGL(k_act_bwd16<1>, grid, dim3(kBlock), 0, (hipStream_t)s, g, z, m, n, d16, ldd, dtype, part, rpb);
+    else
+        hipLaunchKernelGGL(k_act_bwd16<2>, grid, dim3(kBlock), 0, (hipStream_t)s, g, z, m, n, d16, ldd, dtype, part, rpb);
     if (db)
         hipLaunchKernelGGL(k_colsum_fin, dim3((unsigned)((n + 63) / 64)), dim3(64), 0, (hipStream_t)s, part, nrb, n,
                            db, db_beta);
