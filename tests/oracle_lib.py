@@ -197,6 +197,21 @@ def rel_fro(x: np.ndarray, ref: np.ndarray) -> float:
     return float(np.linalg.norm(x - ref) / max(np.linalg.norm(ref), 1e-300))
 
 
+def pure_rel(x: np.ndarray, ref: np.ndarray) -> dict:
+    """The unfloored elementwise relative error |x - ref| / |ref| over the
+    elements with ref != 0: its maximum, 99.9th percentile and median, and
+    the number of exact zeros of ref left out.  Reported beside max_rel: near
+    a zero of GELU' or tanh' the pure measure is ~eps * 0.5 / |ref| for any
+    f32 evaluation, so its maximum says where the zeros are rather than how
+    good the kernel is; the percentiles show the bulk."""
+    x = x.astype(np.float64).ravel()
+    ref = ref.astype(np.float64).ravel()
+    nz = ref != 0
+    r = np.abs(x[nz] - ref[nz]) / np.abs(ref[nz])
+    return {"max": float(r.max()) if r.size else 0.0, "p999": float(np.quantile(r, 0.999)) if r.size else 0.0,
+            "median": float(np.median(r)) if r.size else 0.0, "zeros_left_out": int((~nz).sum())}
+
+
 def max_rel(x: np.ndarray, ref: np.ndarray, floor_frac: float = 1e-2) -> float:
     """max |x - ref| / (|ref| + floor), floor = floor_frac * max|ref|.
 
