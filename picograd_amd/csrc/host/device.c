@@ -262,7 +262,7 @@ void *pgd_scratch(int slot, size_t nbytes)
     return g_scratch[slot];
 }
 
-/* Small host-to-device copies (up to 256 KiB) are batched.  The source is
+/* Host-to-device copies up to 4 MiB are batched.  The source is
  * copied into a ring of pinned staging slots that the device reads
  * directly, and the copy becomes an entry of the pending batch; one scatter
  * kernel (k_upload) writes the whole batch, launched when anything else is
@@ -271,11 +271,13 @@ void *pgd_scratch(int slot, size_t nbytes)
  * costs one kernel on the compute queue instead of one DMA each, with no
  * switch between the copy engine and the compute queue.  A slot is reused
  * once the last kernel that read it has finished (its event, recorded when
- * the ring moves on from the slot).  Larger
+ * the ring moves on from the slot).  Copies up to 4 MiB are staged as
+ * slot-sized pieces, one entry each.  Larger
  * copies go straight from pageable memory, which stages them before the
  * call returns. */
 #define PGD_STAGE_SLOTS 64
 #define PGD_STAGE_BYTES ((size_t)256 << 10)
+#define PGD_STAGE_LARGE ((size_t)4 << 20) /* staged in slot-sized pieces up to this */
 static unsigned char *g_stage;     /* host address */
 static unsigned char *g_stage_dev; /* the same memory as the device addresses it */
 static hipEvent_t g_stage_ev[PGD_STAGE_SLOTS];
@@ -382,21 +384,26 @@ bool pgd_h2d(void *dst, const void *src, size_t nbytes)
     /* deferred ops recorded before this copy may read what it overwrites */
     if (pga_lazy_pending() && !flush_pending())
         return false;
-    if (nbytes <= PGD_STAGE_BYTES && stage_ready()) {
+    if (nbytes <= PGD_STAGE_LARGE && stage_ready()) {
         up_flush_if_overlaps(dst, nbytes); /* a second write of the same bytes keeps its order */
-        size_t off = (g_up_off + 15) & ~(size_t)15;
-        if (off + nbytes > PGD_STAGE_BYTES || g_up_n == PGK_UPLOAD_MAX) {
-            if (!up_flush() || !stage_next_slot())
-                return false;
-            off = 0;
+        /* larger copies as slot-sized pieces, each an entry of the batch */
+        for (size_t done = 0; done < nbytes;) {
+            const size_t piece = nbytes - done < PGD_STAGE_BYTES ? nbytes - done : PGD_STAGE_BYTES;
+            size_t off = (g_up_off + 15) & ~(size_t)15;
+            if (off + piece > PGD_STAGE_BYTES || g_up_n == PGK_UPLOAD_MAX) {
+                if (!up_flush() || !stage_next_slot())
+                    return false;
+                off = 0;
+            }
+            const size_t at = (size_t)g_up_slot * PGD_STAGE_BYTES + off;
+            memcpy(g_stage + at, (const unsigned char *)src + done, piece);
+            g_up[g_up_n].dst = (unsigned char *)dst + done;
+            g_up[g_up_n].src = g_stage_dev + at;
+            g_up[g_up_n].n = piece;
+            g_up_n++;
+            g_up_off = off + piece;
+            done += piece;
         }
-        const size_t at = (size_t)g_up_slot * PGD_STAGE_BYTES + off;
-        memcpy(g_stage + at, src, nbytes);
-        g_up[g_up_n].dst = dst;
-        g_up[g_up_n].src = g_stage_dev + at;
-        g_up[g_up_n].n = nbytes;
-        g_up_n++;
-        g_up_off = off + nbytes;
         return true;
     }
     if (!up_flush())

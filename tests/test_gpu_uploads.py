@@ -87,3 +87,32 @@ def test_chain_loop_grads_stay_exact(lib, oracle):
                 assert np.max(np.abs(got - want)) <= 1e-5 * max(1.0, float(np.max(np.abs(want)))), it
         for n in (loss, t3, t2, t1, t0, na, nb, nc):
             lib.pg_node_free(n)
+
+
+def test_large_uploads_in_pieces(lib):
+    """Copies above one staging slot (256 KiB) up to 4 MiB go through the
+    ring as slot-sized pieces; larger ones through a pageable copy.  Odd
+    sizes around the piece and batch boundaries, interleaved with small
+    uploads, a rewrite of a large tensor, and a kernel reading one: every
+    read back equals its source."""
+    rng = np.random.default_rng(7)
+    sizes = [65536, 65537, 65536 * 3 + 5, 262143, 262144, 1048576, 1048577 - 4, 1000003, 4 << 18, (4 << 18) + 1]
+    made = []
+    for n in sizes:
+        arr = rng.standard_normal(n).astype(np.float32)
+        made.append((lib.tensor(arr), arr))
+        small = rng.standard_normal(int(rng.integers(1, 5000))).astype(np.float32)
+        made.append((lib.tensor(small), small))
+    for t, arr in made:
+        assert np.array_equal(lib.read(t), arr), arr.size
+    t, arr = made[10]  # 1,048,573 floats
+    arr2 = -arr
+    assert lib.pg_tensor_copy_from_host(t, arr2.ctypes.data)
+    x = lib.var(arr2)
+    y = lib.op("add", x, x)
+    assert np.array_equal(lib.value(y), arr2 + arr2)
+    assert np.array_equal(lib.read(t), arr2)
+    for n in (y, x):
+        lib.pg_node_free(n)
+    for t, _ in made:
+        lib.pg_tensor_free(t)
