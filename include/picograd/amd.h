@@ -102,6 +102,20 @@ pg_node *pg_amd_ag_linear16(pg_node *x, pg_node *w, pg_node *b, int act, pg_dtyp
 size_t pg_amd_jit_compiles(void);
 size_t pg_amd_jit_cache_hits(void);
 
+/* The launch plan of a 16-bit MFMA GEMM C[m, n] over a reduction of k
+ * (batch entries of it), as the library's GEMM paths choose it (a
+ * measurement and test aid): returns the tile (1: 128 x 128, four waves;
+ * 2: 256 x 256, eight waves; 3: 128 x 256, eight waves), stores the
+ * split-K factor (1 = none) in *splits and the planner's time estimate in
+ * seconds in *seconds (either may be NULL).  cu_budget: the CUs the launch
+ * may occupy when it shares the chip with another (a matmul's dgrad and
+ * wgrad run side by side when each alone leaves CUs idle), 0 for all.
+ * ta = 1: A is MN-contiguous (A^T stored), tb = 1: B is MN-contiguous; only
+ * a k that is not a multiple of 8 with a K-contiguous operand changes the
+ * plan. */
+int pg_amd_gemm16_plan(int ta, int tb, size_t m, size_t n, size_t k, size_t batch, int cu_budget, int *splits,
+                       double *seconds);
+
 /* Attainable bf16 MFMA rate of this device in TFLOP/s (a measurement aid
  * for rooflines): one block of eight waves per CU issues back-to-back
  * v_mfma_f32_32x32x16_bf16 on pseudo-random bf16 operands, from registers

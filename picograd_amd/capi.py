@@ -196,6 +196,7 @@ _AMD_PROTOS = {
     "pg_tensor_full_dtype": (vp, [ip, sz, SZP, fl]),
     "pg_amd_timer_enable": (None, [ip]),
     "pg_amd_mfma_probe": (C.c_double, [ip]),
+    "pg_amd_gemm16_plan": (ip, [ip, ip, sz, sz, sz, sz, ip, C.POINTER(C.c_int), C.POINTER(C.c_double)]),
     "pg_amd_timer_read": (C.c_double, [ip, C.POINTER(C.c_size_t)]),
     "pg_amd_timer_reset": (None, []),
     "pg_amd_params_save": (bo, [C.POINTER(vp), sz, C.c_char_p]),

@@ -434,6 +434,14 @@ void pg_gemm_ex(pg_dtype dtype, size_t m, size_t n, size_t k, const void *a, siz
         pgd_free(bp, bbytes);
 }
 
+int pg_amd_gemm16_plan(int ta, int tb, size_t m, size_t n, size_t k, size_t batch, int cu_budget, int *splits,
+                       double *seconds)
+{
+    if (seconds)
+        *seconds = pgk_gemm16_time(ta, tb, m, n, k, batch, cu_budget);
+    return pgk_gemm16_plan(ta, tb, m, n, k, batch, cu_budget, splits);
+}
+
 /* pg_gemm_ex with every buffer it needs (the zero-padded operand copies,
  * split-K partials, k-tail slabs) carved from the fixed no-alloc workspace
  * instead of the library allocator.  The operands take the same path as in

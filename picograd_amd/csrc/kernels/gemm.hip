@@ -836,24 +836,36 @@ int launch_tile(const gemm_args &g, const pgk_epi &epi, hipStream_t s)
     return (int)hipGetLastError();
 }
 
-// the configuration launch_layout picks: 256 x 256 tiles (eight waves, each
-// 128 x 64) whenever they still give most CUs a tile, else 128 x 128 (four
-// waves, each 64 x 64; k-tiles of 64, two stages).  Big tiles take k-tiles
-// of 32 in a four-stage ring (128 KiB of LDS), except with both operands
-// K-contiguous: there a k-tile of 32 covers half of each 128-byte row
-// segment per load, and k-tiles of 64 in two stages measure faster
-inline bool use_big_tile(const gemm_args &g)
+// The configurations launch_layout picks from (the planner's tile ids):
+//  - 2: 256 x 256 tiles, eight waves of 128 x 64; k-tiles of 32 in a
+//    four-stage ring (128 KiB of LDS), except with both operands
+//    K-contiguous: there a k-tile of 32 covers half of each 128-byte row
+//    segment per load, and k-tiles of 64 in two stages measure faster;
+//  - 3: 128 x 256 tiles, eight waves of 64 x 64: twice the tiles of 2 for
+//    grids 2 leaves short of the chip, without split-K's partials; k-tiles
+//    of 64 in three stages (144 KiB) with both operands K-contiguous, else
+//    of 32 in four stages (96 KiB);
+//  - 1: 128 x 128 tiles, four waves of 64 x 64; k-tiles of 64, two stages.
+// An unplanned launch (tile 0) takes 2 when that still gives most CUs a
+// tile, else 1.
+inline int tile_of(const gemm_args &g)
 {
+    if (g.tile)
+        return g.tile;
     const size_t big = (size_t)((g.m + 255) / 256) * ((g.n + 255) / 256) * g.batch;
-    return g.tile == 2 || (g.tile == 0 && big >= 128);
+    return big >= 128 ? 2 : 1;
 }
 
-template <bool TA, bool TB, bool F16, bool EPI, bool BIG>
+template <bool TA, bool TB, bool F16, bool EPI, int TILE>
 using layout_cfg = typename std::conditional<
-    BIG,
+    TILE == 2,
     typename std::conditional<!TA && !TB, gcfg<256, 256, 2, 4, TA, TB, F16, EPI, 64, 2>,
                               gcfg<256, 256, 2, 4, TA, TB, F16, EPI, 32, 4>>::type,
-    gcfg<128, 128, 2, 2, TA, TB, F16, EPI, 64, 2>>::type;
+    typename std::conditional<
+        TILE == 3,
+        typename std::conditional<!TA && !TB, gcfg<128, 256, 2, 4, TA, TB, F16, EPI, 64, 3>,
+                                  gcfg<128, 256, 2, 4, TA, TB, F16, EPI, 32, 4>>::type,
+        gcfg<128, 128, 2, 2, TA, TB, F16, EPI, 64, 2>>::type>::type;
 
 template <class CF>
 int launch_cfg(const gemm_args &g, const pgk_epi &epi, hipStream_t s)
@@ -864,23 +876,36 @@ int launch_cfg(const gemm_args &g, const pgk_epi &epi, hipStream_t s)
 template <bool TA, bool TB, bool F16, bool EPI = false>
 int launch_layout(const gemm_args &g, hipStream_t s, const pgk_epi &epi = pgk_epi{})
 {
-    if (use_big_tile(g))
-        return launch_cfg<layout_cfg<TA, TB, F16, EPI, true>>(g, epi, s);
-    return launch_cfg<layout_cfg<TA, TB, F16, EPI, false>>(g, epi, s);
+    switch (tile_of(g)) {
+    case 2: return launch_cfg<layout_cfg<TA, TB, F16, EPI, 2>>(g, epi, s);
+    case 3: return launch_cfg<layout_cfg<TA, TB, F16, EPI, 3>>(g, epi, s);
+    default: return launch_cfg<layout_cfg<TA, TB, F16, EPI, 1>>(g, epi, s);
+    }
 }
 
-// dgrad (both operands K-contiguous) and wgrad (both MN-contiguous) of one
-// matmul in one launch; both on the same tile size
-template <bool F16, bool BIG>
+// dgrad (both operands K-contiguous, tile TD) and wgrad (both MN-contiguous,
+// tile TW) of one matmul in one launch
+template <bool F16, int TD, int TW>
 int launch_pair_dw(const gemm_args &gd, const gemm_args &gw, hipStream_t s)
 {
-    using CD = layout_cfg<false, false, F16, false, BIG>;
-    using CW = layout_cfg<true, true, F16, false, BIG>;
+    using CD = layout_cfg<false, false, F16, false, TD>;
+    using CW = layout_cfg<true, true, F16, false, TW>;
     const gemm_kargs kd = make_kargs<CD>(gd, pgk_epi{}), kw = make_kargs<CW>(gw, pgk_epi{});
     const int nb1 = kd.tiles_m * kd.tiles_n, nb2 = kw.tiles_m * kw.tiles_n;
     const int n1 = nb1 * (int)gd.batch, n2 = nb2 * (int)gw.batch;
     hipLaunchKernelGGL((k_gemm16_pair<CD, CW>), dim3((unsigned)(n1 + n2)), dim3(CD::NT), 0, s, kd, kw, nb1, n1, nb2);
     return (int)hipGetLastError();
+}
+
+// both problems on tile `tile`
+template <bool F16>
+int launch_pair_tiles(int tile, const gemm_args &gd, const gemm_args &gw, hipStream_t s)
+{
+    switch (tile) {
+    case 2: return launch_pair_dw<F16, 2, 2>(gd, gw, s);
+    case 3: return launch_pair_dw<F16, 3, 3>(gd, gw, s);
+    default: return launch_pair_dw<F16, 1, 1>(gd, gw, s);
+    }
 }
 
 int launch_any(int f16, int ta, int tb, const gemm_args &g, hipStream_t s)
@@ -983,7 +1008,7 @@ __global__ void __launch_bounds__(512, 1) k_mfma_probe(float *sink, int iters, i
 // Ragged shapes such as M = 4097 (33 rows of 128-tiles) and weight grads
 // with a short output dim are where it matters.
 typedef struct {
-    int tile; // 2 = 256 x 256, 1 = 128 x 128
+    int tile; // 2 = 256 x 256, 3 = 128 x 256, 1 = 128 x 128
     int sp;   // split-K factor, 1 = none
 } gemm_plan;
 
@@ -991,28 +1016,37 @@ typedef struct {
 // runs beside it on the rest), 0 for the whole chip.
 static constexpr int kCUs = 256;
 
+// Time model: rounds of one block per CU, each block at its tile's rate
+// per CU (measured under a loaded chip), plus for a split its partials:
+// the slices write sp - 1 more tiles of C than one launch would, the sum
+// reads sp and writes one, at ~5 TB/s, and one more launch.  A split must
+// still win by 8 %: its partials also cost HBM capacity.
 static gemm_plan plan_gemm(size_t m, size_t n, size_t kin, size_t batch, int cu_budget = 0, double *time = nullptr)
 {
     const double cus = cu_budget > 0 && cu_budget < kCUs ? (double)cu_budget : (double)kCUs;
-    const double rate[3] = {0.0, 2.6e12, 4.4e12}, bw = 5.0e12;
+    struct shape {
+        int tile;
+        size_t bm, bn;
+        double rate;
+    };
+    static const shape shapes[3] = {{2, 256, 256, 4.4e12}, {3, 128, 256, 3.75e12}, {1, 128, 128, 2.6e12}};
+    const double bw = 5.0e12, launch = 5e-6;
     gemm_plan best = {2, 1};
     double best_t = 1e300;
-    for (int tile = 2; tile >= 1; --tile) {
-        const size_t bm = tile == 2 ? 256 : 128;
-        const size_t tiles = ((m + bm - 1) / bm) * ((n + bm - 1) / bm) * batch;
+    for (const shape &sh : shapes) {
+        const size_t tiles = ((m + sh.bm - 1) / sh.bm) * ((n + sh.bn - 1) / sh.bn) * batch;
         const int max_sp = batch == 1 && kin >= 1024 ? 8 : 1;
         for (int sp = 1; sp <= max_sp; ++sp) {
             const size_t ks = ((kin + sp - 1) / sp + BK - 1) / BK * BK;
             if (sp > 1 && ks * (size_t)(sp - 1) >= kin)
                 break; // the last slice would be empty
             const double rounds = ceil((double)(tiles * sp) / cus);
-            double t = rounds * 2.0 * (double)bm * (double)bm * (double)(sp > 1 ? ks : kin) / rate[tile];
+            double t = rounds * 2.0 * (double)sh.bm * (double)sh.bn * (double)(sp > 1 ? ks : kin) / sh.rate;
             if (sp > 1)
-                t += (double)(sp + 1) * (double)m * (double)n * 4.0 / bw;
-            // a split must win clearly: its partials also cost HBM capacity
+                t += 2.0 * (double)sp * (double)m * (double)n * 4.0 / bw + launch;
             if (t < best_t * (sp > 1 ? 0.92 : 1.0)) {
                 best_t = t;
-                best.tile = tile;
+                best.tile = sh.tile;
                 best.sp = sp;
             }
         }
@@ -1066,6 +1100,14 @@ extern "C" size_t pgk_gemm16_workspace_cu(int ta, int tb, size_t m, size_t n, si
 extern "C" size_t pgk_gemm16_workspace(int ta, int tb, size_t m, size_t n, size_t k, size_t batch)
 {
     return pgk_gemm16_workspace_cu(ta, tb, m, n, k, batch, 0);
+}
+
+extern "C" int pgk_gemm16_plan(int ta, int tb, size_t m, size_t n, size_t k, size_t batch, int cu_budget, int *splits)
+{
+    const gemm_plan pl = plan_gemm(m, n, k_inkernel(ta, tb, k), batch, cu_budget);
+    if (splits)
+        *splits = pl.sp;
+    return pl.tile;
 }
 
 extern "C" double pgk_gemm16_time(int ta, int tb, size_t m, size_t n, size_t k, size_t batch, int cu_budget)
@@ -1226,9 +1268,7 @@ extern "C" int pgk_gemm16_pair_dw(int dtype, const pgk_gemm_desc *d, const pgk_g
     float *part_d = (float *)ws, *part_w = (float *)((char *)ws + off_w);
     const gemm_args gd = args(d, 0, 0, pd, part_d), gw = args(w, 1, 1, pw, part_w);
     hipStream_t st = (hipStream_t)s;
-    const bool big = pd.tile == 2;
-    int rc = dtype == 1 ? (big ? launch_pair_dw<true, true>(gd, gw, st) : launch_pair_dw<true, false>(gd, gw, st))
-                        : (big ? launch_pair_dw<false, true>(gd, gw, st) : launch_pair_dw<false, false>(gd, gw, st));
+    int rc = dtype == 1 ? launch_pair_tiles<true>(pd.tile, gd, gw, st) : launch_pair_tiles<false>(pd.tile, gd, gw, st);
     if (rc || (pd.sp <= 1 && pw.sp <= 1))
         return rc;
     const splitk_desc s1 = pd.sp > 1 ? splitk_of(part_d, pd.sp, d->m, d->n, d->c, d->ldc, d->beta) : splitk_desc{};

@@ -155,6 +155,9 @@ int pgk_gemm16_cu(int dtype, int ta, int tb, size_t m, size_t n, size_t k, const
                   int cu_budget, pgk_stream s);
 size_t pgk_gemm16_workspace_cu(int ta, int tb, size_t m, size_t n, size_t k, size_t batch, int cu_budget);
 double pgk_gemm16_time(int ta, int tb, size_t m, size_t n, size_t k, size_t batch, int cu_budget);
+/* the tile (1: 128 x 128, 2: 256 x 256, 3: 128 x 256) and split-K factor
+ * (*splits) pgk_gemm16_cu's main launch takes for these sizes */
+int pgk_gemm16_plan(int ta, int tb, size_t m, size_t n, size_t k, size_t batch, int cu_budget, int *splits);
 /* One GEMM problem of pgk_gemm16's parameters */
 typedef struct {
     size_t m, n, k;

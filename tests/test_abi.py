@@ -192,3 +192,34 @@ def test_tensor_and_ops_abi_is_complete():
                  "pg_cos", "pg_erf", "pg_abs", "pg_clamp", "pg_relu", "pg_leaky_relu", "pg_sigmoid", "pg_tanh",
                  "pg_gelu", "pg_matmul", "pg_bmm"):
         assert name in every and hasattr(lib, name), name
+
+
+def _plan(lib, ta, tb, m, n, k, batch=1, cus=0):
+    sp, sec = C.c_int(0), C.c_double(0.0)
+    tile = lib.pg_amd_gemm16_plan(ta, tb, m, n, k, batch, cus, C.byref(sp), C.byref(sec))
+    assert sec.value > 0.0
+    return tile, sp.value
+
+
+def test_gemm_launch_plans_of_the_configs():
+    """The MFMA GEMM planner's choices for the configs' GEMMs (host logic):
+    256 x 256 tiles where they fill the chip (config 3, config 5's 4096-wide
+    layers), the 128 x 256 tile for config 4's ragged grads on their shares
+    of the chip (160 CUs for dgrad, 96 for wgrad: both then run without
+    split-K, in one launch), 128 x 128 tiles for config 5's first-layer
+    wgrad and split-K over 128 x 128 tiles for its 10-wide layer."""
+    lib = picograd_amd.load()
+    assert _plan(lib, 0, 0, 8192, 4096, 4096) == (2, 1)    # config 3 dgrad
+    assert _plan(lib, 1, 1, 4096, 4096, 8192) == (2, 1)    # config 3 wgrad
+    assert _plan(lib, 0, 1, 4096, 4096, 4096) == (2, 1)    # config 5 forward
+    assert _plan(lib, 1, 1, 1024, 4096, 4096) == (1, 1)    # config 5 first-layer wgrad
+    assert _plan(lib, 0, 1, 4096, 10, 4096) == (1, 8)      # config 5 10-wide forward
+    assert _plan(lib, 0, 0, 4097, 1000, 3000, cus=160) == (3, 1)  # config 4 dgrad
+    assert _plan(lib, 1, 1, 1000, 3000, 4097, cus=96) == (3, 1)   # config 4 wgrad
+    assert _plan(lib, 0, 0, 512, 128, 512, batch=32, cus=128) == (1, 1)  # config 4 bmm grads
+    # a budget of fewer CUs never makes the estimate faster
+    t_all, t_half = C.c_double(), C.c_double()
+    sp = C.c_int()
+    lib.pg_amd_gemm16_plan(0, 0, 4097, 1000, 3000, 1, 0, C.byref(sp), C.byref(t_all))
+    lib.pg_amd_gemm16_plan(0, 0, 4097, 1000, 3000, 1, 128, C.byref(sp), C.byref(t_half))
+    assert t_half.value >= t_all.value
