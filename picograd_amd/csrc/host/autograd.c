@@ -944,6 +944,31 @@ static pg_node *reduce_all(pg_node *a, bool mean)
         pg_node_free(n1);
         return out;
     }
+    if (t->ndim == 2 && pgk_sum_all2s_fits(t->shape[0], t->shape[1])) {
+        /* sliced column sums: the same sums in the same order as the
+         * pg_ag_sum / pg_ag_mean chain below, from one launch */
+        if (!need_f32(t, "reduce"))
+            return NULL;
+        const size_t cols = t->shape[1];
+        pg_tensor *v1 = pgt_alloc(PG_DTYPE_F32, 1, (size_t[]){cols});
+        pg_tensor *v2 = v1 ? pgt_alloc(PG_DTYPE_F32, 1, (size_t[]){1}) : NULL;
+        if (!v2 || !pgd_check(pgk_sum_all2s_f32((const float *)t->dev, (float *)v1->dev, (float *)v2->dev,
+                                                t->shape[0], cols, mean ? 1.0f / (float)cols : 1.0f,
+                                                pgd_stream()),
+                              "reduce")) {
+            pg_tensor_free(v1);
+            pg_tensor_free(v2);
+            return NULL;
+        }
+        pg_node *n1 = reduce_attach(a, 0, false, false, v1);
+        if (!n1) {
+            pg_tensor_free(v2);
+            return NULL;
+        }
+        pg_node *out = reduce_attach(n1, 0, false, mean, v2);
+        pg_node_free(n1);
+        return out;
+    }
     pg_node *cur = pg_node_retain(a);
     for (size_t d = a->value->ndim; d > 1; d--) {
         pg_node *nx = pg_ag_sum(cur, 0, false);

@@ -368,6 +368,47 @@ __global__ void __launch_bounds__(kSumAll2Max) k_sum_all2(const float *__restric
     }
 }
 
+// Both reductions of a [rows, cols] reduce_all in one block when the
+// column sums are sliced: lane (sl, c) adds rows [sl slice_len, ...) of
+// column c in row order (k_sum_axis_part's partial), lane c adds the
+// slices in order (k_sum_axis_fin, scale 1), then lane 0 adds the column
+// sums in order, times scale (k_sum_axis_part with one slice).  The same
+// additions in the same order as the three launches it replaces.
+constexpr int kSumAll2sThreads = 1024;
+__global__ void __launch_bounds__(kSumAll2sThreads) k_sum_all2s(const float *__restrict__ x, float *__restrict__ y1,
+                                                               float *__restrict__ y2, int rows, int cols,
+                                                               int slices, int slice_len, float scale)
+{
+    __shared__ float part[kSumAll2sThreads];
+    __shared__ float col[kSumAll2sThreads];
+    const int t = threadIdx.x;
+    if (t < slices * cols) {
+        const int sl = t / cols, c = t - sl * cols;
+        const int l0 = sl * slice_len, l1 = l0 + slice_len < rows ? l0 + slice_len : rows;
+        const float *p = x + c;
+        float acc = 0.0f;
+#pragma unroll 8
+        for (int l = l0; l < l1; ++l)
+            acc += p[(size_t)l * cols];
+        part[t] = acc;
+    }
+    __syncthreads();
+    if (t < cols) {
+        float acc = 0.0f;
+        for (int sl = 0; sl < slices; ++sl)
+            acc += part[sl * cols + t];
+        col[t] = acc;
+        y1[t] = acc;
+    }
+    __syncthreads();
+    if (t == 0) {
+        float acc = 0.0f;
+        for (int l = 0; l < cols; ++l)
+            acc += col[l];
+        y2[0] = acc * scale;
+    }
+}
+
 // slices for a reduction: about 2^18 partial sums, runs of at least 64
 inline void sum_axis_plan(size_t outer, size_t len, size_t inner, size_t *slices, size_t *slice_len)
 {
@@ -945,6 +986,26 @@ extern "C" int pgk_sum_all2_f32(const float *x, float *y1, float *y2, size_t row
         return (int)hipErrorInvalidValue;
     hipLaunchKernelGGL(k_sum_all2, dim3(1), dim3(kSumAll2Max), 0, (hipStream_t)s, x, y1, y2, (int)rows, (int)cols,
                        scale);
+    return status();
+}
+
+extern "C" int pgk_sum_all2s_fits(size_t rows, size_t cols)
+{
+    size_t s1, l1, s2, l2;
+    sum_axis_plan(1, rows, cols, &s1, &l1);
+    sum_axis_plan(1, cols, 1, &s2, &l2);
+    return rows && cols && rows < ((size_t)1 << 31) && s1 * cols <= (size_t)kSumAll2sThreads && s2 == 1;
+}
+
+extern "C" int pgk_sum_all2s_f32(const float *x, float *y1, float *y2, size_t rows, size_t cols, float scale,
+                                 pgk_stream s)
+{
+    if (!pgk_sum_all2s_fits(rows, cols))
+        return (int)hipErrorInvalidValue;
+    size_t slices, slice_len;
+    sum_axis_plan(1, rows, cols, &slices, &slice_len);
+    hipLaunchKernelGGL(k_sum_all2s, dim3(1), dim3(kSumAll2sThreads), 0, (hipStream_t)s, x, y1, y2, (int)rows,
+                       (int)cols, (int)slices, (int)slice_len, scale);
     return status();
 }
 

@@ -608,19 +608,26 @@ __global__ void __launch_bounds__(C1::NT, 1) k_gemm16_pair(gemm_kargs g1, gemm_k
         gemm16_block<C2>(g2, (b - n1) % nb2, nb2, (n1 & 7) == 0, (b - n1) / nb2, (LDS uint4 *)smem);
 }
 
-// the same epilogue as a pass over a finished C (split-K or k-tail runs)
+// the epilogue of one element: C = act(v + bias), the pre-activation and
+// the 16-bit copy beside it (gemm16_block's EPI path applies it from LDS)
+__device__ __forceinline__ void epi_store(const pgk_epi &epi, float *c, size_t off, int col, float v)
+{
+    const float zv = v + (epi.bias ? epi.bias[col] : 0.0f);
+    const float o = act_f(epi.act, zv);
+    c[off] = o;
+    if (epi.z)
+        epi.z[off] = zv;
+    if (epi.c16)
+        epi.c16[off] = to16(epi.dtype16, o);
+}
+
+// the same epilogue as a pass over a finished C (k-tail runs)
 __global__ void __launch_bounds__(256) k_bias_act(float *__restrict__ c, size_t ldc, int m, int n, pgk_epi epi)
 {
     const size_t mn = (size_t)m * n;
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < mn; i += (size_t)gridDim.x * blockDim.x) {
         const size_t r = i / n, col = i - r * n, off = r * ldc + col;
-        const float v = c[off] + (epi.bias ? epi.bias[col] : 0.0f);
-        const float o = act_f(epi.act, v);
-        c[off] = o;
-        if (epi.z)
-            epi.z[off] = v;
-        if (epi.c16)
-            epi.c16[off] = to16(epi.dtype16, o);
+        epi_store(epi, c, off, (int)col, c[off]);
     }
 }
 
@@ -651,23 +658,28 @@ __global__ void __launch_bounds__(256) k_pack_slab(int mn_major, const uint16_t 
 
 // split-K finish of up to two problems (grid z picks one; a problem with
 // splits = 0 is absent): C = (beta ? C : 0) + sum over the `splits` partial
-// products (each m x n, dense), added in split order.  With n and ldc
-// allowing 16-byte accesses, rows run along grid y (stride gridDim.y) and
-// columns along x, four per thread; otherwise (narrow outputs such as
-// n = 10) one element per thread over the flattened m x n, indexed with a
-// 32-bit division when m n fits
+// products (each m x n, dense), added in split order, then with `epi` the
+// GEMM's epilogue on that value (k_bias_act's arithmetic, in the same
+// pass).  With n and ldc allowing 16-byte accesses, rows run along grid y
+// (stride gridDim.y) and columns along x, four per thread; otherwise
+// (narrow outputs such as n = 10) one element per thread over the
+// flattened m x n, indexed with a 32-bit division when m n fits
 struct splitk_desc {
     const float *part;
     int splits, m, n;
     float *c;
     size_t ldc;
-    int beta, v4;
+    int beta, v4, has_epi;
+    pgk_epi epi;
 };
 
-splitk_desc splitk_of(const float *part, int splits, size_t m, size_t n, float *c, size_t ldc, int beta)
+splitk_desc splitk_of(const float *part, int splits, size_t m, size_t n, float *c, size_t ldc, int beta,
+                      const pgk_epi *epi = nullptr)
 {
-    const int v4 = ((n | (ldc & 3)) & 3) == 0 && (((uintptr_t)c | (uintptr_t)part) & 15) == 0;
-    return splitk_desc{part, splits, (int)m, (int)n, c, ldc, beta, v4};
+    int v4 = ((n | (ldc & 3)) & 3) == 0 && (((uintptr_t)c | (uintptr_t)part) & 15) == 0;
+    if (epi)
+        v4 = v4 && (((uintptr_t)epi->z) & 15) == 0 && (((uintptr_t)epi->c16) & 7) == 0;
+    return splitk_desc{part, splits, (int)m, (int)n, c, ldc, beta, v4, epi != nullptr, epi ? *epi : pgk_epi{}};
 }
 
 dim3 splitk_grid(const splitk_desc &a, const splitk_desc &b)
@@ -705,7 +717,24 @@ __global__ void __launch_bounds__(256) k_splitk_sum(splitk_desc d0, splitk_desc 
             for (int z = 0; z < splits; ++z)
                 acc += *(const f32x4 *)(p + (size_t)z * mn);
             f32x4 *q = (f32x4 *)(c + (size_t)r * ldc + 4 * j);
-            *q = beta ? *q + acc : acc;
+            const f32x4 v = beta ? *q + acc : acc;
+            if (!d.has_epi) {
+                *q = v;
+                continue;
+            }
+            const pgk_epi &epi = d.epi;
+            const size_t off = (size_t)r * ldc + 4 * j;
+            f32x4 zv = v, o;
+            if (epi.bias)
+                zv += *(const f32x4 *)(epi.bias + 4 * j);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                o[e] = act_f(epi.act, zv[e]);
+            *q = o;
+            if (epi.z)
+                *(f32x4 *)(epi.z + off) = zv;
+            if (epi.c16)
+                *(uint2 *)(epi.c16 + off) = make_uint2(to16x2(epi.dtype16, o[0], o[1]), to16x2(epi.dtype16, o[2], o[3]));
         }
         return;
     }
@@ -723,8 +752,12 @@ __global__ void __launch_bounds__(256) k_splitk_sum(splitk_desc d0, splitk_desc 
         float acc = 0.0f;
         for (int z = 0; z < splits; ++z)
             acc += part[(size_t)z * mn + i];
-        float *o = c + r * ldc + col;
-        *o = beta ? *o + acc : acc;
+        const size_t off = r * ldc + col;
+        const float v = beta ? c[off] + acc : acc;
+        if (d.has_epi)
+            epi_store(d.epi, c, off, (int)col, v);
+        else
+            c[off] = v;
     }
 }
 
@@ -1155,7 +1188,8 @@ extern "C" int pgk_gemm16_cu(int dtype, int ta, int tb, size_t m, size_t n, size
     const gemm_plan pl = plan_gemm(m, n, kmain, batch, cu_budget);
     const int sp = pl.sp > 1 ? pl.sp : 0;
     // the epilogue rides on the GEMM when one launch of the forward layout
-    // finishes C; otherwise it is a pass over C afterwards
+    // finishes C, on the split-K sum when that finishes C, otherwise it is
+    // a pass over C afterwards
     if (has_epi && !sp && !ktail && !ta && tb) {
         gemm_args g = {a, lda, stride_a, (int)a_extent, b, ldb, stride_b, (int)b_extent, c, ldc, stride_c,
                        (int)m, (int)n, (int)kmain, 0, 1u, pl.tile};
@@ -1176,10 +1210,11 @@ extern "C" int pgk_gemm16_cu(int dtype, int ta, int tb, size_t m, size_t n, size
         rc = launch_any(f16, ta, tb, g, st);
         if (rc)
             return rc;
-        const splitk_desc sd = splitk_of(part, sp, m, n, c, ldc, beta);
+        // the epilogue rides on the sum when nothing is added to C after it
+        const splitk_desc sd = splitk_of(part, sp, m, n, c, ldc, beta, has_epi && !ktail ? epi : nullptr);
         hipLaunchKernelGGL(k_splitk_sum, splitk_grid(sd, sd), dim3(256), 0, st, sd, sd);
         rc = (int)hipGetLastError();
-        if (rc)
+        if (rc || (has_epi && !ktail))
             return rc;
     } else if (kmain) {
         gemm_args g = {a, lda, stride_a, (int)a_extent, b, ldb, stride_b, (int)b_extent, c, ldc, stride_c,

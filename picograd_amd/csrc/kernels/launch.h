@@ -94,6 +94,13 @@ int pgk_sum_axis_f32(const float *x, float *y, size_t outer, size_t len, size_t 
 int pgk_sum_all2_fits(size_t rows, size_t cols);
 int pgk_sum_all2_f32(const float *x, float *y1, float *y2, size_t rows, size_t cols, float scale,
                      pgk_stream s);
+/* The same, in one launch, where the column sums are cut into slices of
+ * rows (the slices pgk_sum_axis_f32 takes, each added in row order, then
+ * the slices in order) and the sum over the columns is a single run
+ * (pgk_sum_all2s_fits: slices x cols <= 1024, cols < 128). */
+int pgk_sum_all2s_fits(size_t rows, size_t cols);
+int pgk_sum_all2s_f32(const float *x, float *y1, float *y2, size_t rows, size_t cols, float scale,
+                      pgk_stream s);
 
 /* dtype casts with the reference's RNE bit rules; dtype 1 = f16, 2 = bf16 */
 int pgk_cast_to16(int dtype, const float *src, uint16_t *dst, size_t n, pgk_stream s);

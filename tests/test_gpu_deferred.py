@@ -214,3 +214,34 @@ def test_small_run_with_uploads_it_cannot_fold(lib, nleaves, side):
         assert np.array_equal(bits(u), bits(v))
     for u, v in zip(grads[True], grads[False]):  # fused backward against eager: f32 reassociation only
         assert np.max(np.abs(u - v)) <= 1e-5 * max(1.0, float(np.max(np.abs(v))))
+
+
+@pytest.mark.parametrize("shape", [(4096, 10), (4097, 7), (2000, 17), (65536, 1)])
+@pytest.mark.parametrize("mean", [False, True])
+def test_sliced_reduce_all_in_one_launch(lib, shape, mean):
+    """sum_all / mean_all over [rows, cols] whose column sums are sliced
+    (config 5's mse over [4096, 10]): one launch gives the values of the
+    pg_ag_sum(axis 0) -> pg_ag_sum / pg_ag_mean chain (three launches) bit
+    for bit, and the same grads; the values are within f32 summation error
+    of the f64 sums."""
+    rng = np.random.default_rng(shape[0] + shape[1])
+    x = rng.standard_normal(shape).astype(np.float32)
+    na = lib.var(x)
+    one = lib.op("mean_all" if mean else "sum_all", na)
+    s0 = lib.op("sum", na, 0, False)
+    chain = lib.op("mean" if mean else "sum", s0, 0, False)
+    v1, v2 = lib.value(one), lib.value(chain)
+    assert np.array_equal(bits(v1), bits(v2))
+    col = x.astype(np.float64).sum(axis=0)
+    want = col.mean() if mean else col.sum()
+    assert abs(float(v1[0]) - want) <= 1e-5 * np.abs(x).astype(np.float64).sum() / (shape[1] if mean else 1)
+    lib.pg_backward(one)
+    g1 = lib.grad(na).copy()
+    lib.pg_node_free(one)
+    nb = lib.var(x)
+    s1 = lib.op("sum", nb, 0, False)
+    chain2 = lib.op("mean" if mean else "sum", s1, 0, False)
+    lib.pg_backward(chain2)
+    assert np.array_equal(bits(g1), bits(lib.grad(nb)))
+    for n in (chain2, s1, nb, chain, s0, na):
+        lib.pg_node_free(n)
