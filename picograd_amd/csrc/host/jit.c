@@ -922,34 +922,37 @@ static char *gen_source(const pg_jit_graph *g, const plan_t *P, const bool *reac
     }
     sb_add(&b, "}\n");
     /* finisher: out[c] (beta ? += : =) sum over blocks of part[blk][c].
-     * 16 column lanes x 16 block lanes per workgroup; block lane q sums
-     * partial rows q, q + 16, ... in that order (eight loads in flight, the
-     * adds still in row order) and the 16 lanes are combined in order, so
-     * the result does not depend on the launch shape.  Four columns per
-     * lane when C allows it. */
-    sb_add(&b, "extern \"C\" __global__ void __launch_bounds__(256) pgjit_fin(PgArgs a, unsigned nblk) {\n");
+     * 8 column lanes x 128 block lanes per workgroup of 1024 (32 columns
+     * with four per lane: each partial row is read as whole 128-byte
+     * lines, and a [.., 4096] grad takes 128 workgroups with every load in
+     * flight at once); block lane q sums partial rows q, q + 128, ... in
+     * that order (eight loads in flight, the adds still in row order) and
+     * the 128 lanes are combined by a fixed pairwise tree, so the result
+     * does not depend on timing.  Four columns per lane when C allows it. */
+    sb_add(&b, "extern \"C\" __global__ void __launch_bounds__(1024) pgjit_fin(PgArgs a, unsigned nblk) {\n");
     sb_add(&b, "  const IDX C = (IDX)%lldULL;\n", (long long)P->C);
-    sb_add(&b, "  const IDX tc = threadIdx.x & 15u, tr = threadIdx.x >> 4;\n");
+    sb_add(&b, "  const IDX tc = threadIdx.x & 7u, tr = threadIdx.x >> 3;\n");
     const char *T = vec == 4 ? "pgf4" : "float";
-    sb_add(&b, "  const IDX c = ((IDX)blockIdx.x * 16u + tc) * %du;\n", vec);
-    sb_add(&b, "  __shared__ %s red[16][17];\n", T);
+    sb_add(&b, "  const IDX c = ((IDX)blockIdx.x * 8u + tc) * %du;\n", vec);
+    sb_add(&b, "  __shared__ %s red[128][9];\n", T);
     for (int o = 0; o < P->nout; o++) {
         if (!P->out_red[o])
             continue;
         sb_add(&b, "  { const float *__restrict__ pp = a.part[%d];\n", o);
         sb_add(&b, "    %s s = (%s)(0.0f);\n", T, T);
         sb_add(&b, "    if (c < C) {\n      unsigned k = tr;\n");
-        sb_add(&b, "      for (; k + 112u < nblk; k += 128u) {\n        %s v[8];\n", T);
-        sb_add(&b, "#pragma unroll\n        for (int q = 0; q < 8; q++) v[q] = *(const %s *)(pp + (IDX)(k + 16u * q) * C + c);\n", T);
+        sb_add(&b, "      for (; k + 896u < nblk; k += 1024u) {\n        %s v[8];\n", T);
+        sb_add(&b, "#pragma unroll\n        for (int q = 0; q < 8; q++) v[q] = *(const %s *)(pp + (IDX)(k + 128u * q) * C + c);\n", T);
         sb_add(&b, "#pragma unroll\n        for (int q = 0; q < 8; q++) s += v[q];\n      }\n");
-        sb_add(&b, "      for (; k < nblk; k += 16u) s += *(const %s *)(pp + (IDX)k * C + c);\n    }\n", T);
+        sb_add(&b, "      for (; k < nblk; k += 128u) s += *(const %s *)(pp + (IDX)k * C + c);\n    }\n", T);
         sb_add(&b, "    red[tr][tc] = s; __syncthreads();\n");
-        sb_add(&b, "    if (tr == 0 && c < C) { %s t = red[0][tc];\n", T);
-        sb_add(&b, "      for (int q = 1; q < 16; q++) t += red[q][tc];\n");
+        sb_add(&b, "    for (unsigned h = 64u; h > 0u; h >>= 1) {\n");
+        sb_add(&b, "      if (tr < h) red[tr][tc] += red[tr + h][tc];\n      __syncthreads();\n    }\n");
+        sb_add(&b, "    if (tr == 0 && c < C) {\n");
         if (P->out_beta[o])
-            sb_add(&b, "      *(%s *)(a.out[%d] + c) += t; }\n", T, o);
+            sb_add(&b, "      *(%s *)(a.out[%d] + c) += red[0][tc]; }\n", T, o);
         else
-            sb_add(&b, "      *(%s *)(a.out[%d] + c) = t; }\n", T, o);
+            sb_add(&b, "      *(%s *)(a.out[%d] + c) = red[0][tc]; }\n", T, o);
         sb_add(&b, "    __syncthreads(); }\n");
     }
     sb_add(&b, "}\n");
@@ -1271,7 +1274,7 @@ static centry *get_entry(const pg_jit_graph *g, size_t lnd, const size_t *ls, in
             rb = 65535;
         e->grid_x = (unsigned)cb;
         e->grid_y = (unsigned)rb;
-        e->fin_grid = (unsigned)((P.C + 16 * vec - 1) / (16 * vec));
+        e->fin_grid = (unsigned)((P.C + 8 * vec - 1) / (8 * vec));
         size_t off = 0;
         for (int o = 0; o < P.nout; o++) {
             e->part_floats[o] = P.out_red[o] ? (size_t)rb * (size_t)P.C : 0;
@@ -1336,7 +1339,7 @@ static bool launch_entry(centry *e, const void *const *inputs, size_t nin, void 
         unsigned nblk = e->grid_y;
         void *fparams[] = {a.p, &nblk};
         tk = pgd_tbegin(PGD_T_JIT_FIN);
-        err = hipModuleLaunchKernel(e->ffin, e->fin_grid, 1, 1, 256, 1, 1, 0, s, fparams, NULL);
+        err = hipModuleLaunchKernel(e->ffin, e->fin_grid, 1, 1, 1024, 1, 1, 0, s, fparams, NULL);
         pgd_tend(tk);
     }
     if (err != hipSuccess) {

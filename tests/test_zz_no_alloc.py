@@ -101,9 +101,13 @@ def test_noalloc_gemm_other_shapes(lib, oracle, dt, m, n, k):
 
 
 def test_noalloc_gemm_refuses_beyond_the_workspace(lib):
-    """4096 x 2048 x 8192 splits its reduction in two: 64 MiB of partials,
-    above the 32 MiB workspace.  The call is refused and C is not written."""
-    m, n, k = 4096, 2048, 8192
+    """2048 x 2048 x 16384 splits its reduction in four: 64 MiB of
+    partials, above the 32 MiB workspace.  The call is refused and C is not
+    written."""
+    m, n, k = 2048, 2048, 16384
+    sp = C.c_int(0)
+    lib.pg_amd_gemm16_plan(0, 1, m, n, k, 1, 0, C.byref(sp), None)
+    assert sp.value * m * n * 4 > (32 << 20), "the planner no longer splits this shape"
     print(f"no-alloc gemm refusal m={m} n={n} k={k}", flush=True)
     nd, sh = _shape(m, k)
     ta = lib.pg_tensor_full_dtype(BF16, nd, sh, 1.0)
