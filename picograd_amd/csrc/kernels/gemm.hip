@@ -1062,7 +1062,7 @@ static gemm_plan plan_gemm(size_t m, size_t n, size_t kin, size_t batch, int cu_
         size_t bm, bn;
         double rate;
     };
-    static const shape shapes[3] = {{2, 256, 256, 4.4e12}, {3, 128, 256, 3.75e12}, {1, 128, 128, 2.6e12}};
+    static const shape shapes[3] = {{2, 256, 256, 4.4e12}, {3, 128, 256, 3.75e12}, {1, 128, 128, 2.0e12}};
     const double bw = 5.0e12, launch = 5e-6;
     gemm_plan best = {2, 1};
     double best_t = 1e300;
