@@ -1053,7 +1053,8 @@ static constexpr int kCUs = 256;
 // per CU (measured under a loaded chip), plus for a split its partials:
 // the slices write sp - 1 more tiles of C than one launch would, the sum
 // reads sp and writes one, at ~5 TB/s, and one more launch.  A split must
-// still win by 8 %: its partials also cost HBM capacity.
+// still win by 8 % over the best plan without one: its partials also cost
+// HBM capacity.
 static gemm_plan plan_gemm(size_t m, size_t n, size_t kin, size_t batch, int cu_budget = 0, double *time = nullptr)
 {
     const double cus = cu_budget > 0 && cu_budget < kCUs ? (double)cu_budget : (double)kCUs;
@@ -1077,7 +1078,7 @@ static gemm_plan plan_gemm(size_t m, size_t n, size_t kin, size_t batch, int cu_
             double t = rounds * 2.0 * (double)sh.bm * (double)sh.bn * (double)(sp > 1 ? ks : kin) / sh.rate;
             if (sp > 1)
                 t += 2.0 * (double)sp * (double)m * (double)n * 4.0 / bw + launch;
-            if (t < best_t * (sp > 1 ? 0.92 : 1.0)) {
+            if (t < best_t * (sp > 1 && best.sp == 1 ? 0.92 : 1.0)) {
                 best_t = t;
                 best.tile = sh.tile;
                 best.sp = sp;
