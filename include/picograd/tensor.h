@@ -36,6 +36,11 @@ typedef struct pg_data_ref {
     void *shadow;
     int shadow_dtype;  /* PG_DTYPE_F16 or PG_DTYPE_BF16 */
     bool shadow_stale; /* an in-place write happened after it was made */
+    /* rows of shadow_cols elements at a pitch of shadow_ld (zeros between),
+     * for a GEMM operand whose rows are not whole 16-byte pieces; 0: the
+     * elements in storage order */
+    size_t shadow_cols, shadow_ld;
+    size_t shadow_bytes; /* its allocation */
 } pg_data_ref;
 
 typedef struct pg_tensor {

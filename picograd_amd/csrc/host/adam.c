@@ -210,6 +210,8 @@ void pg_adam_step(pg_adam *opt)
         bool shadow = r && r->shadow && p->value->dev == r->ptr && p->value->numel * 4 == r->nbytes;
         q->shadow = shadow ? r->shadow : NULL;
         q->shadow_dtype = shadow ? r->shadow_dtype : 0;
+        q->shadow_cols = shadow ? r->shadow_cols : 0;
+        q->shadow_ld = shadow ? r->shadow_ld : 0;
         if (shadow)
             r->shadow_stale = false;
         else

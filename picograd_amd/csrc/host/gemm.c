@@ -551,8 +551,10 @@ static bool mm16_dims(const pg_tensor *a, const pg_tensor *b, size_t *M, size_t 
 }
 
 /* q(t) as a [rows_pad, cols_pad] matrix whose first rows x cols hold the
- * rounded elements: the shadow when no padding is needed, else a padded
- * copy returned in *owned (*bytes long) */
+ * rounded elements: the shadow when no padding is needed, the pitched
+ * shadow when only the rows are padded (cols_pad: whole 16-byte pieces)
+ * and t is its whole storage -- kept, and rewritten by the optimisers like
+ * the plain one -- else a padded copy returned in *owned (*bytes long) */
 static const uint16_t *operand16(pg_tensor *t, int dt, size_t rows, size_t cols, size_t rows_pad, size_t cols_pad,
                                  uint16_t **owned, size_t *bytes)
 {
@@ -560,6 +562,10 @@ static const uint16_t *operand16(pg_tensor *t, int dt, size_t rows, size_t cols,
     *bytes = 0;
     if (rows == rows_pad && cols == cols_pad)
         return pgt_shadow16(t, (pg_dtype)dt);
+    const pg_data_ref *r = t->data_ref;
+    if (rows == rows_pad && r && t->dev == r->ptr && t->numel == rows * cols && t->numel * 4 == r->nbytes &&
+        pgt_is_contiguous(t))
+        return pgt_shadow16_rows(t, (pg_dtype)dt, cols, cols_pad);
     *owned = stage16(dt, 0, t->dev, rows, cols, cols, rows_pad, cols_pad, 1, 0, bytes);
     return *owned;
 }
@@ -788,6 +794,7 @@ pg_node *pg_amd_ag_linear16(pg_node *x, pg_node *w, pg_node *b, int act, pg_dtyp
     if (ok && N % 8 == 0 && M * N) {
         pg_data_ref *r = out->data_ref;
         r->shadow = pgd_malloc(M * N * 2);
+        r->shadow_bytes = M * N * 2;
         r->shadow_dtype = dt;
         r->shadow_stale = true;
         ok = r->shadow != NULL;

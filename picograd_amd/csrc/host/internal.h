@@ -72,6 +72,10 @@ void pgt_materialize(pg_tensor *t);
  * (pgt_touch), rewritten by pg_sgd_step in the pass that updates the
  * elements.  NULL (device error set) on failure. */
 const uint16_t *pgt_shadow16(pg_tensor *t, pg_dtype dt);
+/* the same copy held as rows of `cols` elements at a pitch of `ld`
+ * (ld % 8 == 0: rows of whole 16-byte pieces) with zeros between, for a
+ * GEMM operand whose rows are not; the storage is whole rows of cols */
+const uint16_t *pgt_shadow16_rows(pg_tensor *t, pg_dtype dt, size_t cols, size_t ld);
 /* records an in-place write of t's elements: its shadow is stale */
 void pgt_touch(pg_tensor *t);
 /* t itself when contiguous, else a new contiguous tensor holding t's

@@ -131,6 +131,8 @@ void pg_sgd_step(pg_sgd *opt)
         bool shadow = r && r->shadow && p->value->dev == r->ptr && p->value->numel * 4 == r->nbytes;
         segs[ns].shadow = shadow ? r->shadow : NULL;
         segs[ns].shadow_dtype = shadow ? r->shadow_dtype : 0;
+        segs[ns].shadow_cols = shadow ? r->shadow_cols : 0;
+        segs[ns].shadow_ld = shadow ? r->shadow_ld : 0;
         if (shadow)
             r->shadow_stale = false;
         else

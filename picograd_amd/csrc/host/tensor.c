@@ -85,7 +85,7 @@ void pgt_ref_release(pg_data_ref *r)
     if (r && --r->refs == 0) {
         pgd_free(r->ptr, r->nbytes);
         if (r->shadow)
-            pgd_free(r->shadow, r->nbytes / 2);
+            pgd_free(r->shadow, r->shadow_bytes);
         free(r);
     }
 }
@@ -308,7 +308,18 @@ bool pg_amd_tensor_refresh16(pg_tensor *t)
     pg_data_ref *r = t->data_ref;
     if (!r->shadow || !r->shadow_stale)
         return true;
+    if (r->shadow_cols)
+        return pgt_shadow16_rows(t, (pg_dtype)r->shadow_dtype, r->shadow_cols, r->shadow_ld) != NULL;
     return pgt_shadow16(t, (pg_dtype)r->shadow_dtype) != NULL;
+}
+
+static void shadow_drop(pg_data_ref *r)
+{
+    if (r->shadow)
+        pgd_free(r->shadow, r->shadow_bytes);
+    r->shadow = NULL;
+    r->shadow_bytes = 0;
+    r->shadow_cols = r->shadow_ld = 0;
 }
 
 const uint16_t *pgt_shadow16(pg_tensor *t, pg_dtype dt)
@@ -319,16 +330,54 @@ const uint16_t *pgt_shadow16(pg_tensor *t, pg_dtype dt)
     }
     pg_data_ref *r = t->data_ref;
     size_t n = r->nbytes / 4;
+    if (r->shadow && r->shadow_cols)
+        shadow_drop(r); /* a pitched copy: remade in storage order */
     if (r->shadow && r->shadow_dtype == (int)dt && !r->shadow_stale)
         return r->shadow;
     if (!r->shadow) {
-        r->shadow = pgd_malloc(n ? n * 2 : 1);
+        const size_t bytes = n ? n * 2 : 1;
+        r->shadow = pgd_malloc(bytes);
         if (!r->shadow)
             return NULL;
+        r->shadow_bytes = bytes;
     }
     r->shadow_dtype = (int)dt;
     pgt_materialize(t);
     if (!pgd_check(pgk_cast_to16((int)dt, r->ptr, r->shadow, n, pgd_stream()), "shadow16"))
+        return NULL;
+    r->shadow_stale = false;
+    return r->shadow;
+}
+
+const uint16_t *pgt_shadow16_rows(pg_tensor *t, pg_dtype dt, size_t cols, size_t ld)
+{
+    if (ld == cols)
+        return pgt_shadow16(t, dt);
+    if (!t || !t->data_ref || t->dtype != PG_DTYPE_F32 || (dt != PG_DTYPE_F16 && dt != PG_DTYPE_BF16) || !cols ||
+        ld < cols || (t->data_ref->nbytes / 4) % cols) {
+        pgd_set_err("shadow16: needs an f32 tensor of whole rows and a 16-bit dtype");
+        return NULL;
+    }
+    pg_data_ref *r = t->data_ref;
+    if (r->shadow && (r->shadow_cols != cols || r->shadow_ld != ld))
+        shadow_drop(r);
+    if (r->shadow && r->shadow_dtype == (int)dt && !r->shadow_stale)
+        return r->shadow;
+    const size_t rows = r->nbytes / 4 / cols;
+    if (!r->shadow) {
+        const size_t bytes = rows * ld ? rows * ld * 2 : 1;
+        r->shadow = pgd_malloc(bytes);
+        if (!r->shadow)
+            return NULL;
+        r->shadow_bytes = bytes;
+        r->shadow_cols = cols;
+        r->shadow_ld = ld;
+    }
+    r->shadow_dtype = (int)dt;
+    pgt_materialize(t);
+    /* the pad columns are written as zeros here and never touched again */
+    if (!pgd_check(pgk_copy_to16((int)dt, 0, r->ptr, rows, cols, cols, r->shadow, ld, rows, 1, 0, 0, pgd_stream()),
+                   "shadow16"))
         return NULL;
     r->shadow_stale = false;
     return r->shadow;

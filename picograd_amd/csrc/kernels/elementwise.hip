@@ -571,8 +571,10 @@ __global__ void __launch_bounds__(kBlock) k_sgd(sgd_table tab, float lr, float m
     const pgk_sgd_seg sg = tab.seg[si];
     const size_t n = sg.n, base = (size_t)(blk - tab.first[si]) * kSgdChunk;
     const bool has_buf = sg.buf != nullptr;
+    // a pitched shadow takes the per-element path (its rows break the
+    // 4-element groups)
     const bool aligned = ((((uintptr_t)sg.p) | ((uintptr_t)sg.g) | ((uintptr_t)sg.buf)) & 15) == 0 &&
-                         (((uintptr_t)sg.shadow) & 7) == 0;
+                         (((uintptr_t)sg.shadow) & 7) == 0 && !sg.shadow_cols;
     if (aligned) {
         const bool full = base + kSgdChunk <= n;
         if (full && has_buf)
@@ -592,7 +594,7 @@ __global__ void __launch_bounds__(kBlock) k_sgd(sgd_table tab, float lr, float m
             if (has_buf)
                 sg.buf[j] = bj;
             if (sg.shadow)
-                sg.shadow[j] = to16(sg.shadow_dtype, pj);
+                sg.shadow[shadow_at(sg, j)] = to16(sg.shadow_dtype, pj);
         }
     }
 }

@@ -217,6 +217,9 @@ typedef struct {
     uint16_t *shadow; /* optional 16-bit copy of p written after the update */
     int shadow_dtype; /* 1 = f16, 2 = bf16 (RNE) */
     size_t n;
+    /* shadow_cols != 0: element j's copy at (j / shadow_cols) * shadow_ld +
+     * j % shadow_cols (rows padded to a pitch); 0: at j */
+    size_t shadow_cols, shadow_ld;
 } pgk_sgd_seg;
 int pgk_sgd_multi(const pgk_sgd_seg *segs, int nseg, float lr, float momentum, float dampening,
                   float weight_decay, int nesterov, pgk_stream s);
@@ -231,6 +234,7 @@ typedef struct {
     int shadow_dtype; /* 1 = f16, 2 = bf16 (RNE) */
     float lr, wd;     /* this tensor's learning rate and weight decay */
     size_t n;
+    size_t shadow_cols, shadow_ld; /* as pgk_sgd_seg's */
 } pgk_adam_seg;
 typedef struct {
     float beta1, beta2, eps;

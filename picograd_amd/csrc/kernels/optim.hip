@@ -73,8 +73,9 @@ __global__ void __launch_bounds__(kBlock) k_adam(adam_table tab, pgk_adam_hyper 
     float *__restrict__ M = sg.m;
     float *__restrict__ V = sg.v;
     float *__restrict__ VM = sg.vmax;
+    // a pitched shadow takes the per-element path
     const bool vec = ((((uintptr_t)P) | ((uintptr_t)G) | ((uintptr_t)M) | ((uintptr_t)V) | ((uintptr_t)VM)) & 15) == 0 &&
-                     (((uintptr_t)sg.shadow) & 7) == 0;
+                     (((uintptr_t)sg.shadow) & 7) == 0 && !sg.shadow_cols;
     if (vec) {
         float4 p[kAdamVec], g[kAdamVec], m[kAdamVec], v[kAdamVec], vm[kAdamVec];
         size_t e[kAdamVec];
@@ -126,7 +127,7 @@ __global__ void __launch_bounds__(kBlock) k_adam(adam_table tab, pgk_adam_hyper 
             if (ams)
                 VM[j] = vmj;
             if (sg.shadow)
-                sg.shadow[j] = to16(sg.shadow_dtype, pj);
+                sg.shadow[shadow_at(sg, j)] = to16(sg.shadow_dtype, pj);
         }
     }
 }

@@ -26,6 +26,18 @@ __device__ __forceinline__ int seg_of(const unsigned (&first)[MAX + 1], unsigned
     return (int)s;
 }
 
+// index of element j's 16-bit copy in a segment's shadow: rows of
+// shadow_cols elements at a pitch of shadow_ld when the shadow is pitched
+// (shadow_cols != 0), else j
+template <class SEG>
+__device__ __forceinline__ size_t shadow_at(const SEG &sg, size_t j)
+{
+    if (!sg.shadow_cols)
+        return j;
+    const size_t r = j / sg.shadow_cols;
+    return r * sg.shadow_ld + (j - r * sg.shadow_cols);
+}
+
 // host side: first[cnt .. MAX] = blocks
 template <int MAX>
 inline void seg_close(unsigned (&first)[MAX + 1], int cnt, unsigned blocks)

@@ -20,6 +20,7 @@ from pathlib import Path
 import numpy as np
 import pytest
 
+from oracle_lib import rel_fro
 from picograd_amd.capi import BF16, F16, F32
 from picograd_amd.mlp import ACT_NONE
 
@@ -111,7 +112,8 @@ def test_cast_kernel_decodes_every_pattern(lib, dt):
 
 class _DataRef(C.Structure):
     _fields_ = [("ptr", C.c_void_p), ("nbytes", C.c_size_t), ("refs", C.c_int), ("shadow", C.c_void_p),
-                ("shadow_dtype", C.c_int), ("shadow_stale", C.c_bool)]
+                ("shadow_dtype", C.c_int), ("shadow_stale", C.c_bool), ("shadow_cols", C.c_size_t),
+                ("shadow_ld", C.c_size_t), ("shadow_bytes", C.c_size_t)]
 
 
 def _read_kept16(lib, t, rows, cols, dt):
@@ -196,4 +198,55 @@ def test_sgd_rewrites_the_kept_copy_like_the_reference(lib, oracle, dt):
     assert np.array_equal(kept.view(np.uint32), _decoded(oracle, dt, w).view(np.uint32))
     lib.pg_sgd_free(opt)
     for n in (loss, y, x, nw):
+        lib.pg_node_free(n)
+
+
+@pytest.mark.parametrize("opt_kind", ["sgd", "adam"])
+@pytest.mark.parametrize("dt", [BF16, F16])
+def test_pitched_kept_copy_of_a_narrow_weight(lib, oracle, dt, opt_kind):
+    """A weight [64, 10] (rows not whole 16-byte pieces) used as a GEMM
+    operand keeps its 16-bit copy as rows at a pitch of 16 with zeros
+    between (no padded copy per call); the optimiser's update pass rewrites
+    it in that layout.  After a real step the copy must be the reference's
+    encoding of the updated weight, and the pad columns zero."""
+    from picograd_amd.capi import SgdCfg
+    K, N, LD = 64, 10, 16
+    rng = np.random.default_rng(dt * 7 + len(opt_kind))
+    w = (rng.standard_normal((K, N)) * 0.5).astype(np.float32)
+    nw = lib.var(w)
+    x = lib.var(rng.standard_normal((8, K)).astype(np.float32), requires_grad=False)
+    y = lib._check(lib.pg_amd_ag_matmul16(x, nw, dt))
+    ref = _DataRef.from_address(lib.tinfo(lib.node(nw).value).data_ref)
+    assert ref.shadow and ref.shadow_cols == N and ref.shadow_ld == LD and ref.shadow_bytes == K * LD * 2
+    loss = lib.op("sum_all", y)
+    if opt_kind == "sgd":
+        opt = lib.pg_sgd_new(C.byref(SgdCfg(0.05, 0.9, 0.0, 0.0, True)))
+        assert lib.pg_sgd_add_param(opt, nw) == 0
+    else:
+        cfg = lib.pg_adam_cfg_default()
+        cfg.lr = 0.05
+        opt = lib.pg_adam_new(C.byref(cfg))
+        assert lib.pg_adam_add_param(opt, nw) == 0
+    lib.pg_backward(loss)
+    (lib.pg_sgd_step if opt_kind == "sgd" else lib.pg_adam_step)(opt)
+    w1 = lib.value(nw)
+    assert not np.array_equal(w1, w)
+    ref = _DataRef.from_address(lib.tinfo(lib.node(nw).value).data_ref)
+    assert ref.shadow and not ref.shadow_stale and ref.shadow_cols == N and ref.shadow_ld == LD
+    # decode the [64, 16] pitched copy through an identity GEMM
+    e32 = lib.tensor(np.eye(LD, dtype=np.float32))
+    te = lib._check(lib.pg_amd_tensor_to_dtype(e32, dt))
+    tc = lib.pg_tensor_empty_dtype(F32, 2, (C.c_size_t * 2)(K, LD))
+    lib.pg_gemm_ex(dt, K, LD, LD, ref.shadow, LD, lib.tinfo(te).dev, LD, lib.tinfo(tc).dev, LD)
+    kept = lib.read(tc)
+    assert np.array_equal(kept[:, :N].view(np.uint32), _decoded(oracle, dt, w1).view(np.uint32))
+    assert np.all(kept[:, N:] == 0.0)
+    # the next forward reads the kept copy: it equals the oracle's product
+    y2 = lib._check(lib.pg_amd_ag_matmul16(x, nw, dt))
+    want = oracle.gemm(dt, oracle.cast16(dt, lib.value(x)), oracle.cast16(dt, w1))
+    assert rel_fro(lib.value(y2), want) <= 1e-5
+    for t in (e32, te, tc):
+        lib.pg_tensor_free(t)
+    (lib.pg_sgd_free if opt_kind == "sgd" else lib.pg_adam_free)(opt)
+    for n in (y2, loss, y, x, nw):
         lib.pg_node_free(n)
