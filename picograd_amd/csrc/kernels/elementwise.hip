@@ -387,8 +387,19 @@ __global__ void __launch_bounds__(kSumAll2sThreads) k_sum_all2s(const float *__r
         const int l0 = sl * slice_len, l1 = l0 + slice_len < rows ? l0 + slice_len : rows;
         const float *p = x + c;
         float acc = 0.0f;
-#pragma unroll 8
-        for (int l = l0; l < l1; ++l)
+        int l = l0;
+        // 32 loads in flight before their (ordered) adds: the walk is one
+        // lane's, so memory latency, not bandwidth, sets its pace
+        for (; l + 32 <= l1; l += 32) {
+            float v[32];
+#pragma unroll
+            for (int q = 0; q < 32; ++q)
+                v[q] = p[(size_t)(l + q) * cols];
+#pragma unroll
+            for (int q = 0; q < 32; ++q)
+                acc += v[q];
+        }
+        for (; l < l1; ++l)
             acc += p[(size_t)l * cols];
         part[t] = acc;
     }
@@ -711,6 +722,59 @@ __global__ void __launch_bounds__(kBlock) k_act_bwd16(const float *__restrict__ 
                 part[(size_t)blockIdx.y * n + col] = sum;
         }
     }
+}
+
+// The same pass in one block of 1024 lanes for a small [m, n] (config 5's
+// [4096, 10] output layer): lane (rl, c) takes column c of rows rl,
+// rl + RL, ... (RL = 1024 / ldd row lanes), 16 loads in flight before the
+// products, writes dz's 16-bit element (zeros in the pad columns) and adds
+// its column sum in row order; the RL partials of a column are then added
+// by a fixed pairwise tree and written to db (+= with beta).  One launch in
+// place of k_act_bwd16 + k_colsum_fin.
+constexpr int kActSmallLanes = 1024;
+template <int ACT>
+__global__ void __launch_bounds__(kActSmallLanes) k_act_bwd16_small(const float *__restrict__ g,
+                                                                   const float *__restrict__ z, int m, int n,
+                                                                   uint16_t *__restrict__ d16, int ldd, int dtype,
+                                                                   float *__restrict__ db, int beta)
+{
+    __shared__ float red[kActSmallLanes];
+    const int t = threadIdx.x, c = t % ldd, rl = t / ldd, RL = kActSmallLanes / ldd;
+    float acc = 0.0f;
+    int r = rl;
+    for (; r + 15 * RL < m; r += 16 * RL) {
+        float gv[16], zv[16];
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            const size_t off = (size_t)(r + q * RL) * n + c;
+            gv[q] = c < n ? g[off] : 0.0f;
+            zv[q] = (ACT && c < n) ? z[off] : 0.0f;
+        }
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            const float d = ACT ? gv[q] * act_grad(ACT, zv[q]) : gv[q];
+            acc += d;
+            d16[(size_t)(r + q * RL) * ldd + c] = to16(dtype, d);
+        }
+    }
+    for (; r < m; r += RL) {
+        const size_t off = (size_t)r * n + c;
+        const float gv = c < n ? g[off] : 0.0f;
+        const float d = ACT ? gv * act_grad(ACT, (c < n) ? z[off] : 0.0f) : gv;
+        acc += d;
+        d16[(size_t)r * ldd + c] = to16(dtype, d);
+    }
+    if (!db)
+        return;
+    red[t] = acc;
+    __syncthreads();
+    for (int h = RL / 2; h > 0; h >>= 1) {
+        if (rl < h)
+            red[t] += red[t + h * ldd];
+        __syncthreads();
+    }
+    if (rl == 0 && c < n)
+        db[c] = beta ? db[c] + red[c] : red[c];
 }
 
 __global__ void __launch_bounds__(64) k_colsum_fin(const float *__restrict__ part, size_t nblk, size_t n,
@@ -1109,6 +1173,20 @@ extern "C" int pgk_act_bwd16(int act, const float *g, const float *z, size_t m, 
         return 0;
     if ((ldd & 7) || ldd < n || (((uintptr_t)d16) & 15) || (act && !z) || (db && !ws) || act < 0 || act > 2)
         return (int)hipErrorInvalidValue;
+    if (m * ldd <= ((size_t)1 << 16) && kActSmallLanes % ldd == 0) {
+        // small: one block does the pass and the column sums
+        const dim3 g1(1), b1(kActSmallLanes);
+        if (act == 0)
+            hipLaunchKernelGGL(k_act_bwd16_small<0>, g1, b1, 0, (hipStream_t)s, g, z, (int)m, (int)n, d16, (int)ldd,
+                               dtype, db, db_beta);
+        else if (act == 1)
+            hipLaunchKernelGGL(k_act_bwd16_small<1>, g1, b1, 0, (hipStream_t)s, g, z, (int)m, (int)n, d16, (int)ldd,
+                               dtype, db, db_beta);
+        else
+            hipLaunchKernelGGL(k_act_bwd16_small<2>, g1, b1, 0, (hipStream_t)s, g, z, (int)m, (int)n, d16, (int)ldd,
+                               dtype, db, db_beta);
+        return status();
+    }
     const size_t rpb = act_bwd_rpb(m, ldd), nrb = (m + rpb - 1) / rpb;
     if (nrb > 65535)
         return (int)hipErrorInvalidValue;
