@@ -724,59 +724,6 @@ __global__ void __launch_bounds__(kBlock) k_act_bwd16(const float *__restrict__ 
     }
 }
 
-// The same pass in one block of 1024 lanes for a small [m, n] (config 5's
-// [4096, 10] output layer): lane (rl, c) takes column c of rows rl,
-// rl + RL, ... (RL = 1024 / ldd row lanes), 16 loads in flight before the
-// products, writes dz's 16-bit element (zeros in the pad columns) and adds
-// its column sum in row order; the RL partials of a column are then added
-// by a fixed pairwise tree and written to db (+= with beta).  One launch in
-// place of k_act_bwd16 + k_colsum_fin.
-constexpr int kActSmallLanes = 1024;
-template <int ACT>
-__global__ void __launch_bounds__(kActSmallLanes) k_act_bwd16_small(const float *__restrict__ g,
-                                                                   const float *__restrict__ z, int m, int n,
-                                                                   uint16_t *__restrict__ d16, int ldd, int dtype,
-                                                                   float *__restrict__ db, int beta)
-{
-    __shared__ float red[kActSmallLanes];
-    const int t = threadIdx.x, c = t % ldd, rl = t / ldd, RL = kActSmallLanes / ldd;
-    float acc = 0.0f;
-    int r = rl;
-    for (; r + 15 * RL < m; r += 16 * RL) {
-        float gv[16], zv[16];
-#pragma unroll
-        for (int q = 0; q < 16; ++q) {
-            const size_t off = (size_t)(r + q * RL) * n + c;
-            gv[q] = c < n ? g[off] : 0.0f;
-            zv[q] = (ACT && c < n) ? z[off] : 0.0f;
-        }
-#pragma unroll
-        for (int q = 0; q < 16; ++q) {
-            const float d = ACT ? gv[q] * act_grad(ACT, zv[q]) : gv[q];
-            acc += d;
-            d16[(size_t)(r + q * RL) * ldd + c] = to16(dtype, d);
-        }
-    }
-    for (; r < m; r += RL) {
-        const size_t off = (size_t)r * n + c;
-        const float gv = c < n ? g[off] : 0.0f;
-        const float d = ACT ? gv * act_grad(ACT, (c < n) ? z[off] : 0.0f) : gv;
-        acc += d;
-        d16[(size_t)r * ldd + c] = to16(dtype, d);
-    }
-    if (!db)
-        return;
-    red[t] = acc;
-    __syncthreads();
-    for (int h = RL / 2; h > 0; h >>= 1) {
-        if (rl < h)
-            red[t] += red[t + h * ldd];
-        __syncthreads();
-    }
-    if (rl == 0 && c < n)
-        db[c] = beta ? db[c] + red[c] : red[c];
-}
-
 __global__ void __launch_bounds__(64) k_colsum_fin(const float *__restrict__ part, size_t nblk, size_t n,
                                                    float *__restrict__ out, int beta)
 {
@@ -1173,20 +1120,6 @@ extern "C" int pgk_act_bwd16(int act, const float *g, const float *z, size_t m, 
         return 0;
     if ((ldd & 7) || ldd < n || (((uintptr_t)d16) & 15) || (act && !z) || (db && !ws) || act < 0 || act > 2)
         return (int)hipErrorInvalidValue;
-    if (m * ldd <= ((size_t)1 << 16) && kActSmallLanes % ldd == 0) {
-        // small: one block does the pass and the column sums
-        const dim3 g1(1), b1(kActSmallLanes);
-        if (act == 0)
-            hipLaunchKernelGGL(k_act_bwd16_small<0>, g1, b1, 0, (hipStream_t)s, g, z, (int)m, (int)n, d16, (int)ldd,
-                               dtype, db, db_beta);
-        else if (act == 1)
-            hipLaunchKernelGGL(k_act_bwd16_small<1>, g1, b1, 0, (hipStream_t)s, g, z, (int)m, (int)n, d16, (int)ldd,
-                               dtype, db, db_beta);
-        else
-            hipLaunchKernelGGL(k_act_bwd16_small<2>, g1, b1, 0, (hipStream_t)s, g, z, (int)m, (int)n, d16, (int)ldd,
-                               dtype, db, db_beta);
-        return status();
-    }
     const size_t rpb = act_bwd_rpb(m, ldd), nrb = (m + rpb - 1) / rpb;
     if (nrb > 65535)
         return (int)hipErrorInvalidValue;
