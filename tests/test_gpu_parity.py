@@ -178,14 +178,17 @@ def dbias_bound(rdx: np.ndarray, depth: int = 128) -> np.ndarray:
 
 
 @pytest.mark.parametrize("R,Cc", [(512, 1024), (37, 515), (1, 8), (1000, 4), (4096, 64), (4000, 64),
-                                  (3000, 63)])
+                                  (3000, 63), (24000, 64), (33001, 63)])
 @pytest.mark.parametrize("jit", [True, False])
 def test_chain2_broadcast_grads_match_oracle(lib, oracle, R, Cc, jit):
     """Config 2 at reduced size: y = gelu(x + bias) * sigmoid(g), dbias is a
-    column sum over R rows fused into the backward kernel.  (4096, 64),
-    (4000, 64) and (3000, 63) leave one column block, so the fused kernel
-    writes 256, 250 and 188 partial rows: the finisher's eight-deep loop runs
-    (once or twice per lane), as at config 2's full shape (1024 rows)."""
+    column sum over R rows fused into the backward kernel.  The narrow
+    shapes leave one column block, so the fused kernel writes one partial
+    row per 16-row band: 256, 250 and 188 rows take only the finisher's
+    one-row loop (each of its 128 block lanes adds every 128th row); 1500
+    and 2063 rows also take its eight-deep loop (once or twice per lane, then
+    the one-row loop), as config 2's full shape does (1024 rows, eight per
+    lane); (33001, 63) also ends on a partial band."""
     oracle.orc_seed(43)
     x = oracle.normal(R * Cc, 0.0, 1.0).reshape(R, Cc)
     bias = oracle.normal(Cc, 0.0, 0.1)
