@@ -678,7 +678,7 @@ splitk_desc splitk_of(const float *part, int splits, size_t m, size_t n, float *
 {
     int v4 = ((n | (ldc & 3)) & 3) == 0 && (((uintptr_t)c | (uintptr_t)part) & 15) == 0;
     if (epi)
-        v4 = v4 && (((uintptr_t)epi->z) & 15) == 0 && (((uintptr_t)epi->c16) & 7) == 0;
+        v4 = v4 && ((((uintptr_t)epi->z) | ((uintptr_t)epi->bias)) & 15) == 0 && (((uintptr_t)epi->c16) & 7) == 0;
     return splitk_desc{part, splits, (int)m, (int)n, c, ldc, beta, v4, epi != nullptr, epi ? *epi : pgk_epi{}};
 }
 
