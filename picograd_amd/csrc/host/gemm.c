@@ -131,6 +131,28 @@ static bool gemm16(int dt, int ta, int tb, size_t m, size_t n, size_t k, const u
     return gemm16x(dt, ta, tb, m, n, k, a, lda, sa, aext, b, ldb, sb, bext, c, ldc, sc, batch, beta, NULL, what);
 }
 
+/* A matmul's dgrad and wgrad as ONE launch on the whole chip (the paired
+ * kernel, both halves planned for all 256 CUs) when both plan 256 x 256
+ * tiles without split-K: one launch boundary less, and the second problem's
+ * first blocks start on the CUs the first leaves free while its last tiles
+ * drain.  Measured 434 against 438 us for config 3's pair and 212 against
+ * 215 us for a 4096^3 pair.  False (nothing launched) otherwise. */
+static bool pair_full(int dt, const pgk_gemm_desc *dd, const pgk_gemm_desc *dw, const char *what)
+{
+    int sd = 0, sw = 0;
+    if (!dd->m || !dd->n || !dd->k || !dd->batch || !dw->m || !dw->n || !dw->k || !dw->batch)
+        return false;
+    if (pgk_gemm16_plan(0, 0, dd->m, dd->n, dd->k, dd->batch, 0, &sd) != 2 || sd != 1 ||
+        pgk_gemm16_plan(1, 1, dw->m, dw->n, dw->k, dw->batch, 0, &sw) != 2 || sw != 1 || dd->k % 8)
+        return false;
+    int tk = pgd_tbegin(PGD_T_GEMM16);
+    int rc = pgk_gemm16_pair_dw(dt, dd, dw, 0, NULL, pgd_stream());
+    pgd_tend(tk);
+    if (rc == PGK_GEMM_NOT_PAIRED) /* excluded by the checks above */
+        return false;
+    return pgd_check(rc, what);
+}
+
 /* 16-bit copy of `rows x cols` (leading dim lds, `batch` matrices `sstride`
  * apart) padded with zeros to rows_pad x cols_pad; src_dtype 0 casts f32 */
 static uint16_t *stage16(int dt, int src_dtype, const void *src, size_t rows, size_t cols, size_t lds,
@@ -359,6 +381,18 @@ void pgm_matmul_backward(pg_node *n)
             if (side) {
                 pd.cus = best_cus;
                 pw = (gemm_place){side, 5, 256 - best_cus, false};
+            }
+        } else {
+            pgk_gemm_desc dd = {M, K, N8, g16, N8, M * N8, M, wp, N8, s.bbat ? K * N8 : 0, K, ga->dev, K, M * K, B, ba};
+            pgk_gemm_desc dw = {K, N, Mw, ap, lda_w, sa_w, lda_w, g16, N8, Mw * N8, N8, gb->dev, N,
+                                s.bbat ? K * N : 0, Bw, bbeta};
+            if (pair_full(dt, &dd, &dw, "dgrad + wgrad")) {
+                if (wpad)
+                    pgd_free(wpad, wbytes);
+                if (apad)
+                    pgd_free(apad, abytes);
+                pgd_free(g16, gbytes);
+                return;
             }
         }
     }
@@ -724,28 +758,28 @@ void pgm_linear16_backward(pg_node *n)
                                       dbeta, ws, pgd_stream()),
                         "linear16 act backward");
     pgd_tend(tk);
-    if (ok && K && px->requires_grad) {
-        int beta;
-        pg_tensor *gx = pga_grad_for_write(px, &beta);
-        uint16_t *own;
-        size_t ob;
-        const uint16_t *qw = operand16(w, dt, K, N, K, N8, &own, &ob);
-        if (gx && qw)
-            gemm16(dt, 0, 0, M, K, N8, dz16, N8, 0, M, qw, N8, 0, K, gx->dev, K, 0, 1, beta, "linear16 dgrad");
-        if (own)
-            pgd_free(own, ob);
+    /* each grad taken for writing once (that clears a pending zero and
+     * fixes beta), then both GEMMs as one whole-chip launch when they pair,
+     * else one after the other */
+    int bx = 0, bw = 0;
+    pg_tensor *gx = ok && K && px->requires_grad ? pga_grad_for_write(px, &bx) : NULL;
+    pg_tensor *gw = ok && K && pw->requires_grad ? pga_grad_for_write(pw, &bw) : NULL;
+    uint16_t *ow = NULL, *ox = NULL;
+    size_t obw = 0, obx = 0;
+    const uint16_t *qw = gx ? operand16(w, dt, K, N, K, N8, &ow, &obw) : NULL;
+    const uint16_t *qx = gw ? operand16(x, dt, M, K, M, K8, &ox, &obx) : NULL;
+    const pgk_gemm_desc dd = {M, K, N8, dz16, N8, 0, M, qw, N8, 0, K, gx ? gx->dev : NULL, K, 0, 1, bx};
+    const pgk_gemm_desc dw = {K, N, M, qx, K8, 0, K8, dz16, N8, 0, N8, gw ? gw->dev : NULL, N, 0, 1, bw};
+    if (!(qw && qx && pair_full(dt, &dd, &dw, "linear16 dgrad + wgrad"))) {
+        if (qw)
+            gemm16(dt, 0, 0, M, K, N8, dz16, N8, 0, M, qw, N8, 0, K, gx->dev, K, 0, 1, bx, "linear16 dgrad");
+        if (qx)
+            gemm16(dt, 1, 1, K, N, M, qx, K8, 0, K8, dz16, N8, 0, N8, gw->dev, N, 0, 1, bw, "linear16 wgrad");
     }
-    if (ok && K && pw->requires_grad) {
-        int beta;
-        pg_tensor *gw = pga_grad_for_write(pw, &beta);
-        uint16_t *own;
-        size_t ob;
-        const uint16_t *qx = operand16(x, dt, M, K, M, K8, &own, &ob);
-        if (gw && qx)
-            gemm16(dt, 1, 1, K, N, M, qx, K8, 0, K8, dz16, N8, 0, N8, gw->dev, N, 0, 1, beta, "linear16 wgrad");
-        if (own)
-            pgd_free(own, ob);
-    }
+    if (ow)
+        pgd_free(ow, obw);
+    if (ox)
+        pgd_free(ox, obx);
     pgd_free(dz16, dzb);
 }
 

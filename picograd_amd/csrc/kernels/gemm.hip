@@ -1267,7 +1267,7 @@ extern "C" size_t pgk_gemm16_pair_dw_workspace(const pgk_gemm_desc *d, const pgk
 extern "C" int pgk_gemm16_pair_dw(int dtype, const pgk_gemm_desc *d, const pgk_gemm_desc *w, int cu_d, void *ws,
                                   pgk_stream s)
 {
-    if (cu_d <= 0 || cu_d >= kCUs || !d->m || !d->n || !d->batch || !w->m || !w->n || !w->batch || !d->k || !w->k)
+    if (cu_d < 0 || cu_d >= kCUs || !d->m || !d->n || !d->batch || !w->m || !w->n || !w->batch || !d->k || !w->k)
         return PGK_GEMM_NOT_PAIRED;
     int bad = check_gemm_args(0, 0, d->m, d->n, d->k, d->a, d->lda, d->stride_a, d->a_extent, d->b, d->ldb,
                               d->stride_b, d->b_extent, d->batch);

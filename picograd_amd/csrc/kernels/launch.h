@@ -180,7 +180,8 @@ typedef struct {
  * (both MN-contiguous: ta = tb = 1) in ONE launch, d planned for cu_d CUs
  * and w for the rest, each split along k as its plan says (one more launch
  * then adds both problems' slices): the two run side by side with no second
- * stream.
+ * stream.  cu_d = 0 plans both for the whole chip: d's blocks, then w's,
+ * in one grid of several rounds.
  * PGK_GEMM_NOT_PAIRED (nothing launched) when one launch cannot hold the
  * pair: a k that needs a zero-padded tail launch, or the plans choose
  * different tile sizes.  ws: pgk_gemm16_pair_dw_workspace bytes. */
