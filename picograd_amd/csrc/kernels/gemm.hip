@@ -99,7 +99,11 @@ __device__ __forceinline__ void dma16(const void *src, LDS uint4 *dst)
 // per-lane byte offset: the form for k-tiles that lie wholly below the end
 // of the reduction dim, whose per-lane offsets stay fixed from tile to tile
 // (only the scalar base moves), so the loop spends no vector ALU work on
-// addresses.  `sbase` must be wave-uniform.
+// addresses.  `sbase` must be wave-uniform and the compiler must keep it in
+// SGPRs: if a change to the kernel leads it to compute the base in VGPRs,
+// the assembler rejects the instruction and the build fails.  (Forcing it
+// with v_readfirstlane costs two VALU ops per load in the k-loop; when doing
+// so, zero-extend each 32-bit half: the builtin returns a signed int.)
 __device__ __forceinline__ void dma16s(uint32_t voff, const void *sbase, LDS uint4 *dst)
 {
     const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)dst);
