@@ -103,29 +103,30 @@ def test_big_tile_fused_epilogue(lib, oracle, dt):
         lib.pg_node_free(n)
 
 
-def test_whole_chip_pair_accumulates(lib, oracle):
-    """A matmul whose dgrad and wgrad each fill the chip (4096^3 bf16: 256
+@pytest.mark.parametrize("dt", [BF16, F16])
+def test_whole_chip_pair_accumulates(lib, oracle, dt):
+    """A matmul whose dgrad and wgrad each fill the chip (4096^3 bf16 or f16: 256
     tiles of 256 x 256 each) runs both as one paired launch; used twice with
     two upstream grads, the second backward accumulates into both grads
     (beta = 1).  dX = q(G1).W^T + q(G2).W^T and dW = X^T.q(G1) + X^T.q(G2)
     against the oracle on sampled rows and columns; a repeat reproduces every
     bit."""
     n = 4096
-    print("whole-chip dgrad + wgrad pair, 4096^3 bf16, used twice (beta = 1)", flush=True)
+    print(f"whole-chip dgrad + wgrad pair, 4096^3 dt={dt}, used twice (beta = 1)", flush=True)
     rng = np.random.default_rng(4096)
-    x16 = oracle.cast16(BF16, rng.standard_normal((n, n)).astype(np.float32))
-    w16 = oracle.cast16(BF16, (0.02 * rng.standard_normal((n, n))).astype(np.float32))
-    g1 = oracle.cast16(BF16, rng.standard_normal((n, n)).astype(np.float32))
-    g2 = oracle.cast16(BF16, rng.standard_normal((n, n)).astype(np.float32))
+    x16 = oracle.cast16(dt, rng.standard_normal((n, n)).astype(np.float32))
+    w16 = oracle.cast16(dt, (0.02 * rng.standard_normal((n, n))).astype(np.float32))
+    g1 = oracle.cast16(dt, rng.standard_normal((n, n)).astype(np.float32))
+    g2 = oracle.cast16(dt, rng.standard_normal((n, n)).astype(np.float32))
     for ta in (0, 1):  # both plan 256 x 256 tiles without split-K: the pair launch
         sp, sec = C.c_int(0), C.c_double(0.0)
         assert lib.pg_amd_gemm16_plan(ta, ta, n, n, n, 1, 0, C.byref(sp), C.byref(sec)) == 2 and sp.value == 1
 
     def run():
-        nx, nw = lib.var(x16, dtype=BF16), lib.var(w16, dtype=BF16)
+        nx, nw = lib.var(x16, dtype=dt), lib.var(w16, dtype=dt)
         c1, c2 = lib.op("matmul", nx, nw), lib.op("matmul", nx, nw)
-        ng1 = lib.var(_to_f32(BF16, g1), requires_grad=False)
-        ng2 = lib.var(_to_f32(BF16, g2), requires_grad=False)
+        ng1 = lib.var(_to_f32(dt, g1), requires_grad=False)
+        ng2 = lib.var(_to_f32(dt, g2), requires_grad=False)
         p1, p2 = lib.op("mul", c1, ng1), lib.op("mul", c2, ng2)
         s1, s2 = lib.op("sum_all", p1), lib.op("sum_all", p2)
         loss = lib.op("add", s1, s2)
@@ -138,11 +139,11 @@ def test_whole_chip_pair_accumulates(lib, oracle):
     dx, dw = run()
     rows = np.array([0, 1, 255, 256, 2047, 2048, 4095])
     cols = np.array([0, 255, 256, 3000, 4095])
-    gx = lambda g, r: oracle.gemm(BF16, np.ascontiguousarray(g[r]), w16, tb=True, threads=16)  # noqa: E731
+    gx = lambda g, r: oracle.gemm(dt, np.ascontiguousarray(g[r]), w16, tb=True, threads=16)  # noqa: E731
     assert rel_fro(dx[rows], gx(g1, rows) + gx(g2, rows)) <= 1e-5
-    gw = lambda g, k: oracle.gemm(BF16, np.ascontiguousarray(x16[:, k]), g, ta=True, threads=16)  # noqa: E731
+    gw = lambda g, k: oracle.gemm(dt, np.ascontiguousarray(x16[:, k]), g, ta=True, threads=16)  # noqa: E731
     assert rel_fro(dw[rows], gw(g1, rows) + gw(g2, rows)) <= 1e-5
-    gwc = lambda g: oracle.gemm(BF16, x16, np.ascontiguousarray(g[:, cols]), ta=True, threads=16)  # noqa: E731
+    gwc = lambda g: oracle.gemm(dt, x16, np.ascontiguousarray(g[:, cols]), ta=True, threads=16)  # noqa: E731
     assert rel_fro(dw[:, cols], gwc(g1) + gwc(g2)) <= 1e-5
     dx2, dw2 = run()
     assert np.array_equal(dx2, dx) and np.array_equal(dw2, dw)
