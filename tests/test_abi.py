@@ -204,7 +204,7 @@ def _plan(lib, ta, tb, m, n, k, batch=1, cus=0):
 def test_gemm_launch_plans_of_the_configs():
     """The MFMA GEMM planner's choices for the configs' GEMMs (host logic):
     256 x 256 tiles where they fill the chip (config 3, config 5's 4096-wide
-    layers), the 128 x 256 tile for config 4's ragged grads on their shares
+    layers: their dgrad and wgrad then pair in one launch), the 128 x 256 tile for config 4's ragged grads on their shares
     of the chip (160 CUs for dgrad, 96 for wgrad: both then run without
     split-K, in one launch), 128 x 256 tiles split two ways for config 5's
     first-layer wgrad and split-K over 128 x 128 tiles for its 10-wide
@@ -213,6 +213,10 @@ def test_gemm_launch_plans_of_the_configs():
     assert _plan(lib, 0, 0, 8192, 4096, 4096) == (2, 1)    # config 3 dgrad
     assert _plan(lib, 1, 1, 4096, 4096, 8192) == (2, 1)    # config 3 wgrad
     assert _plan(lib, 0, 1, 4096, 4096, 4096) == (2, 1)    # config 5 forward
+    # config 5's 4096-wide dgrad and wgrad: both 256 x 256 without split-K,
+    # so the backward runs them as one whole-chip paired launch (as config 3)
+    assert _plan(lib, 0, 0, 4096, 4096, 4096) == (2, 1)
+    assert _plan(lib, 1, 1, 4096, 4096, 4096) == (2, 1)
     assert _plan(lib, 1, 1, 1024, 4096, 4096) == (3, 2)    # config 5 first-layer wgrad
     assert _plan(lib, 0, 1, 4096, 10, 4096) == (1, 8)      # config 5 10-wide forward
     assert _plan(lib, 0, 0, 4097, 1000, 3000, cus=160) == (3, 1)  # config 4 dgrad
