@@ -97,6 +97,22 @@ bool pg_amd_tensor_refresh16(pg_tensor *t);
  * Returns NULL (pg_autograd_last_error) for bad shapes, dtype or act. */
 pg_node *pg_amd_ag_linear16(pg_node *x, pg_node *w, pg_node *b, int act, pg_dtype dtype);
 
+/* Read access to what a linear16 node's backward works from, for checking
+ * the fused activation backward against a CPU model (no counterpart in the
+ * reference, whose fused GEMM has no backward):
+ *  - pg_amd_linear16_preact: the kept pre-activation z = q(x).q(W) + b
+ *    (f32 [M, N]), or NULL for act PG_ACT_NONE or a node built without
+ *    grads.  Borrowed: valid while the node lives.
+ *  - pg_amd_linear16_keep_dz(true): from then on each linear16 backward
+ *    keeps the 16-bit dz it computed, q(dout * act'(z)) as [M, N8] with
+ *    N8 = N rounded up to 8 (zero columns past N), on its node, replacing
+ *    the previous one, instead of freeing it (costs M * N8 * 2 bytes per
+ *    node until the node is freed).  pg_amd_linear16_dz returns it
+ *    (borrowed; PG_DTYPE_BF16 or F16 bits), or NULL. */
+const pg_tensor *pg_amd_linear16_preact(const pg_node *n);
+void pg_amd_linear16_keep_dz(bool keep);
+const pg_tensor *pg_amd_linear16_dz(const pg_node *n);
+
 /* JIT compile statistics: programs compiled by hiprtc, and cache lookups
  * that found a loaded kernel. */
 size_t pg_amd_jit_compiles(void);

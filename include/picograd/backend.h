@@ -36,11 +36,12 @@ void pg_bgemm(size_t m, size_t n, size_t k, const uint16_t *a, size_t lda, const
  * process, instead of the library allocator.  A call whose buffers exceed
  * it is rejected.  Calls share the workspace: they are ordered on the
  * library stream, and calls overlapping on one device from two host
- * threads would race.  Work other calls left queued in the library (batched
- * uploads, deferred elementwise ops) is launched first, as by any entry
- * point.  Returns 0, or -1 with pg_amd_last_error() set (library not
- * initialised by pg_amd_init, bad arguments, workspace too small, launch
- * failure). */
+ * threads would race.  Work other calls left waiting to be queued (batched
+ * uploads, deferred elementwise ops: queueing them may compile, allocate or
+ * wait) makes the call fail instead; pg_amd_sync() queues it.  Returns 0,
+ * or -1 with pg_amd_last_error() set (library not initialised by
+ * pg_amd_init, such work pending, bad arguments, workspace too small,
+ * launch failure). */
 int pg_amd_gemm_ex_noalloc(pg_dtype dtype, size_t m, size_t n, size_t k, const void *a, size_t lda,
                            const void *b, size_t ldb, float *c, size_t ldc);
 

@@ -178,6 +178,9 @@ _AMD_PROTOS = {
     "pg_amd_backward_from": (None, [vp, vp]),
     "pg_amd_ag_matmul16": (vp, [vp, vp, ip]),
     "pg_amd_ag_linear16": (vp, [vp, vp, vp, ip, ip]),
+    "pg_amd_linear16_preact": (vp, [vp]),
+    "pg_amd_linear16_keep_dz": (None, [bo]),
+    "pg_amd_linear16_dz": (vp, [vp]),
     "pg_amd_tensor_modified": (None, [vp]),
     "pg_amd_tensor_refresh16": (bo, [vp]),
     "pg_amd_tensor_to_dtype": (vp, [vp, ip]),

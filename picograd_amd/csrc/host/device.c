@@ -74,6 +74,10 @@ int pg_amd_init(void)
 
 bool pgd_initialised(void) { return g_init_state > 0; }
 
+static int g_up_n;
+
+bool pgd_work_pending(void) { return g_up_n > 0 || pga_lazy_pending(); }
+
 bool pgd_ok(void) { return pg_amd_init() == 0; }
 
 static bool up_flush(void);
@@ -286,8 +290,6 @@ static int g_stage_state; /* 0 = not tried, 1 = ok, -1 = unavailable */
 static int g_up_slot;
 static size_t g_up_off;
 static pgk_upload g_up[PGK_UPLOAD_MAX];
-static int g_up_n;
-
 static bool stage_ready(void)
 {
     if (g_stage_state)

@@ -336,6 +336,11 @@ void pgm_matmul_backward(pg_node *n)
         ap = apad = stage16(dt, dt, a->dev, a_rows, K, K, a_rows, K8, 1, 0, &abytes);
     size_t lda_w = K8 != K ? K8 : K, sa_w = (s.abat && !fold) ? M * K8 : 0;
     bool d_one = ga && wp && (s.abat || B == 1), w_one = gb && ap && (s.bbat || Bw == 1);
+    /* x.x (one node on both sides) has ONE grad: dgrad writes it with the
+     * beta taken first, wgrad then adds to it (beta 1), so the two run in
+     * that order on the main stream -- never side by side in one launch or
+     * on two streams, where wgrad's blocks would read what dgrad's write */
+    const bool alias = ga && gb && (ga == gb || ga->data_ref == gb->data_ref);
 
     /* When each GEMM alone would leave CUs idle (the bmm grads of config 4:
      * 128 blocks each), run the two side by side, each planned for its share
@@ -344,7 +349,7 @@ void pgm_matmul_backward(pg_node *n)
      * run one after the other on the whole chip. */
     gemm_place pd = PLACE_MAIN, pw = PLACE_MAIN;
     int tk = -1;
-    if (d_one && w_one) {
+    if (d_one && w_one && !alias) {
         double td = pgk_gemm16_time(0, 0, M, K, N8, B, 0), tw = pgk_gemm16_time(1, 1, K, N, Mw, Bw, 0);
         double best = 0.85 * (td + tw);
         int best_cus = 0;
@@ -377,7 +382,11 @@ void pgm_matmul_backward(pg_node *n)
                 pgd_free(g16, gbytes);
                 return;
             }
-            pgk_stream side = pgd_fork();
+            /* the side stream's scratch (slot 5) is sized before the fork:
+             * growing it afterwards would reuse a freed block in main-stream
+             * order, which the side stream does not follow */
+            size_t w5 = pgk_gemm16_workspace_cu(1, 1, K, N, Mw, Bw, 256 - best_cus);
+            pgk_stream side = !w5 || pgd_scratch(5, w5) ? pgd_fork() : NULL;
             if (side) {
                 pd.cus = best_cus;
                 pw = (gemm_place){side, 5, 256 - best_cus, false};
@@ -396,16 +405,7 @@ void pgm_matmul_backward(pg_node *n)
             }
         }
     }
-    if (gb && ap) {
-        if (w_one) {
-            gemm16p(&pw, dt, 1, 1, K, N, Mw, ap, lda_w, sa_w, lda_w, g16, N8, Mw * N8, N8, gb->dev, N,
-                    s.bbat ? K * N : 0, Bw, bbeta, NULL, "wgrad");
-        } else {
-            for (size_t z = 0; z < Bw; z++)
-                gemm16(dt, 1, 1, K, N, Mw, ap + z * sa_w, lda_w, 0, lda_w, g16 + z * Mw * N8, N8, 0, N8, gb->dev, N,
-                       0, 1, z == 0 ? bbeta : 1, "wgrad");
-        }
-    }
+    /* dgrad first: with one grad for both (x.x) it holds the first beta */
     if (ga && wp) {
         if (d_one) {
             gemm16p(&pd, dt, 0, 0, M, K, N8, g16, N8, M * N8, M, wp, N8, s.bbat ? K * N8 : 0, K, ga->dev, K, M * K, B,
@@ -415,6 +415,16 @@ void pgm_matmul_backward(pg_node *n)
             for (size_t z = 0; z < B; z++)
                 gemm16(dt, 0, 0, M, K, N8, g16 + z * M * N8, N8, 0, M, wp + z * K * N8, N8, 0, K, ga->dev, K, 0, 1,
                        z == 0 ? ba : 1, "dgrad");
+        }
+    }
+    if (gb && ap) {
+        if (w_one) {
+            gemm16p(&pw, dt, 1, 1, K, N, Mw, ap, lda_w, sa_w, lda_w, g16, N8, Mw * N8, N8, gb->dev, N,
+                    s.bbat ? K * N : 0, Bw, bbeta, NULL, "wgrad");
+        } else {
+            for (size_t z = 0; z < Bw; z++)
+                gemm16(dt, 1, 1, K, N, Mw, ap + z * sa_w, lda_w, 0, lda_w, g16 + z * Mw * N8, N8, 0, N8, gb->dev, N,
+                       0, 1, z == 0 ? bbeta : 1, "wgrad");
         }
     }
     if (pw.st)
@@ -499,6 +509,12 @@ int pg_amd_gemm_ex_noalloc(pg_dtype dtype, size_t m, size_t n, size_t k, const v
         return 0;
     if ((k && (!a || !b)) || !c || lda < k || ldb < n || ldc < n) {
         pgd_set_err("pg_amd_gemm_ex_noalloc: null operand or a leading dim below its row length");
+        return -1;
+    }
+    /* queueing pending uploads or deferred ops may compile, allocate or wait
+     * on a staging slot: refused here rather than done behind the caller */
+    if (pgd_work_pending()) {
+        pgd_set_err("pg_amd_gemm_ex_noalloc: uploads or deferred ops are pending; call pg_amd_sync() first");
         return -1;
     }
     pgk_stream st = pgd_stream();
@@ -719,29 +735,61 @@ pg_node *pg_amd_ag_matmul16(pg_node *a, pg_node *b, pg_dtype dtype)
 
 typedef struct {
     int dt, act;
-    pg_tensor *z; /* pre-activation, NULL for act NONE or when no grad is needed */
+    pg_tensor *z;  /* pre-activation, NULL for act NONE or when no grad is needed */
+    pg_tensor *dz; /* the last backward's 16-bit dz, kept when g_keep_dz is set */
 } lin16_ctx;
+
+/* pg_amd_linear16_keep_dz: keep each backward's dz on its node (tests) */
+static bool g_keep_dz;
 
 void pgm_linear16_free_ctx(void *ctx)
 {
     lin16_ctx *cx = ctx;
-    if (cx)
+    if (cx) {
         pg_tensor_free(cx->z);
+        pg_tensor_free(cx->dz);
+    }
     free(cx);
+}
+
+void pg_amd_linear16_keep_dz(bool keep) { g_keep_dz = keep; }
+
+static const lin16_ctx *lin16_of(const pg_node *n)
+{
+    return n && n->backward == pgm_linear16_backward ? (const lin16_ctx *)n->ctx : NULL;
+}
+
+const pg_tensor *pg_amd_linear16_preact(const pg_node *n)
+{
+    const lin16_ctx *cx = lin16_of(n);
+    return cx ? cx->z : NULL;
+}
+
+const pg_tensor *pg_amd_linear16_dz(const pg_node *n)
+{
+    const lin16_ctx *cx = lin16_of(n);
+    return cx ? cx->dz : NULL;
 }
 
 void pgm_linear16_backward(pg_node *n)
 {
     pg_node *px = n->parents[0], *pw = n->parents[1], *pb = n->nparents > 2 ? n->parents[2] : NULL;
     pg_tensor *x = px->value, *w = pw->value;
-    const lin16_ctx *cx = n->ctx;
+    lin16_ctx *cx = n->ctx;
     const int dt = cx->dt;
     size_t M, K, N;
     if (!mm16_dims(x, w, &M, &K, &N) || !M || !N)
         return;
     const size_t K8 = up8(K), N8 = up8(N);
     const size_t dzb = M * N8 * 2;
-    uint16_t *dz16 = tmp_alloc(dzb);
+    /* dz lives in a tensor kept on the node when asked, else in a
+     * temporary freed (stream-ordered) after the GEMMs */
+    pg_tensor *keep = NULL;
+    if (g_keep_dz) {
+        pg_tensor_free(cx->dz);
+        cx->dz = keep = pgt_alloc((pg_dtype)dt, 2, (size_t[]){M, N8});
+    }
+    uint16_t *dz16 = keep ? keep->dev : tmp_alloc(dzb);
     if (!dz16)
         return;
     float *db = NULL;
@@ -766,13 +814,22 @@ void pgm_linear16_backward(pg_node *n)
     pg_tensor *gw = ok && K && pw->requires_grad ? pga_grad_for_write(pw, &bw) : NULL;
     uint16_t *ow = NULL, *ox = NULL;
     size_t obw = 0, obx = 0;
+    /* x and W in one storage (linear16(x, x) with x square) share one kept
+     * 16-bit copy and, for one node, one grad: then each operand is taken
+     * right before its GEMM (taking the second may remake the copy the
+     * first GEMM reads, which stream order makes safe only once that GEMM
+     * is queued) and the GEMMs run one after the other, dgrad first (it
+     * holds the grad's first beta) */
+    const bool alias = x->data_ref == w->data_ref || (gx && gw && (gx == gw || gx->data_ref == gw->data_ref));
     const uint16_t *qw = gx ? operand16(w, dt, K, N, K, N8, &ow, &obw) : NULL;
-    const uint16_t *qx = gw ? operand16(x, dt, M, K, M, K8, &ox, &obx) : NULL;
+    const uint16_t *qx = gw && !alias ? operand16(x, dt, M, K, M, K8, &ox, &obx) : NULL;
     const pgk_gemm_desc dd = {M, K, N8, dz16, N8, 0, M, qw, N8, 0, K, gx ? gx->dev : NULL, K, 0, 1, bx};
     const pgk_gemm_desc dw = {K, N, M, qx, K8, 0, K8, dz16, N8, 0, N8, gw ? gw->dev : NULL, N, 0, 1, bw};
     if (!(qw && qx && pair_full(dt, &dd, &dw, "linear16 dgrad + wgrad"))) {
         if (qw)
             gemm16(dt, 0, 0, M, K, N8, dz16, N8, 0, M, qw, N8, 0, K, gx->dev, K, 0, 1, bx, "linear16 dgrad");
+        if (gw && alias)
+            qx = operand16(x, dt, M, K, M, K8, &ox, &obx);
         if (qx)
             gemm16(dt, 1, 1, K, N, M, qx, K8, 0, K8, dz16, N8, 0, N8, gw->dev, N, 0, 1, bw, "linear16 wgrad");
     }
@@ -780,7 +837,8 @@ void pgm_linear16_backward(pg_node *n)
         pgd_free(ow, obw);
     if (ox)
         pgd_free(ox, obx);
-    pgd_free(dz16, dzb);
+    if (!keep)
+        pgd_free(dz16, dzb);
 }
 
 pg_node *pg_amd_ag_linear16(pg_node *x, pg_node *w, pg_node *b, int act, pg_dtype dtype)
@@ -865,6 +923,7 @@ pg_node *pg_amd_ag_linear16(pg_node *x, pg_node *w, pg_node *b, int act, pg_dtyp
     cx->dt = dt;
     cx->act = act;
     cx->z = z;
+    cx->dz = NULL;
     pg_node *parents[3] = {x, w, b};
     pg_node *n = pga_attach(out, b ? 3 : 2, parents, pgm_linear16_backward, NULL, PG_AG_OP_MATMUL);
     if (n && n->backward) {

@@ -22,6 +22,9 @@
 /* ---- device layer (device.c) ---- */
 bool pgd_ok(void);                 /* init on first use; false if no device */
 bool pgd_initialised(void);        /* pg_amd_init has succeeded (never inits) */
+/* uploads or deferred forward ops are waiting to be queued: the next
+ * pgd_stream()/pgd_sync() queues them (which may compile, allocate or wait) */
+bool pgd_work_pending(void);
 size_t pgd_cached_blocks(void);    /* freed blocks held by the allocator's cache */
 pgk_stream pgd_stream(void);
 /* side stream: work launched on pgd_fork()'s stream runs after everything

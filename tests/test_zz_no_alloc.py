@@ -126,3 +126,24 @@ def test_noalloc_gemm_refuses_beyond_the_workspace(lib):
     assert lib.pg_amd_gemm_ex_noalloc(7, m, n, k, ti(ta).dev, k, ti(tb).dev, n, ti(tc).dev, n) == -1
     for t in (ta, tb, tc):
         lib.pg_tensor_free(t)
+
+
+def test_noalloc_gemm_refuses_pending_work(lib, oracle):
+    """With an upload still waiting to be queued (a leaf made from host
+    data), the call is refused instead of queueing it (which may wait on a
+    staging slot); after pg_amd_sync() the same call runs and matches
+    pg_gemm_ex bit for bit."""
+    print("no-alloc gemm with a pending upload", flush=True)
+    cs = _Case(lib, oracle, BF16, 256, 64, 512, 7)
+    cs.run_ref(lib)
+    lib.sync()
+    pending = lib.tensor(np.ones((64, 64), np.float32))  # a small upload: batched, not yet queued
+    assert cs.run_new(lib) == -1
+    assert "pending" in lib.pg_amd_last_error().decode()
+    assert np.all(lib.read(cs.c_new) == 7.0)  # C untouched (the read queues the upload)
+    lib.sync()
+    assert cs.run_new(lib) == 0, lib.pg_amd_last_error().decode()
+    assert np.array_equal(lib.read(cs.c_new).view(np.uint32), lib.read(cs.c_ref).view(np.uint32))
+    assert np.all(lib.read(pending) == 1.0)
+    lib.pg_tensor_free(pending)
+    cs.free(lib)
