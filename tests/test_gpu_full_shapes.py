@@ -142,23 +142,37 @@ def _q(oracle, x):
     return bf16_to_f32(oracle.cast16(BF16, x))
 
 
-def _bits_within_one_ulp(got16, ref16):
-    """Fraction of 16-bit values that differ from the reference encoding,
-    after asserting that each differing value is the reference's neighbour
-    (adjacent encodings of one sign, or both of magnitude <= 1 ulp)."""
-    g, r = got16.astype(np.int32), ref16.astype(np.int32)
-    diff = g != r
-    same_sign = (g & 0x8000) == (r & 0x8000)
-    near = np.where(same_sign, np.abs(g - r) <= 1, ((g & 0x7FFF) <= 1) & ((r & 0x7FFF) <= 1))
-    assert near[diff].all(), f"{int((~near & diff).sum())} values more than one ulp from the reference"
-    return float(diff.mean())
+def _dz_within_one_ulp(dz16, dz_ref, z, dout):
+    """The fused backward's bf16 dz against q(dz_ref), dz_ref = the oracle's
+    f32 dout * gelu'(z): each value within one bf16 ulp of the reference's
+    encoding, plus the two f32 evaluations' distance where gelu'(z) cancels
+    (pgmath.h's GELU' and the oracle's are each within 5e-7 max(|gelu'|, 0.5)
+    of the exact value, test_pgmath.py), so near a zero of gelu' the bf16
+    values may differ by more ulps of their own tiny magnitude.  Returns the
+    fraction of values whose encoding differs."""
+    from scipy.special import erf
+    got = bf16_to_f32(dz16).astype(np.float64)
+    ref = bf16_to_f32(dz_ref).astype(np.float64) if dz_ref.dtype == np.uint16 else None
+    assert ref is not None
+    mag = np.maximum(np.abs(got), np.abs(ref))
+    ulp = np.exp2(np.floor(np.log2(np.maximum(mag, 2.0 ** -126))) - 7)
+    if z is None:
+        slack = 0.0
+    else:
+        z64 = z.astype(np.float64)
+        d64 = 0.5 * (1.0 + erf(z64 / np.sqrt(2.0))) + z64 * np.exp(-0.5 * z64 * z64) / np.sqrt(2.0 * np.pi)
+        slack = 1e-6 * np.maximum(np.abs(d64), 0.5) * np.abs(dout.astype(np.float64))
+    bad = np.abs(got - ref) > ulp + slack
+    assert not bad.any(), f"{int(bad.sum())} bf16 dz values outside one ulp (+ gelu' evaluation slack)"
+    return float((dz16 != dz_ref).mean())
 
 
-# Fraction of the fused backward's bf16 dz that may sit one ulp from
+# Fraction of the fused backward's bf16 dz that may differ from
 # q(orc_gelu_backward(z, dout)): the device's GELU' differs from the
 # oracle's by a few f32 ulps (pgmath.h's fitted tail), so a value whose f32
 # product lies within that distance of a bf16 rounding boundary rounds the
-# other way -- a fraction of about (few x 2^-24) / 2^-8 ~ 1e-4 at most.
+# other way -- a fraction of about (few x 2^-24) / 2^-8 ~ 1e-4 at most
+# (measured 7.8e-5 on config 5's first layer).
 DZ_ULP_FRAC = 1e-3
 
 
@@ -194,7 +208,7 @@ def _c5_check_gemms(lib, oracle, mlp, nx, x, made, fused):
             assert dz16.shape == (C5_BATCH, (N + 7) // 8 * 8)
             assert not dz16[:, N:].any(), "dz pad columns not zero"
             dz16 = np.ascontiguousarray(dz16[:, :N])
-            frac = _bits_within_one_ulp(dz16, oracle.cast16(BF16, dz_ref))
+            frac = _dz_within_one_ulp(dz16, oracle.cast16(BF16, dz_ref), z if l + 1 < nl else None, dout)
             print(f"  layer {l}: bf16 dz one ulp off q(gelu'(z) dout) in {frac:.2e} of elements", flush=True)
             assert frac <= (DZ_ULP_FRAC if l + 1 < nl else 0.0), (l, frac)
             qdz = bf16_to_f32(dz16)
