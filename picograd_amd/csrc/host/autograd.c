@@ -424,9 +424,11 @@ static bool lz_run_eager(int k)
 }
 
 /* the run as one block with the pending uploads (and the recorded
- * reduction) folded in; false when it does not fit or fails to build, with
- * nothing launched and the uploads still pending */
-static bool lz_run_small(pg_jit_graph *g, const int *ido)
+ * reduction) folded in; g's inputs and outputs are the run's followed by
+ * `nx_in` / `nx_out` more (x_in, x_out: a backward region merged into the
+ * run).  False when it does not fit or fails to build, with nothing
+ * launched and the uploads still pending */
+static bool lz_run_small(pg_jit_graph *g, const void *const *x_in, size_t nx_in, void *const *x_out, size_t nx_out)
 {
     size_t numel = pg_shape_numel(g_lz.ndim, g_lz.shape);
     if (numel > PGJ_SMALL_MAX)
@@ -441,20 +443,72 @@ static bool lz_run_small(pg_jit_graph *g, const int *ido)
             pgd_upload_requeue(&up[i]);
         return false;
     }
-    (void)ido;
-    const void *ip[LZ_MAX];
-    void *op[LZ_MAX];
+    const void *ip[2 * LZ_MAX + 32];
+    void *op[2 * LZ_MAX + 32];
+    size_t ni = 0, no = 0;
     for (int j = 0; j < g_lz.nin; j++)
-        ip[j] = g_lz.in[j].dev;
+        ip[ni++] = g_lz.in[j].dev;
+    for (size_t j = 0; j < nx_in; j++)
+        ip[ni++] = x_in[j];
     for (int k = 0; k < g_lz.nops; k++)
-        op[k] = g_lz.op[k].out.dev;
-    bool ok = pgj_launch_small(g, g_lz.ndim, g_lz.shape, ip, (size_t)g_lz.nin, op, (size_t)g_lz.nops, up,
-                               (size_t)nup, g_lz.red.on ? g_lz.red.src : -1, g_lz.red.on ? g_lz.red.r1.dev : NULL,
+        op[no++] = g_lz.op[k].out.dev;
+    for (size_t k = 0; k < nx_out; k++)
+        op[no++] = x_out[k];
+    bool ok = pgj_launch_small(g, g_lz.ndim, g_lz.shape, ip, ni, op, no, up, (size_t)nup,
+                               g_lz.red.on ? g_lz.red.src : -1, g_lz.red.on ? g_lz.red.r1.dev : NULL,
                                g_lz.red.on ? g_lz.red.r2.dev : NULL, g_lz.red.scale);
     if (!ok)
         for (int i = 0; i < nup; i++)
             pgd_upload_requeue(&up[i]);
     return ok;
+}
+
+/* the run's graph: inputs idi[], one op per recorded op (ido[]), every op
+ * an output; NULL on failure */
+static pg_jit_graph *lz_graph(int *idi, int *ido)
+{
+    pg_jit_graph *g = pg_jit_graph_new();
+    if (!g)
+        return NULL;
+    pgj_graph_set_exact(g);
+    bool built = true;
+    for (int j = 0; j < g_lz.nin && built; j++)
+        built = (idi[j] = pg_jit_add_input(g, g_lz.in[j].ndim, g_lz.in[j].shape)) >= 0;
+    for (int k = 0; k < g_lz.nops && built; k++) {
+        int args[2];
+        for (int i = 0; i < g_lz.op[k].nin; i++)
+            args[i] = g_lz.op[k].in[i] >= 0 ? idi[g_lz.op[k].in[i]] : ido[-g_lz.op[k].in[i] - 1];
+        built = (ido[k] = pg_jit_add_op(g, (pg_jit_op_t)g_lz.op[k].code, args, (size_t)g_lz.op[k].nin)) >= 0;
+    }
+    for (int k = 0; k < g_lz.nops && built; k++)
+        pg_jit_mark_output(g, ido[k]);
+    if (!built) {
+        pg_jit_graph_free(g);
+        return NULL;
+    }
+    return g;
+}
+
+/* the run has executed (or failed with its device error recorded): the
+ * recorded reduction falls back to its own launch if the run's kernel did
+ * not compute it, and every held reference is released */
+static void lz_finish(bool ran, bool red_done)
+{
+    if (g_lz.red.on) {
+        if (!red_done && ran)
+            pgd_check(pgk_sum_all2_f32(g_lz.op[g_lz.red.src].out.dev, g_lz.red.r1.dev, g_lz.red.r2.dev,
+                                       g_lz.shape[0], g_lz.shape[1], g_lz.red.scale, pgd_stream()),
+                      "reduce");
+        pgt_ref_release(g_lz.red.r1.ref);
+        pgt_ref_release(g_lz.red.r2.ref);
+        g_lz.red.on = false;
+    }
+    for (int j = 0; j < g_lz.nin; j++)
+        pgt_ref_release(g_lz.in[j].ref);
+    for (int k = 0; k < g_lz.nops; k++)
+        pgt_ref_release(g_lz.op[k].out.ref);
+    g_lz.nops = g_lz.nin = 0;
+    g_lz.flushing = false;
 }
 
 void pga_lazy_flush(void)
@@ -463,25 +517,12 @@ void pga_lazy_flush(void)
         return;
     g_lz.flushing = true;
     bool ok = false, red_done = false;
-    pg_jit_graph *g = pg_jit_graph_new();
+    int idi[LZ_MAX], ido[LZ_MAX];
+    pg_jit_graph *g = lz_graph(idi, ido);
     if (g) {
-        pgj_graph_set_exact(g);
-        int idi[LZ_MAX], ido[LZ_MAX];
-        bool built = true;
-        for (int j = 0; j < g_lz.nin && built; j++)
-            built = (idi[j] = pg_jit_add_input(g, g_lz.in[j].ndim, g_lz.in[j].shape)) >= 0;
-        for (int k = 0; k < g_lz.nops && built; k++) {
-            int args[2];
-            for (int i = 0; i < g_lz.op[k].nin; i++)
-                args[i] = g_lz.op[k].in[i] >= 0 ? idi[g_lz.op[k].in[i]] : ido[-g_lz.op[k].in[i] - 1];
-            built = (ido[k] = pg_jit_add_op(g, (pg_jit_op_t)g_lz.op[k].code, args, (size_t)g_lz.op[k].nin)) >= 0;
-        }
-        for (int k = 0; k < g_lz.nops && built; k++)
-            pg_jit_mark_output(g, ido[k]);
-        if (built && lz_run_small(g, ido)) {
+        if (lz_run_small(g, NULL, 0, NULL, 0))
             ok = red_done = true;
-        }
-        pg_jit_exe *exe = built && !ok ? pg_jit_compile(g) : NULL;
+        pg_jit_exe *exe = !ok ? pg_jit_compile(g) : NULL;
         if (exe) {
             pg_tensor tin[LZ_MAX], tout[LZ_MAX];
             const pg_tensor *pin[LZ_MAX];
@@ -503,21 +544,93 @@ void pga_lazy_flush(void)
     for (int k = 0; k < g_lz.nops && !ok; k++)
         if (!(eager_ok = lz_run_eager(k))) /* the device error is recorded; the rest are not run */
             break;
-    if (g_lz.red.on) {
-        if (!red_done && eager_ok)
-            pgd_check(pgk_sum_all2_f32(g_lz.op[g_lz.red.src].out.dev, g_lz.red.r1.dev, g_lz.red.r2.dev,
-                                       g_lz.shape[0], g_lz.shape[1], g_lz.red.scale, pgd_stream()),
-                      "reduce");
-        pgt_ref_release(g_lz.red.r1.ref);
-        pgt_ref_release(g_lz.red.r2.ref);
-        g_lz.red.on = false;
+    lz_finish(eager_ok, red_done);
+}
+
+static bool lz_overlaps_ptr(const lz_tensor *x, const void *p, size_t nbytes)
+{
+    const char *a = x->dev, *b = p;
+    const size_t na = pg_shape_numel(x->ndim, x->shape) * 4;
+    return a < b + nbytes && b < a + na;
+}
+
+/* A fused backward region (graph bwd over the loop shape (lnd, ls),
+ * inputs bin[], full-shape outputs bout[]) executed in the same one-block
+ * kernel as the pending small run, after the run's values in each element
+ * (one launch instead of two: config 1's leaves, forward, reduction and
+ * backward).  bwd's inputs that are run inputs or outputs read those
+ * values; its outputs (the grads) must not overlap the run's tensors.  The
+ * merged body is compiled without FMA contraction, as the run is.  True
+ * when the merged kernel was launched (the run is then done); false with
+ * nothing launched and the run still pending otherwise. */
+bool pga_lazy_flush_with_backward(const pg_jit_graph *bwd, size_t lnd, const size_t *ls, const void *const *bin,
+                                  size_t bnin, void *const *bout, size_t bnout)
+{
+    if (!g_lz.nops || g_lz.flushing || !pg_shape_equal(lnd, ls, g_lz.ndim, g_lz.shape) ||
+        pg_shape_numel(lnd, ls) > PGJ_SMALL_MAX || bnin > 32 || bnout > 32)
+        return false;
+    const size_t obytes = pg_shape_numel(lnd, ls) * 4;
+    for (size_t o = 0; o < bnout; o++) {
+        for (int j = 0; j < g_lz.nin; j++)
+            if (lz_overlaps_ptr(&g_lz.in[j], bout[o], obytes))
+                return false;
+        for (int k = 0; k < g_lz.nops; k++)
+            if (lz_overlaps_ptr(&g_lz.op[k].out, bout[o], obytes))
+                return false;
+        if (g_lz.red.on && (lz_overlaps_ptr(&g_lz.red.r1, bout[o], obytes) ||
+                            lz_overlaps_ptr(&g_lz.red.r2, bout[o], obytes)))
+            return false;
     }
-    for (int j = 0; j < g_lz.nin; j++)
-        pgt_ref_release(g_lz.in[j].ref);
-    for (int k = 0; k < g_lz.nops; k++)
-        pgt_ref_release(g_lz.op[k].out.ref);
-    g_lz.nops = g_lz.nin = 0;
-    g_lz.flushing = false;
+    int idi[LZ_MAX], ido[LZ_MAX];
+    pg_jit_graph *g = lz_graph(idi, ido);
+    if (!g)
+        return false;
+    /* bwd's inputs: a run output or input with the same address and shape,
+     * else a new input of the merged kernel (one overlapping a run tensor
+     * otherwise cannot be read in the same pass) */
+    int in_map[32];
+    const void *x_in[32];
+    size_t nx = 0;
+    bool ok = true;
+    for (size_t i = 0; i < bnin && ok; i++) {
+        size_t nd;
+        const size_t *sh;
+        ok = pgj_input_shape(bwd, i, &nd, &sh);
+        if (!ok)
+            break;
+        const size_t nb = pg_shape_numel(nd, sh) * 4;
+        in_map[i] = -1;
+        for (int k = 0; k < g_lz.nops && in_map[i] < 0 && ok; k++) {
+            const lz_tensor *x = &g_lz.op[k].out;
+            if (x->dev == bin[i] && pg_shape_equal(x->ndim, x->shape, nd, sh))
+                in_map[i] = ido[k];
+            else if (lz_overlaps_ptr(x, bin[i], nb))
+                ok = false;
+        }
+        for (int j = 0; j < g_lz.nin && in_map[i] < 0 && ok; j++) {
+            const lz_tensor *x = &g_lz.in[j];
+            if (x->dev == bin[i] && pg_shape_equal(x->ndim, x->shape, nd, sh))
+                in_map[i] = idi[j];
+        }
+        if (ok && in_map[i] < 0) {
+            if (g_lz.nin + nx >= 2 * LZ_MAX) {
+                ok = false;
+                break;
+            }
+            ok = (in_map[i] = pg_jit_add_input(g, nd, sh)) >= 0;
+            x_in[nx++] = bin[i];
+        }
+    }
+    ok = ok && pgj_graph_append(g, bwd, in_map, lnd, ls);
+    if (ok) {
+        g_lz.flushing = true;
+        ok = lz_run_small(g, x_in, nx, bout, bnout);
+        g_lz.flushing = false;
+        if (ok)
+            lz_finish(true, true);
+    }
+    pg_jit_graph_free(g);
+    return ok;
 }
 
 /* reduce_all's two values from the pending run when t is one of its

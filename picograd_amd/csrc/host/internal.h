@@ -104,6 +104,10 @@ bool pgc_load_into(pg_tensor *dst, FILE *fp);
  * else is queued or waited on */
 bool pga_lazy_pending(void);
 void pga_lazy_flush(void);
+/* the pending small run and the fused backward region bwd in one launch
+ * (true), or nothing launched (false) */
+bool pga_lazy_flush_with_backward(const pg_jit_graph *bwd, size_t lnd, const size_t *ls, const void *const *bin,
+                                  size_t bnin, void *const *bout, size_t bnout);
 
 /* ---- JIT internals (jit.c) ---- */
 /* the graph's kernel is compiled without contracting a product and a sum
@@ -153,6 +157,10 @@ int pgj_add_input_ex(pg_jit_graph *g, size_t ndim, const size_t *shape);
  * broadcast-compatible with the loop shape, combining with beta */
 void pgj_mark_output_ex(pg_jit_graph *g, int id, size_t ndim, const size_t *shape, int beta);
 int pgj_op_internal(pg_jit_graph *g, int op, int a, int b);
+/* dst gains src's nodes (src input i -> dst node in_map[i]) and, after its
+ * own, src's outputs, each of which must have the loop shape (lnd, ls) */
+bool pgj_graph_append(pg_jit_graph *dst, const pg_jit_graph *src, const int *in_map, size_t lnd, const size_t *ls);
+bool pgj_input_shape(const pg_jit_graph *g, size_t i, size_t *ndim, const size_t **shape);
 enum { PGJ_OP_GELU_GRAD = 100, PGJ_OP_SIGN = 101, PGJ_OP_ERF_GRAD = 102 };
 /* compile (cached) and launch with device pointers; loop shape given
  * explicitly.  Returns false and sets the JIT error on failure. */

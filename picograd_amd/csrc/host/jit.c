@@ -346,6 +346,55 @@ void pgj_mark_output_ex(pg_jit_graph *g, int id, size_t ndim, const size_t *shap
     o->beta = beta;
 }
 
+/* Appends src's nodes to dst: src's input i becomes dst's node in_map[i],
+ * constants and ops are copied in order, and src's outputs are marked on
+ * dst after dst's own (same shapes and betas).  Every output of src must be
+ * a full loop-shape output (lnd, ls): the caller's one-block run stores
+ * them element by element.  False when that fails (dst may hold unused
+ * extra nodes then, and no extra outputs). */
+bool pgj_graph_append(pg_jit_graph *dst, const pg_jit_graph *src, const int *in_map, size_t lnd, const size_t *ls)
+{
+    if (!dst || !src || dst->nout + src->nout > MAXIO * 2)
+        return false;
+    for (size_t o = 0; o < src->nout; o++)
+        if (!pg_shape_equal(src->outs[o].ndim, src->outs[o].shape, lnd, ls))
+            return false;
+    int *map = malloc((src->nn ? src->nn : 1) * sizeof(int));
+    if (!map)
+        return false;
+    bool ok = true;
+    for (size_t id = 0; id < src->nn && ok; id++) {
+        const jnode *n = &src->nodes[id];
+        if (n->kind == JN_INPUT) {
+            map[id] = -1;
+            for (size_t i = 0; i < src->nin; i++)
+                if (src->inputs[i] == (int)id)
+                    map[id] = in_map[i];
+            ok = map[id] >= 0 && (size_t)map[id] < dst->nn &&
+                 pg_shape_equal(dst->nodes[map[id]].ndim, dst->nodes[map[id]].shape, n->ndim, n->shape);
+        } else if (n->kind == JN_CONST) {
+            ok = (map[id] = pg_jit_add_const(dst, n->cval)) >= 0;
+        } else {
+            ok = (map[id] = pgj_op_internal(dst, n->op, map[n->in[0]], n->nin == 2 ? map[n->in[1]] : -1)) >= 0;
+        }
+    }
+    for (size_t o = 0; o < src->nout && ok; o++)
+        pgj_mark_output_ex(dst, map[src->outs[o].node], src->outs[o].ndim, src->outs[o].shape, src->outs[o].beta);
+    free(map);
+    return ok;
+}
+
+/* input i's shape */
+bool pgj_input_shape(const pg_jit_graph *g, size_t i, size_t *ndim, const size_t **shape)
+{
+    if (!g || i >= g->nin)
+        return false;
+    const jnode *n = &g->nodes[g->inputs[i]];
+    *ndim = n->ndim;
+    *shape = n->shape;
+    return true;
+}
+
 void pg_jit_mark_output(pg_jit_graph *g, int id)
 {
     if (!g || id < 0 || (size_t)id >= g->nn) {

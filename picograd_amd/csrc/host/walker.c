@@ -455,7 +455,10 @@ static bool run_region(wctx *w, int r, const pg_tensor *root_grad, float scale, 
         }
     }
     if (ok) {
-        ok = pgj_launch(b.g, L->ndim, L->shape, b.in_ptr, b.nin, optr, nout);
+        /* a small forward run still pending (config 1: leaves, forward and
+         * sum in one block) takes the region into its own launch */
+        ok = pga_lazy_flush_with_backward(b.g, L->ndim, L->shape, b.in_ptr, b.nin, optr, nout) ||
+             pgj_launch(b.g, L->ndim, L->shape, b.in_ptr, b.nin, optr, nout);
         if (!ok) {
             pga_set_err("fused backward failed: %s", pg_jit_last_error());
             /* restore the zero flag of grads the kernel did not write */

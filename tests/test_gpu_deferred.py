@@ -245,3 +245,56 @@ def test_sliced_reduce_all_in_one_launch(lib, shape, mean):
     assert np.array_equal(bits(g1), bits(lib.grad(nb)))
     for n in (chain2, s1, nb, chain, s0, na):
         lib.pg_node_free(n)
+
+
+@pytest.mark.parametrize("shape", [(64, 64), (37, 63), (127, 127), (1, 100)])
+@pytest.mark.parametrize("reuse", [False, True])
+def test_backward_joins_the_small_run(lib, oracle, shape, reuse):
+    """Config 1's iteration -- three fresh leaves, a deferred forward run
+    ending in sum_all, pg_backward -- takes ONE launch with the JIT on: the
+    fused backward region joins the pending run's one-block kernel
+    (uploads, forward values, both reduction stages, grads).  The forward
+    values and the loss equal the eager path's bit for bit, and the grads
+    agree with the eager backward to 1e-6 (both evaluate the same chain
+    rule; the joined body is compiled without FMA contraction).  `reuse`
+    feeds leaf a into two ops (its grad sums two contributions)."""
+    import ctypes as C
+    rng = np.random.default_rng(shape[0] * 7 + shape[1] + reuse)
+    a, b, c = (rng.uniform(-1, 1, shape).astype(np.float32) for _ in range(3))
+
+    def build(L):
+        na, nb, nc = L.var(a), L.var(b), L.var(c)
+        t0 = L.op("add", na, nb)
+        t1 = L.op("mul", t0, na if reuse else nc)
+        t2 = L.op("tanh", L.op("relu", t1))
+        loss = L.op("sum_all", t2)
+        return (na, nb, nc, t2, loss), [na, nb, nc, t0, t1, t2, loss]
+
+    got = {}
+    for jit in (True, False):
+        lib.pg_autograd_set_jit(jit)
+        try:
+            (na, nb, nc, t2, loss), made = build(lib)
+            lib.pg_amd_timer_reset()
+            lib.pg_amd_timer_enable(1)
+            lib.pg_backward(loss)
+            cnt = C.c_size_t(0)
+            lib.pg_amd_timer_read(0, C.byref(cnt))  # JIT kernel launches (PGD_T_JIT_MAIN)
+            lib.pg_amd_timer_enable(0)
+            lib.pg_amd_timer_reset()
+            got[jit] = dict(vals=[lib.value(t2), lib.value(loss)], grads=[lib.grad(n) for n in (na, nb, nc)],
+                            launches=cnt.value)
+            for n in reversed(made):
+                lib.pg_node_free(n)
+        finally:
+            lib.pg_autograd_set_jit(True)
+    assert got[True]["launches"] == 1, got[True]["launches"]
+    for u, v in zip(got[True]["vals"], got[False]["vals"]):
+        assert np.array_equal(bits(u), bits(v))
+    for g1, g0 in zip(got[True]["grads"], got[False]["grads"]):
+        assert g1 is not None and g0 is not None
+        assert np.max(np.abs(g1 - g0)) <= 1e-6 * max(1.0, float(np.abs(g0).max()))
+    if not reuse and shape == (64, 64):
+        da, db, dc = oracle.chain1(a.ravel(), b.ravel(), c.ravel())
+        for g, want in zip(got[True]["grads"], (da, db, dc)):
+            assert np.max(np.abs(g.ravel() - want)) <= 1e-6
