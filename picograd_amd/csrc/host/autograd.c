@@ -433,16 +433,20 @@ static bool lz_run_small(pg_jit_graph *g, const void *const *x_in, size_t nx_in,
     size_t numel = pg_shape_numel(g_lz.ndim, g_lz.shape);
     if (numel > PGJ_SMALL_MAX)
         return false;
+    if (g_lz.red.on && !pgj_small_reduce_fits(g_lz.ndim, g_lz.shape))
+        return false;
+    /* the pending uploads ride in the block when they fit it; otherwise
+     * they stay in the batch, which the launch queues (one k_upload) ahead
+     * of the block */
     pgk_upload up[PGK_UPLOAD_MAX];
     int nup = pgd_upload_take(up, PGK_UPLOAD_MAX);
-    if (nup < 0)
-        return false;
-    if (!pgj_small_fits(numel, (size_t)nup, up) ||
-        (g_lz.red.on && !pgj_small_reduce_fits(g_lz.ndim, g_lz.shape))) {
+    if (nup > 0 && !pgj_small_fits(numel, (size_t)nup, up)) {
         for (int i = 0; i < nup; i++) /* back to the batch, in order */
             pgd_upload_requeue(&up[i]);
-        return false;
+        nup = 0;
     }
+    if (nup < 0)
+        nup = 0;
     const void *ip[2 * LZ_MAX + 32];
     void *op[2 * LZ_MAX + 32];
     size_t ni = 0, no = 0;

@@ -251,9 +251,11 @@ def test_sliced_reduce_all_in_one_launch(lib, shape, mean):
 @pytest.mark.parametrize("reuse", [False, True])
 def test_backward_joins_the_small_run(lib, oracle, shape, reuse):
     """Config 1's iteration -- three fresh leaves, a deferred forward run
-    ending in sum_all, pg_backward -- takes ONE launch with the JIT on: the
-    fused backward region joins the pending run's one-block kernel
-    (uploads, forward values, both reduction stages, grads).  The forward
+    ending in sum_all, pg_backward -- takes ONE JIT launch with the JIT on:
+    the fused backward region joins the pending run's one-block kernel
+    (uploads, forward values, both reduction stages, grads; leaves that are
+    not whole 16-byte pieces, (37, 63) and (127, 127), are uploaded by one
+    k_upload ahead of it).  The forward
     values and the loss equal the eager path's bit for bit, and the grads
     agree with the eager backward to 1e-6 (both evaluate the same chain
     rule; the joined body is compiled without FMA contraction).  `reuse`
