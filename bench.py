@@ -928,13 +928,18 @@ def cpu_c1():
     from picograd_amd.capi import PgLib
     if not REF_SO.exists():
         return None
+    c_jit, c_eager = run_chain_loop(REF_SO, 10000, True), run_chain_loop(REF_SO, 10000, False)
     R = PgLib(REF_SO, device=False)
     jit = chain_backward_loop(R, (64, 64), 10000)
     R.pg_autograd_set_jit(False)
     eager = chain_backward_loop(R, (64, 64), 10000)
     R.pg_autograd_set_jit(True)
-    return {"value": jit, "unit": "us/iter", "eager_us_per_iter": eager, "cores": 1, "kind": "reference",
-            "sample": "10,000 iterations of the config-1 loop, JIT on (value) and off"}
+    out = {"value": c_jit["us_per_iter"] if c_jit else jit, "unit": "us/iter",
+           "eager_us_per_iter": c_eager["us_per_iter"] if c_eager else eager,
+           "python_ctypes_us_per_iter": jit, "python_ctypes_eager_us_per_iter": eager, "cores": 1,
+           "kind": "reference", "loop": "C (tests/c_callers/chain_loop.c)" if c_jit else "Python ctypes",
+           "sample": "10,000 iterations of the config-1 loop, JIT on (value) and off"}
+    return out
 
 
 def bench_jit(L):
@@ -992,8 +997,37 @@ def bench_c1(L, iters=10000):
     for _ in range(iters):
         one()
     L.sync()
-    return {"us_per_iter": (time.perf_counter() - s) / iters * 1e6, "iters": iters,
-            "reference_cpu_us_per_iter": 114.0}
+    py_us = (time.perf_counter() - s) / iters * 1e6
+    c_loop = run_chain_loop(picograd_amd_lib_path(), iters)
+    out = {"us_per_iter": c_loop["us_per_iter"] if c_loop else py_us, "iters": iters,
+           "loop": "C (tests/c_callers/chain_loop.c)" if c_loop else "Python ctypes",
+           "us_per_iter_python_ctypes": py_us, "reference_published_us_per_iter": 114.0}
+    if c_loop:
+        out["c_loop_max_grad_err"] = c_loop["max_err"]
+    return out
+
+
+CHAIN_LOOP = ROOT / "tests" / "c_callers" / "bin" / "chain_loop"
+
+
+def picograd_amd_lib_path():
+    from picograd_amd.capi import _DEFAULT_LIB
+    return _DEFAULT_LIB
+
+
+def run_chain_loop(lib_path, iters, jit=True):
+    """Config 1's loop as a C program (the reference's benchmark is a C
+    loop, examples/train_xor_jit.c:200-214) over `lib_path`, run as a child
+    process: {"us_per_iter", "iters", "max_err"}, or None when the program
+    is not built or fails."""
+    if not CHAIN_LOOP.exists():
+        return None
+    r = subprocess.run([str(CHAIN_LOOP), str(lib_path), str(iters), "1" if jit else "0"], capture_output=True,
+                       text=True, timeout=600)
+    if r.returncode != 0:
+        log(f"[c1] chain_loop failed ({r.returncode}): {r.stderr.strip()[-300:]}")
+        return None
+    return json.loads(r.stdout.strip().splitlines()[-1])
 
 
 def main(argv=None):

@@ -293,8 +293,10 @@ def test_backward_joins_the_small_run(lib, oracle, shape, reuse):
     assert got[True]["launches"] == 1, got[True]["launches"]
     for u, v in zip(got[True]["vals"], got[False]["vals"]):
         assert np.array_equal(bits(u), bits(v))
-    for g1, g0 in zip(got[True]["grads"], got[False]["grads"]):
-        assert g1 is not None and g0 is not None
+    for i, (g1, g0) in enumerate(zip(got[True]["grads"], got[False]["grads"])):
+        if reuse and i == 2:  # c is not in the graph
+            assert g1 is None and g0 is None
+            continue
         assert np.max(np.abs(g1 - g0)) <= 1e-6 * max(1.0, float(np.abs(g0).max()))
     if not reuse and shape == (64, 64):
         da, db, dc = oracle.chain1(a.ravel(), b.ravel(), c.ravel())
