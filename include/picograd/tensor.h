@@ -41,6 +41,11 @@ typedef struct pg_data_ref {
      * elements in storage order */
     size_t shadow_cols, shadow_ld;
     size_t shadow_bytes; /* its allocation */
+    /* a clip-by-norm scale not yet written to the f32 elements: each
+     * element's value is (x * clip_mul) * clip_inv (pg_clip_grad_norm);
+     * library-internal */
+    bool clip_pending;
+    float clip_mul, clip_inv;
 } pg_data_ref;
 
 typedef struct pg_tensor {

@@ -182,7 +182,12 @@ void pg_adam_step(pg_adam *opt)
             pga_set_err("pg_adam_step: parameter and grad storage must be f32");
             continue;
         }
-        pgt_materialize(g);
+        /* a pending zero is written; a pending clip scale is applied by
+         * the update kernel as it reads the grad (it stays pending on the
+         * grad's storage for any other reader) */
+        if (g->pg_flags & PG_TENSOR_ZERO_PENDING)
+            pgt_materialize(g);
+        const pg_data_ref *gr = g->data_ref;
         if (!s->m) {
             /* adam.c:140-153: moments created at zero on first use */
             s->m = pg_tensor_zeros(p->value->ndim, p->value->shape);
@@ -198,6 +203,9 @@ void pg_adam_step(pg_adam *opt)
         pgk_adam_seg *q = &segs[ns];
         q->p = p->value->dev;
         q->g = g->dev;
+        q->gclip = gr && gr->clip_pending;
+        q->gmul = q->gclip ? gr->clip_mul : 1.0f;
+        q->ginv = q->gclip ? gr->clip_inv : 1.0f;
         q->m = s->m->dev;
         q->v = s->v->dev;
         q->vmax = c.amsgrad ? s->vmax->dev : NULL;

@@ -199,8 +199,10 @@ pg_tensor *pga_grad_for_write(pg_node *n, int *beta)
     }
     if (n->grad->pg_flags & PG_TENSOR_ZERO_PENDING) {
         n->grad->pg_flags &= ~PG_TENSOR_ZERO_PENDING;
+        pgt_overwrite(n->grad);
         *beta = 0;
     } else {
+        pgt_settle(n->grad); /* accumulating reads the current values */
         *beta = 1;
     }
     return n->grad;

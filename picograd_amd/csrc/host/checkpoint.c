@@ -374,6 +374,7 @@ bool pgc_load_into(pg_tensor *dst, FILE *fp)
         same = dst->shape[d] == t->shape[d];
     if (same) {
         dst->pg_flags &= ~PG_TENSOR_ZERO_PENDING;
+        pgt_overwrite(dst);
         pgt_touch(dst);
         same = pgd_d2d(dst->dev, t->dev, t->numel * t->elem_size);
     }

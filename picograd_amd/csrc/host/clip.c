@@ -39,6 +39,7 @@ static int collect(pg_node **params, size_t n, pgk_grad_seg **out, int **round, 
         pg_tensor *g = p->grad;
         if ((g->pg_flags & PG_TENSOR_ZERO_PENDING) || g->numel == 0)
             continue;
+        pgt_settle(g); /* an earlier clip's scale, before the squares are read */
         int r = 0;
         for (int q = 0; q < ns; q++)
             r += segs[q].g == (float *)g->dev ? 1 : 0;
@@ -55,10 +56,38 @@ static int collect(pg_node **params, size_t n, pgk_grad_seg **out, int **round, 
     return ns;
 }
 
+/* Whether the scale can stay pending on the grads' storages instead of a
+ * pass of its own: each listed grad is the whole of a storage no other
+ * listed grad shares (a grad listed twice is scaled twice, clip.c:34-39,
+ * which one pending factor cannot express). */
+static bool lazy_ok(pg_node **params, size_t n)
+{
+    for (size_t i = 0; i < n; i++) {
+        const pg_tensor *g = params[i] && params[i]->grad ? params[i]->grad : NULL;
+        if (!g || (g->pg_flags & PG_TENSOR_ZERO_PENDING) || g->numel == 0)
+            continue;
+        const pg_data_ref *r = g->data_ref;
+        if (!r || g->dev != r->ptr || g->numel * 4 != r->nbytes || g->dtype != PG_DTYPE_F32)
+            return false;
+        for (size_t j = 0; j < i; j++) {
+            const pg_tensor *h = params[j] && params[j]->grad ? params[j]->grad : NULL;
+            if (h && h->data_ref == r && !(h->pg_flags & PG_TENSOR_ZERO_PENDING) && h->numel)
+                return false;
+        }
+    }
+    return true;
+}
+
 /* queues the norm (and with clip, the scaling); writes the norm to *norm
- * after one wait.  Returns false on a device error. */
+ * after one wait.  Returns false on a device error.  With clip, the scale
+ * (max_norm and 1 / (norm + eps), as the finisher computed them) is left
+ * pending on the grads' storages when lazy_ok: the next optimiser step
+ * applies it as it reads the grads, and any other reader first writes it
+ * (pgt_settle), so the grads read as scaled everywhere without a pass of
+ * their own between the norm and the step. */
 static bool norm_pass(pg_node **params, size_t n, int clip, float max_norm, float eps, float *norm)
 {
+    const bool lazy = clip && lazy_ok(params, n);
     pgk_grad_seg *segs;
     int *rd, rounds;
     int ns = collect(params, n, &segs, &rd, &rounds);
@@ -79,6 +108,22 @@ static bool norm_pass(pg_node **params, size_t n, int clip, float max_norm, floa
     float *res = (float *)(ws + res_off);
     int tk = pgd_tbegin(PGD_T_CLIP);
     ok = pgd_check(pgk_grad_norm(segs, ns, clip, max_norm, eps, res, ws, pgd_stream()), "grad norm");
+    if (ok && lazy) {
+        float r4[4];
+        pgd_tend(tk);
+        ok = pgd_d2h(r4, res, sizeof r4);
+        *norm = r4[0];
+        if (ok && r4[2] != 0.0f) /* clip.c:32-33: scaled only above max_norm */
+            for (size_t i = 0; i < n; i++) {
+                pg_tensor *g = params[i] && params[i]->grad ? params[i]->grad : NULL;
+                if (!g || (g->pg_flags & PG_TENSOR_ZERO_PENDING) || g->numel == 0)
+                    continue;
+                g->data_ref->clip_pending = true;
+                g->data_ref->clip_mul = r4[3];
+                g->data_ref->clip_inv = r4[1];
+            }
+        goto done;
+    }
     if (ok && clip) {
         /* round r holds the r-th repeat of each grad: one launch per round */
         pgk_grad_seg *sub = malloc(ns * sizeof *sub);

@@ -18,6 +18,14 @@
 
 /* pg_tensor.pg_flags */
 #define PG_TENSOR_ZERO_PENDING 1u /* logically zero; device bytes not written */
+/* A clip-by-norm scale pending on a storage (pg_data_ref.clip_pending):
+ * pgt_settle writes it to the elements (before any read of them other than
+ * by the optimiser kernels, which apply it as they read), pgt_overwrite
+ * drops it when all of the storage is about to be written (else settles),
+ * pgt_drop_clip drops it (the storage's value is being discarded). */
+bool pgt_settle(const pg_tensor *t);
+void pgt_overwrite(const pg_tensor *t);
+void pgt_drop_clip(const pg_tensor *t);
 
 /* ---- device layer (device.c) ---- */
 bool pgd_ok(void);                 /* init on first use; false if no device */

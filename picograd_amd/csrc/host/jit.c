@@ -1594,6 +1594,7 @@ bool pg_jit_run(pg_jit_exe *exe, const pg_tensor **inputs, size_t ninputs, pg_te
             return false;
         }
         t->pg_flags &= ~PG_TENSOR_ZERO_PENDING;
+        pgt_overwrite(t);
         pgt_touch(t); /* its 16-bit copy, if any, is stale */
         op[i] = t->dev;
     }

@@ -116,7 +116,12 @@ void pg_sgd_step(pg_sgd *opt)
             pga_set_err("pg_sgd_step: parameter storage must be f32");
             continue;
         }
-        pgt_materialize(g);
+        /* a pending zero is written; a pending clip scale is applied by
+         * the update kernel as it reads the grad (it stays pending on the
+         * grad's storage for any other reader) */
+        if (g->pg_flags & PG_TENSOR_ZERO_PENDING)
+            pgt_materialize(g);
+        const pg_data_ref *gr = g->data_ref;
         if (c.momentum != 0.0f && !opt->st[i].buf) {
             opt->st[i].buf = pg_tensor_zeros(p->value->ndim, p->value->shape);
             if (!opt->st[i].buf)
@@ -124,6 +129,9 @@ void pg_sgd_step(pg_sgd *opt)
         }
         segs[ns].p = p->value->dev;
         segs[ns].g = g->dev;
+        segs[ns].gclip = gr && gr->clip_pending;
+        segs[ns].gmul = segs[ns].gclip ? gr->clip_mul : 1.0f;
+        segs[ns].ginv = segs[ns].gclip ? gr->clip_inv : 1.0f;
         segs[ns].buf = c.momentum != 0.0f ? opt->st[i].buf->dev : NULL;
         /* a 16-bit shadow of the parameter (kept for the MFMA GEMMs) is
          * rewritten from the updated values in the same pass */

@@ -125,8 +125,38 @@ static bool fill_value(pg_tensor *t, float v)
     return pgd_check(pgk_fill_u16((uint16_t *)t->dev, t->numel, h, pgd_stream()), "fill");
 }
 
+bool pgt_settle(const pg_tensor *t)
+{
+    pg_data_ref *r = t ? t->data_ref : NULL;
+    if (!r || !r->clip_pending)
+        return true;
+    r->clip_pending = false;
+    r->shadow_stale = true;
+    const pgk_grad_seg seg = {(float *)r->ptr, r->nbytes / 4};
+    return pgd_check(pgk_grad_scale_const(&seg, 1, r->clip_mul, r->clip_inv, pgd_stream()), "clip scale");
+}
+
+void pgt_drop_clip(const pg_tensor *t)
+{
+    if (t && t->data_ref)
+        t->data_ref->clip_pending = false;
+}
+
+void pgt_overwrite(const pg_tensor *t)
+{
+    if (!t || !t->data_ref || !t->data_ref->clip_pending)
+        return;
+    /* every element of t is about to be written: a pending clip scale of
+     * the whole storage is dropped, of a larger storage applied first */
+    if (t->dev == t->data_ref->ptr && t->numel * t->elem_size == t->data_ref->nbytes)
+        pgt_drop_clip(t);
+    else
+        pgt_settle(t);
+}
+
 void pgt_materialize(pg_tensor *t)
 {
+    pgt_settle(t);
     if (t && (t->pg_flags & PG_TENSOR_ZERO_PENDING)) {
         fill_value(t, 0.0f);
         t->pg_flags &= ~PG_TENSOR_ZERO_PENDING;
@@ -271,6 +301,7 @@ pg_tensor *pg_amd_tensor_to_dtype(const pg_tensor *t, pg_dtype dtype)
     }
     if (t->dtype == dtype)
         return pg_tensor_clone(t);
+    pgt_settle(t);
     pg_tensor *own;
     const pg_tensor *src = pgt_contiguous(t, &own);
     if (!src)
@@ -394,6 +425,7 @@ pg_tensor *pg_tensor_clone(const pg_tensor *t)
         fill_value(c, 0.0f);
         return c;
     }
+    pgt_settle(t);
     if (!pgt_is_contiguous(t)) {
         /* a strided view: its elements in row-major order */
         if (!pgd_check(pgk_gather_strided(t->elem_size, t->dev, c->dev, (int)t->ndim, t->shape, t->stride,
@@ -424,6 +456,7 @@ void pg_tensor_fill(pg_tensor *t, float value)
     if (!t)
         return;
     t->pg_flags &= ~PG_TENSOR_ZERO_PENDING;
+    pgt_overwrite(t);
     pgt_touch(t);
     fill_value(t, value);
 }
@@ -436,6 +469,8 @@ void pg_tensor_copy_from(pg_tensor *dst, const pg_tensor *src)
         pg_tensor_fill(dst, 0.0f);
         return;
     }
+    pgt_settle(src);
+    pgt_overwrite(dst);
     dst->pg_flags &= ~PG_TENSOR_ZERO_PENDING;
     pgt_touch(dst);
     pgd_d2d(dst->dev, src->dev, src->numel * src->elem_size);
@@ -530,6 +565,7 @@ bool pg_tensor_copy_to_host(const pg_tensor *t, void *dst)
         memset(dst, 0, nb);
         return true;
     }
+    pgt_settle(t);
     return pgd_d2h(dst, t->dev, nb);
 }
 
@@ -538,6 +574,7 @@ bool pg_tensor_copy_from_host(pg_tensor *t, const void *src)
     if (!t || !src)
         return false;
     t->pg_flags &= ~PG_TENSOR_ZERO_PENDING;
+    pgt_overwrite(t);
     pgt_touch(t);
     return pgd_h2d(t->dev, src, t->numel * t->elem_size);
 }
@@ -721,6 +758,7 @@ float pg_tensor_get(const pg_tensor *t, const size_t *idx)
     assert(t && idx);
     if (t->pg_flags & PG_TENSOR_ZERO_PENDING)
         return 0.0f;
+    pgt_settle(t);
     unsigned char b[4] = {0};
     if (!pgd_d2h(b, (const char *)t->dev + flat_offset(t, idx) * t->elem_size, t->elem_size))
         return 0.0f;

@@ -522,8 +522,10 @@ static bool walk(pg_node *loss, const pg_tensor *seed, wmode mode)
         }
         if (mode != MODE_SUFFIX_ONLY)
             for (size_t k = 0; k < N; k++)
-                if (order.v[k]->grad)
+                if (order.v[k]->grad) {
                     order.v[k]->grad->pg_flags |= PG_TENSOR_ZERO_PENDING;
+                    pgt_overwrite(order.v[k]->grad); /* its values are discarded */
+                }
 
         if (mode != MODE_SEEDED && g_jit_enabled) {
             /* fold the SUM/MEAN chain above the loss into a scalar */

@@ -531,6 +531,15 @@ __device__ __forceinline__ void sgd_elem(float &p, float g, float &b, bool has_b
 // and HAS_BUF are compile-time, so every load of the chunk is issued before
 // the first use: under a per-vector bound or buffer test the compiler
 // issues and waits for each group of loads in turn.
+// the grad as the update reads it: with a pending clip-by-norm scale,
+// (g * gmul) * ginv, the scaling pass's arithmetic (bit for bit the update
+// after that pass)
+__device__ __forceinline__ float sgd_clipped(const pgk_sgd_seg &sg, float g)
+{
+#pragma clang fp contract(off)
+    return sg.gclip ? (g * sg.gmul) * sg.ginv : g;
+}
+
 template <bool FULL, bool HAS_BUF>
 __device__ __forceinline__ void sgd_vec(const pgk_sgd_seg &sg, size_t base, size_t n, float lr, float mu, float damp,
                                         float wd, int nesterov)
@@ -543,6 +552,8 @@ __device__ __forceinline__ void sgd_vec(const pgk_sgd_seg &sg, size_t base, size
         if (FULL || e[k] + 4 <= n) {
             p[k] = reinterpret_cast<const float4 *>(sg.p + e[k])[0];
             g[k] = reinterpret_cast<const float4 *>(sg.g + e[k])[0];
+            g[k] = make_float4(sgd_clipped(sg, g[k].x), sgd_clipped(sg, g[k].y), sgd_clipped(sg, g[k].z),
+                               sgd_clipped(sg, g[k].w));
             b[k] = HAS_BUF ? reinterpret_cast<const float4 *>(sg.buf + e[k])[0] : make_float4(0, 0, 0, 0);
         }
     }
@@ -563,7 +574,7 @@ __device__ __forceinline__ void sgd_vec(const pgk_sgd_seg &sg, size_t base, size
         } else {
             for (size_t j = e[k]; j < n; ++j) { // the last 1-3 elements
                 float pj = sg.p[j], bj = HAS_BUF ? sg.buf[j] : 0.0f;
-                sgd_elem(pj, sg.g[j], bj, HAS_BUF, lr, mu, damp, wd, nesterov);
+                sgd_elem(pj, sgd_clipped(sg, sg.g[j]), bj, HAS_BUF, lr, mu, damp, wd, nesterov);
                 sg.p[j] = pj;
                 if (HAS_BUF)
                     sg.buf[j] = bj;
@@ -600,7 +611,7 @@ __global__ void __launch_bounds__(kBlock) k_sgd(sgd_table tab, float lr, float m
         const size_t end = base + kSgdChunk < n ? base + kSgdChunk : n;
         for (size_t j = base + threadIdx.x; j < end; j += kBlock) {
             float pj = sg.p[j], bj = has_buf ? sg.buf[j] : 0.0f;
-            sgd_elem(pj, sg.g[j], bj, has_buf, lr, mu, damp, wd, nesterov);
+            sgd_elem(pj, sgd_clipped(sg, sg.g[j]), bj, has_buf, lr, mu, damp, wd, nesterov);
             sg.p[j] = pj;
             if (has_buf)
                 sg.buf[j] = bj;

@@ -221,6 +221,9 @@ typedef struct {
     /* shadow_cols != 0: element j's copy at (j / shadow_cols) * shadow_ld +
      * j % shadow_cols (rows padded to a pitch); 0: at j */
     size_t shadow_cols, shadow_ld;
+    /* gclip: g is read as (g * gmul) * ginv (a pending clip-by-norm scale) */
+    int gclip;
+    float gmul, ginv;
 } pgk_sgd_seg;
 int pgk_sgd_multi(const pgk_sgd_seg *segs, int nseg, float lr, float momentum, float dampening,
                   float weight_decay, int nesterov, pgk_stream s);
@@ -236,6 +239,8 @@ typedef struct {
     float lr, wd;     /* this tensor's learning rate and weight decay */
     size_t n;
     size_t shadow_cols, shadow_ld; /* as pgk_sgd_seg's */
+    int gclip;                     /* as pgk_sgd_seg's */
+    float gmul, ginv;
 } pgk_adam_seg;
 typedef struct {
     float beta1, beta2, eps;
@@ -262,6 +267,8 @@ int pgk_grad_norm(const pgk_grad_seg *segs, int nseg, int clip, float max_norm, 
  * device-side decision pgk_grad_norm took); a tensor must not appear twice
  * in one call */
 int pgk_grad_scale(const pgk_grad_seg *segs, int nseg, const float *res, pgk_stream s);
+/* g = (g * mul) * inv for every grad (a scale decided on the host) */
+int pgk_grad_scale_const(const pgk_grad_seg *segs, int nseg, float mul, float inv, pgk_stream s);
 /* g = min(max(g, -c), c) elementwise (NaN kept); a tensor must not
  * appear twice in one call */
 int pgk_clip_value(const pgk_grad_seg *segs, int nseg, float c, pgk_stream s);

@@ -60,6 +60,22 @@ __device__ __forceinline__ void adam_elem(float &p, float g, float &m, float &v,
     p = pj - (m * lr) / denom;
 }
 
+// the grad as the update reads it: with a pending clip-by-norm scale,
+// (g * mul) * inv -- the scaling pass's arithmetic, so the update equals
+// the one after that pass bit for bit
+template <class Seg>
+__device__ __forceinline__ float clipped(const Seg &sg, float g)
+{
+#pragma clang fp contract(off)
+    return sg.gclip ? (g * sg.gmul) * sg.ginv : g;
+}
+
+template <class Seg>
+__device__ __forceinline__ float4 clipped4(const Seg &sg, float4 g)
+{
+    return make_float4(clipped(sg, g.x), clipped(sg, g.y), clipped(sg, g.z), clipped(sg, g.w));
+}
+
 __global__ void __launch_bounds__(kBlock) k_adam(adam_table tab, pgk_adam_hyper h)
 {
     const unsigned b = blockIdx.x;
@@ -84,7 +100,7 @@ __global__ void __launch_bounds__(kBlock) k_adam(adam_table tab, pgk_adam_hyper 
             e[k] = base + 4 * ((size_t)threadIdx.x + (size_t)k * kBlock);
             if (e[k] + 4 <= n) {
                 p[k] = *reinterpret_cast<const float4 *>(P + e[k]);
-                g[k] = *reinterpret_cast<const float4 *>(G + e[k]);
+                g[k] = clipped4(sg, *reinterpret_cast<const float4 *>(G + e[k]));
                 m[k] = *reinterpret_cast<const float4 *>(M + e[k]);
                 v[k] = *reinterpret_cast<const float4 *>(V + e[k]);
                 vm[k] = ams ? *reinterpret_cast<const float4 *>(VM + e[k]) : make_float4(0, 0, 0, 0);
@@ -109,7 +125,7 @@ __global__ void __launch_bounds__(kBlock) k_adam(adam_table tab, pgk_adam_hyper 
             } else {
                 for (size_t j = e[k]; j < n; ++j) { // the last 1-3 elements
                     float pj = P[j], mj = M[j], vj = V[j], vmj = ams ? VM[j] : 0.0f;
-                    adam_elem(pj, G[j], mj, vj, vmj, ams, h, sg.lr, sg.wd);
+                    adam_elem(pj, clipped(sg, G[j]), mj, vj, vmj, ams, h, sg.lr, sg.wd);
                     P[j] = pj, M[j] = mj, V[j] = vj;
                     if (ams)
                         VM[j] = vmj;
@@ -122,7 +138,7 @@ __global__ void __launch_bounds__(kBlock) k_adam(adam_table tab, pgk_adam_hyper 
         const size_t end = base + kAdamChunk < n ? base + kAdamChunk : n;
         for (size_t j = base + threadIdx.x; j < end; j += kBlock) {
             float pj = P[j], mj = M[j], vj = V[j], vmj = ams ? VM[j] : 0.0f;
-            adam_elem(pj, G[j], mj, vj, vmj, ams, h, sg.lr, sg.wd);
+            adam_elem(pj, clipped(sg, G[j]), mj, vj, vmj, ams, h, sg.lr, sg.wd);
             P[j] = pj, M[j] = mj, V[j] = vj;
             if (ams)
                 VM[j] = vmj;
@@ -326,6 +342,11 @@ __global__ void __launch_bounds__(kBlock) k_grad_scale(grad_table tab, const flo
     grad_map(tab, blockIdx.x, scale_op{res[3], res[1]});
 }
 
+__global__ void __launch_bounds__(kBlock) k_grad_scale_const(grad_table tab, float mul, float inv)
+{
+    grad_map(tab, blockIdx.x, scale_op{mul, inv});
+}
+
 __global__ void __launch_bounds__(kBlock) k_grad_clamp(grad_table tab, float c)
 {
     grad_map(tab, blockIdx.x, clamp_op{c});
@@ -400,6 +421,22 @@ extern "C" int pgk_grad_norm(const pgk_grad_seg *segs, int nseg, int clip, float
     hipLaunchKernelGGL(k_norm_fin, dim3(1), dim3(kFinBlock), 0, (hipStream_t)s, (const double *)part, off, clip,
                        max_norm, eps, res);
     return status();
+}
+
+extern "C" int pgk_grad_scale_const(const pgk_grad_seg *segs, int nseg, float mul, float inv, pgk_stream s)
+{
+    for (int base = 0; base < nseg; base += PGK_GRAD_MAX_SEG) {
+        const int cnt = nseg - base < PGK_GRAD_MAX_SEG ? nseg - base : PGK_GRAD_MAX_SEG;
+        grad_table tab;
+        const unsigned blocks = grad_table_fill(tab, segs + base, cnt, kMapChunk);
+        if (!blocks)
+            continue;
+        hipLaunchKernelGGL(k_grad_scale_const, dim3(blocks), dim3(kBlock), 0, (hipStream_t)s, tab, mul, inv);
+        const int st = status();
+        if (st)
+            return st;
+    }
+    return 0;
 }
 
 extern "C" int pgk_grad_scale(const pgk_grad_seg *segs, int nseg, const float *res, pgk_stream s)

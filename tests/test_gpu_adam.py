@@ -303,3 +303,88 @@ def test_clip_many_grads_and_large_norm(lib, oracle):
     assert bits(n1) == bits(n2)
     assert abs(n1 - exact) <= np.spacing(np.float32(exact))
     lib.pg_node_free(nb)
+
+
+@pytest.mark.parametrize("opt_kind", ["adamw", "sgd"])
+def test_clip_scale_applied_by_the_step(lib, oracle, opt_kind):
+    """pg_clip_grad_norm leaves its scale pending on the grads' storage and
+    the optimiser applies it as it reads them: clip then step equals the
+    oracle's clip (grads scaled in place) then step, bit for bit, with no
+    read of the grads in between; a second step with the same grads scales
+    them again as the reference's still-scaled grads would; reading the
+    grads, a second clip, or a backward writing them sees the scaled values
+    (or none, when they are overwritten).  Ragged sizes over two launches of
+    the 32-tensor table."""
+    rng = np.random.default_rng(31 + (opt_kind == "sgd"))
+    sizes = [SIZES[i % len(SIZES)] for i in range(36)]
+    ps = [rng.standard_normal(n).astype(np.float32) for n in sizes]
+    gs = [(rng.standard_normal(n) * 2).astype(np.float32) for n in sizes]
+    nodes = [lib.var(p) for p in ps]
+    for n, g in zip(nodes, gs):
+        set_grad(lib, n, g)
+    pa = params_arg(nodes)
+    ref_g = [g.copy() for g in gs]
+    want_norm = oracle.clip_grad_norm(ref_g, 5.0, 1e-6)
+    if opt_kind == "adamw":
+        cfg = (1e-3, 0.9, 0.999, 1e-8, 0.01, False, True)
+        opt = make_adam(lib, cfg, nodes, [(0.0, -1.0)] * len(nodes))
+        ref = OracleAdam(oracle, cfg, [(0.0, -1.0)] * len(nodes), ps)
+        step, free = lib.pg_adam_step, lib.pg_adam_free
+        ref_params = lambda: ref.p  # noqa: E731
+    else:
+        from picograd_amd.capi import SgdCfg
+        opt = lib.pg_sgd_new(C.byref(SgdCfg(0.01, 0.9, 0.0, 1e-4, True)))
+        for n in nodes:
+            assert lib.pg_sgd_add_param(opt, n) == 0
+        rp = [p.copy() for p in ps]
+        rb = [np.zeros_like(p) for p in ps]
+
+        class _R:
+            def run(self, grads):
+                for k, g in enumerate(grads):
+                    oracle.sgd_step(rp[k], g, rb[k], 0.01, 0.9, 0.0, 1e-4, True)
+        ref = _R()
+        step, free = lib.pg_sgd_step, lib.pg_sgd_free
+        ref_params = lambda: rp  # noqa: E731
+    try:
+        got_norm = lib.pg_clip_grad_norm(pa, len(nodes), 5.0, 1e-6)
+        assert bits(got_norm) == bits(want_norm)
+        for s in range(2):  # the same (clipped) grads twice
+            step(opt)
+            ref.run(ref_g)
+            for k, n in enumerate(nodes):
+                assert np.array_equal(bits(lib.value(n)).reshape(-1), bits(ref_params()[k]).reshape(-1)), (s, k)
+        # a reader sees the scaled grads
+        for k, n in enumerate(nodes):
+            assert np.array_equal(bits(lib.grad(n)), bits(ref_g[k])), k
+        # a second clip reads the scaled values
+        want2 = oracle.clip_grad_norm(ref_g, 1.0, 1e-6)
+        assert bits(lib.pg_clip_grad_norm(pa, len(nodes), 1.0, 1e-6)) == bits(want2)
+        step(opt)
+        ref.run(ref_g)
+        for k, n in enumerate(nodes):
+            assert np.array_equal(bits(lib.value(n)).reshape(-1), bits(ref_params()[k]).reshape(-1)), k
+        for k, n in enumerate(nodes):
+            assert np.array_equal(bits(lib.grad(n)), bits(ref_g[k])), k
+    finally:
+        free(opt)
+        for n in nodes:
+            lib.pg_node_free(n)
+
+
+def test_clip_scale_pending_then_backward_overwrites(lib, oracle):
+    """A grad clipped (scale pending) and then written by a backward: the
+    backward's grads replace the values (the pending scale is dropped, not
+    applied to the new grads), as the reference's zeroing of grads at the
+    start of pg_backward (autograd.c:2490-2492) does."""
+    x = np.linspace(-2, 2, 4096, dtype=np.float32).reshape(64, 64)
+    nx = lib.var(x)
+    set_grad(lib, nx, np.full((64, 64), 100.0, np.float32))
+    assert lib.pg_clip_grad_norm(params_arg([nx]), 1, 1.0, 1e-6) > 1.0
+    y = lib.op("tanh", nx)
+    loss = lib.op("sum_all", y)
+    lib.pg_backward(loss)
+    want = 1.0 - np.tanh(x.astype(np.float64)) ** 2
+    assert np.max(np.abs(lib.grad(nx) - want)) <= 1e-6
+    for n in (loss, y, nx):
+        lib.pg_node_free(n)
