@@ -416,6 +416,35 @@ bool pgd_h2d(void *dst, const void *src, size_t nbytes)
            hip_ok(hipStreamSynchronize(g_stream), "hipStreamSynchronize");
 }
 
+/* Small reads (a norm, a loss, one element) come back through a mapped
+ * pinned buffer that the scatter kernel writes on the compute queue: no
+ * copy-engine command and no staging of pageable memory sit between the
+ * producing kernel and the host's wait. */
+#define PGD_READ_BYTES 4096
+static unsigned char *g_read, *g_read_dev;
+static int g_read_state; /* 0 untried, 1 ready, -1 unavailable */
+
+static bool read_ready(void)
+{
+    if (g_read_state)
+        return g_read_state > 0;
+    g_read_state = -1;
+    if (hipHostMalloc((void **)&g_read, PGD_READ_BYTES, hipHostMallocMapped | hipHostMallocCoherent) !=
+        hipSuccess) {
+        (void)hipGetLastError();
+        g_read = NULL;
+        return false;
+    }
+    if (hipHostGetDevicePointer((void **)&g_read_dev, g_read, 0) != hipSuccess) {
+        (void)hipGetLastError();
+        hipHostFree(g_read);
+        g_read = NULL;
+        return false;
+    }
+    g_read_state = 1;
+    return true;
+}
+
 bool pgd_d2h(void *dst, const void *src, size_t nbytes)
 {
     if (!pgd_ok())
@@ -424,6 +453,14 @@ bool pgd_d2h(void *dst, const void *src, size_t nbytes)
         return pgd_sync();
     if (!flush_pending())
         return false;
+    if (nbytes <= PGD_READ_BYTES && read_ready()) {
+        const pgk_upload e = {g_read_dev, src, nbytes};
+        if (!hip_ok((hipError_t)pgk_upload_scatter(&e, 1, (pgk_stream)g_stream), "small read") ||
+            !hip_ok(hipStreamSynchronize(g_stream), "hipStreamSynchronize"))
+            return false;
+        memcpy(dst, g_read, nbytes);
+        return true;
+    }
     return hip_ok(hipMemcpyAsync(dst, src, nbytes, hipMemcpyDeviceToHost, g_stream),
                   "hipMemcpyAsync D2H") &&
            hip_ok(hipStreamSynchronize(g_stream), "hipStreamSynchronize");
