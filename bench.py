@@ -301,16 +301,24 @@ def host_info() -> dict:
     that decide which reference micro-kernels run (backend/cpu/gemm.c:259-360),
     logical CPUs available, glibc, and the compiler and flags of the
     reference build in oracle/_ref."""
-    model, flags = None, set()
+    model, flags, ident = None, set(), {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name") and model is None:
+                key = line.split(":", 1)[0].strip()
+                if key == "model name" and model is None:
                     model = line.split(":", 1)[1].strip()
-                elif line.startswith("flags") and not flags:
+                elif key == "flags" and not flags:
                     flags = set(line.split(":", 1)[1].split())
+                elif key in ("vendor_id", "cpu family", "model", "stepping", "cache size") and key not in ident:
+                    ident[key] = line.split(":", 1)[1].strip()
     except OSError:
         pass
+    # a virtualised host may name only the product line ("AMD EPYC"): the
+    # family / model / stepping numbers identify the part (family 26: Zen 5)
+    if model and ident:
+        model = (f"{model} (vendor {ident.get('vendor_id')}, family {ident.get('cpu family')}, "
+                 f"model {ident.get('model')}, stepping {ident.get('stepping')}, cache {ident.get('cache size')})")
     isa = {k: k in flags for k in ("avx2", "fma", "f16c", "avx512f", "avx512_bf16", "avx512_fp16",
                                    "amx_bf16", "amx_tile")}
     try:
@@ -604,7 +612,7 @@ def bench_c5(L, ev, steps, warmup, dims=C5_DIMS, batch=C5_BATCH, fused=True):
             "steps_run": len(vals)}
 
 
-def cpu_c5(dims=C5_DIMS, batch=C5_BATCH, budget_s=25.0):
+def cpu_c5(dims=C5_DIMS, batch=C5_BATCH, budget_s=40.0):
     """The reference's CPU path for config 5 at full shape in f32 (its matmul
     cannot take bf16 weights with f32 activations): pg_ag_matmul + add +
     gelu layers, mse, pg_backward, pg_sgd_step, timed per step."""
@@ -630,10 +638,15 @@ def cpu_c5(dims=C5_DIMS, batch=C5_BATCH, budget_s=25.0):
     mlp.free()
     R.pg_node_free(x)
     R.pg_node_free(t)
-    sec = float(np.median(times))
+    # the first step also pays the reference's first allocations of every
+    # buffer: left out of the median whenever a later step fits the budget
+    timed = times[1:] if len(times) > 1 else times
+    sec = float(np.median(timed))
     return {"value": 1.0 / sec, "unit": "steps/s", "cores": _ref_threads(),
-            "kind": "reference", "sample": f"{len(times)} full config-5 steps in f32 (first included)",
-            "ms": sec * 1e3}
+            "kind": "reference",
+            "sample": (f"median of {len(timed)} full config-5 steps in f32 after a first step"
+                       if len(times) > 1 else "one full config-5 step in f32 (the only one within the budget)"),
+            "ms": sec * 1e3, "steps_s": times}
 
 
 # ---------------------------------------------------------------- optimiser leg
