@@ -302,3 +302,36 @@ def test_backward_joins_the_small_run(lib, oracle, shape, reuse):
         da, db, dc = oracle.chain1(a.ravel(), b.ravel(), c.ravel())
         for g, want in zip(got[True]["grads"], (da, db, dc)):
             assert np.max(np.abs(g.ravel() - want)) <= 1e-6
+
+
+def test_broadcast_grad_keeps_the_run_and_region_apart(lib):
+    """A run whose backward region reduces a grad onto a broadcast leaf
+    (tanh(x + b), b [cols]) cannot share the one-block kernel (the region's
+    column reduction needs the main kernel): the run and the region launch
+    separately and the grads equal the eager path's within 1e-6."""
+    import ctypes as C
+    rng = np.random.default_rng(77)
+    x = rng.uniform(-1, 1, (64, 64)).astype(np.float32)
+    b = rng.uniform(-1, 1, 64).astype(np.float32)
+    got = {}
+    for jit in (True, False):
+        lib.pg_autograd_set_jit(jit)
+        try:
+            nx, nb = lib.var(x), lib.var(b)
+            y = lib.op("tanh", lib.op("add", nx, nb))
+            loss = lib.op("sum_all", y)
+            lib.pg_amd_timer_reset()
+            lib.pg_amd_timer_enable(1)
+            lib.pg_backward(loss)
+            cnt = C.c_size_t(0)
+            lib.pg_amd_timer_read(0, C.byref(cnt))
+            lib.pg_amd_timer_enable(0)
+            lib.pg_amd_timer_reset()
+            got[jit] = (lib.grad(nx), lib.grad(nb), cnt.value)
+            for n in (loss, y, nb, nx):
+                lib.pg_node_free(n)
+        finally:
+            lib.pg_autograd_set_jit(True)
+    assert got[True][2] == 2  # the run's block, then the region's main kernel
+    for g1, g0 in zip(got[True][:2], got[False][:2]):
+        assert np.max(np.abs(g1 - g0)) <= 1e-6 * max(1.0, float(np.abs(g0).max()))
