@@ -658,19 +658,10 @@ __device__ __forceinline__ void act_bwd_row(const float (&gv)[8], const float (&
     *reinterpret_cast<uint4 *>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
-// Arrival counters of k_act_bwd16's column blocks: the last row block of a
-// column block to finish adds that block's partial rows (the finisher's
-// work, without its launch) and sets the counter back to zero, so every
-// launch finds them zero (zero-initialised with the code object; launches
-// are ordered on the library stream).
-constexpr int kActCounters = 1024;
-__device__ unsigned g_act_cnt[kActCounters];
-
 template <int ACT>
 __global__ void __launch_bounds__(kBlock) k_act_bwd16(const float *__restrict__ g, const float *__restrict__ z,
                                                       size_t m, size_t n, uint16_t *__restrict__ d16, size_t ldd,
-                                                      int dtype, float *__restrict__ part, size_t rpb,
-                                                      float *__restrict__ db, int db_beta)
+                                                      int dtype, float *__restrict__ part, size_t rpb)
 {
     __shared__ float red[16][129];
     const int cx = threadIdx.x & 15, ry = threadIdx.x >> 4;
@@ -741,34 +732,6 @@ __global__ void __launch_bounds__(kBlock) k_act_bwd16(const float *__restrict__ 
             if (col < n)
                 part[(size_t)blockIdx.y * n + col] = sum;
         }
-        if (!db)
-            return;
-        // the last row block of this column block to arrive adds the
-        // partial rows in row-block order (k_colsum_fin's order): the
-        // barrier orders every lane's partial store before lane 0's
-        // device-scope release, and the last block's acquire makes the
-        // other blocks' rows visible to it
-        __shared__ bool last;
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            __threadfence();
-            last = atomicAdd(&g_act_cnt[blockIdx.x], 1u) == gridDim.y - 1;
-        }
-        __syncthreads();
-        if (!last)
-            return;
-        __threadfence();
-        if (threadIdx.x < 128) {
-            const size_t col = (size_t)blockIdx.x * 128 + threadIdx.x;
-            if (col < n) {
-                float acc = 0.0f;
-                for (size_t b = 0; b < gridDim.y; ++b)
-                    acc += part[b * n + col];
-                db[col] = db_beta ? db[col] + acc : acc;
-            }
-        }
-        if (threadIdx.x == 0)
-            g_act_cnt[blockIdx.x] = 0u;
     }
 }
 
@@ -1174,19 +1137,13 @@ extern "C" int pgk_act_bwd16(int act, const float *g, const float *z, size_t m, 
     const unsigned gx = (unsigned)((ldd + 127) / 128);
     float *part = db ? (float *)ws : nullptr;
     const dim3 grid(gx, (unsigned)nrb);
-    // the bias grad is finished by each column block's last row block when
-    // there is a counter for every column block, else by k_colsum_fin
-    float *fold = gx <= (unsigned)kActCounters ? db : nullptr;
     if (act == 0)
-        hipLaunchKernelGGL(k_act_bwd16<0>, grid, dim3(kBlock), 0, (hipStream_t)s, g, z, m, n, d16, ldd, dtype, part, rpb,
-                           fold, db_beta);
+        hipLaunchKernelGGL(k_act_bwd16<0>, grid, dim3(kBlock), 0, (hipStream_t)s, g, z, m, n, d16, ldd, dtype, part, rpb);
     else if (act == 1)
-        hipLaunchKernelGGL(k_act_bwd16<1>, grid, dim3(kBlock), 0, (hipStream_t)s, g, z, m, n, d16, ldd, dtype, part, rpb,
-                           fold, db_beta);
+        hipLaunchKernelGGL(k_act_bwd16<1>, grid, dim3(kBlock), 0, (hipStream_t)s, g, z, m, n, d16, ldd, dtype, part, rpb);
     else
-        hipLaunchKernelGGL(k_act_bwd16<2>, grid, dim3(kBlock), 0, (hipStream_t)s, g, z, m, n, d16, ldd, dtype, part, rpb,
-                           fold, db_beta);
-    if (db && !fold)
+        hipLaunchKernelGGL(k_act_bwd16<2>, grid, dim3(kBlock), 0, (hipStream_t)s, g, z, m, n, d16, ldd, dtype, part, rpb);
+    if (db)
         hipLaunchKernelGGL(k_colsum_fin, dim3((unsigned)((n + 63) / 64)), dim3(64), 0, (hipStream_t)s, part, nrb, n,
                            db, db_beta);
     return status();
