@@ -46,6 +46,13 @@ typedef struct pg_data_ref {
      * library-internal */
     bool clip_pending;
     float clip_mul, clip_inv;
+    /* elements not yet written: each is act(act_src[i]) (act_pending =
+     * PG_ACT_RELU or PG_ACT_GELU; 0: none), act_src's storage held through
+     * act_src_ref until they are (pg_amd_ag_linear16's output, whose GEMM
+     * wrote the pre-activation and the 16-bit copy); library-internal */
+    int act_pending;
+    const float *act_src;
+    struct pg_data_ref *act_src_ref;
 } pg_data_ref;
 
 typedef struct pg_tensor {

@@ -187,6 +187,7 @@ void pg_adam_step(pg_adam *opt)
          * grad's storage for any other reader) */
         if (g->pg_flags & PG_TENSOR_ZERO_PENDING)
             pgt_materialize(g);
+        pgt_settle(p->value); /* the parameter's own elements, if any are pending */
         const pg_data_ref *gr = g->data_ref;
         if (!s->m) {
             /* adam.c:140-153: moments created at zero on first use */

@@ -616,6 +616,7 @@ static const uint16_t *operand16(pg_tensor *t, int dt, size_t rows, size_t cols,
     if (rows == rows_pad && r && t->dev == r->ptr && t->numel == rows * cols && t->numel * 4 == r->nbytes &&
         pgt_is_contiguous(t))
         return pgt_shadow16_rows(t, (pg_dtype)dt, cols, cols_pad);
+    pgt_materialize(t); /* the copy reads the f32 elements */
     *owned = stage16(dt, 0, t->dev, rows, cols, cols, rows_pad, cols_pad, 1, 0, bytes);
     return *owned;
 }
@@ -684,8 +685,12 @@ pg_node *pg_amd_ag_matmul16(pg_node *a, pg_node *b, pg_dtype dtype)
         pga_set_err("matmul16: no device");
         return NULL;
     }
-    pgt_materialize(av);
-    pgt_materialize(bv);
+    /* the operands' f32 elements are read only to make a 16-bit copy
+     * (operand16 settles them then); a current copy is used as it is */
+    if (av->pg_flags & PG_TENSOR_ZERO_PENDING)
+        pgt_materialize(av);
+    if (bv->pg_flags & PG_TENSOR_ZERO_PENDING)
+        pgt_materialize(bv);
     pg_tensor *c = pgt_alloc(PG_DTYPE_F32, 2, (size_t[]){M, N});
     if (!c)
         return NULL;
@@ -870,8 +875,13 @@ pg_node *pg_amd_ag_linear16(pg_node *x, pg_node *w, pg_node *b, int act, pg_dtyp
         pga_set_err("linear16: no device");
         return NULL;
     }
-    pgt_materialize(xv);
-    pgt_materialize(wv);
+    /* x's and W's f32 elements are read only to make a 16-bit copy
+     * (operand16 settles them then): a previous linear16 output whose
+     * elements are still pending is used through its 16-bit copy alone */
+    if (xv->pg_flags & PG_TENSOR_ZERO_PENDING)
+        pgt_materialize(xv);
+    if (wv->pg_flags & PG_TENSOR_ZERO_PENDING)
+        pgt_materialize(wv);
     if (bv)
         pgt_materialize(bv);
     const int dt = (int)dtype;
@@ -891,9 +901,15 @@ pg_node *pg_amd_ag_linear16(pg_node *x, pg_node *w, pg_node *b, int act, pg_dtyp
         r->shadow_stale = true;
         ok = r->shadow != NULL;
     }
+    /* with the pre-activation kept (a grad-mode layer with an activation),
+     * the GEMM writes z and out's 16-bit copy but not out itself: out's
+     * elements stay pending as act(z) until something reads them (the
+     * next layer reads the copy, the backward reads z), and are then
+     * written by one pass with the epilogue's arithmetic */
+    const bool lazy_out = z && act != PGK_ACT_NONE && K && M && N && out->data_ref->shadow;
     if (ok && M && N) {
         pgk_epi epi = {bv ? (const float *)bv->dev : NULL, act, z ? (float *)z->dev : NULL,
-                       out->data_ref->shadow, dt};
+                       out->data_ref->shadow, dt, lazy_out ? 1 : 0};
         if (!K) {
             ok = gemm16x(dt, 0, 1, M, N, 0, NULL, 8, 0, M, NULL, 8, 0, up8(N), out->dev, N, 0, 1, 0, &epi,
                          "linear16");
@@ -912,6 +928,13 @@ pg_node *pg_amd_ag_linear16(pg_node *x, pg_node *w, pg_node *b, int act, pg_dtyp
         }
         if (ok && out->data_ref->shadow)
             out->data_ref->shadow_stale = false;
+        if (ok && lazy_out) {
+            pg_data_ref *r = out->data_ref;
+            r->act_pending = act;
+            r->act_src = z->dev;
+            r->act_src_ref = z->data_ref;
+            z->data_ref->refs++;
+        }
     }
     if (!ok) {
         pga_set_err("linear16: %s", pg_amd_last_error());

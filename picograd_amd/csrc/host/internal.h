@@ -18,11 +18,13 @@
 
 /* pg_tensor.pg_flags */
 #define PG_TENSOR_ZERO_PENDING 1u /* logically zero; device bytes not written */
-/* A clip-by-norm scale pending on a storage (pg_data_ref.clip_pending):
- * pgt_settle writes it to the elements (before any read of them other than
- * by the optimiser kernels, which apply it as they read), pgt_overwrite
- * drops it when all of the storage is about to be written (else settles),
- * pgt_drop_clip drops it (the storage's value is being discarded). */
+/* Values pending on a storage: a clip-by-norm scale (pg_data_ref.clip_pending)
+ * or elements not yet written as act(pre-activation) (act_pending, a
+ * linear16 output).  pgt_settle writes them to the elements (before any
+ * read of them other than by the optimiser kernels, which apply a pending
+ * clip scale as they read), pgt_overwrite drops them when all of the
+ * storage is about to be written (else settles), pgt_drop_clip drops them
+ * (the storage's value is being discarded). */
 bool pgt_settle(const pg_tensor *t);
 void pgt_overwrite(const pg_tensor *t);
 void pgt_drop_clip(const pg_tensor *t);

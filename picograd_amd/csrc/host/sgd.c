@@ -121,6 +121,7 @@ void pg_sgd_step(pg_sgd *opt)
          * grad's storage for any other reader) */
         if (g->pg_flags & PG_TENSOR_ZERO_PENDING)
             pgt_materialize(g);
+        pgt_settle(p->value); /* the parameter's own elements, if any are pending */
         const pg_data_ref *gr = g->data_ref;
         if (c.momentum != 0.0f && !opt->st[i].buf) {
             opt->st[i].buf = pg_tensor_zeros(p->value->ndim, p->value->shape);

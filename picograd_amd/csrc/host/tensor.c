@@ -86,6 +86,7 @@ void pgt_ref_release(pg_data_ref *r)
         pgd_free(r->ptr, r->nbytes);
         if (r->shadow)
             pgd_free(r->shadow, r->shadow_bytes);
+        pgt_ref_release(r->act_src_ref);
         free(r);
     }
 }
@@ -128,23 +129,46 @@ static bool fill_value(pg_tensor *t, float v)
 bool pgt_settle(const pg_tensor *t)
 {
     pg_data_ref *r = t ? t->data_ref : NULL;
-    if (!r || !r->clip_pending)
+    if (!r)
         return true;
+    bool ok = true;
+    if (r->act_pending) {
+        /* the elements act(src), with the GEMM epilogue's arithmetic (the
+         * unary kernel's ReLU and GELU are the same expressions); the 16-bit
+         * copy the epilogue wrote stays current */
+        const int op = r->act_pending == PGK_ACT_RELU ? PGK_RELU : PGK_GELU;
+        r->act_pending = 0;
+        ok = pgd_check(pgk_unary_f32(op, r->act_src, (float *)r->ptr, r->nbytes / 4, 0.0f, 0.0f, pgd_stream()),
+                       "pending activation");
+        pgt_ref_release(r->act_src_ref);
+        r->act_src_ref = NULL;
+        r->act_src = NULL;
+    }
+    if (!r->clip_pending)
+        return ok;
     r->clip_pending = false;
     r->shadow_stale = true;
     const pgk_grad_seg seg = {(float *)r->ptr, r->nbytes / 4};
-    return pgd_check(pgk_grad_scale_const(&seg, 1, r->clip_mul, r->clip_inv, pgd_stream()), "clip scale");
+    return pgd_check(pgk_grad_scale_const(&seg, 1, r->clip_mul, r->clip_inv, pgd_stream()), "clip scale") && ok;
 }
 
 void pgt_drop_clip(const pg_tensor *t)
 {
-    if (t && t->data_ref)
-        t->data_ref->clip_pending = false;
+    pg_data_ref *r = t ? t->data_ref : NULL;
+    if (!r)
+        return;
+    r->clip_pending = false;
+    if (r->act_pending) {
+        r->act_pending = 0;
+        pgt_ref_release(r->act_src_ref);
+        r->act_src_ref = NULL;
+        r->act_src = NULL;
+    }
 }
 
 void pgt_overwrite(const pg_tensor *t)
 {
-    if (!t || !t->data_ref || !t->data_ref->clip_pending)
+    if (!t || !t->data_ref || !(t->data_ref->clip_pending || t->data_ref->act_pending))
         return;
     /* every element of t is about to be written: a pending clip scale of
      * the whole storage is dropped, of a larger storage applied first */

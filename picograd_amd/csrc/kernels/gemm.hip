@@ -546,7 +546,8 @@ __device__ __forceinline__ void gemm16_block(const gemm_kargs &g, int pid, int n
                     o[q] = act_f(epi.act, zv[q]);
                 const size_t off = (size_t)grow * ldc + gcol;
                 if (v4) {
-                    *reinterpret_cast<float4 *>(Cb + off) = make_float4(o[0], o[1], o[2], o[3]);
+                    if (!epi.skip_out)
+                        *reinterpret_cast<float4 *>(Cb + off) = make_float4(o[0], o[1], o[2], o[3]);
                     if (epi.z)
                         *reinterpret_cast<float4 *>(epi.z + off) = make_float4(zv[0], zv[1], zv[2], zv[3]);
                     if (epi.c16)
@@ -557,7 +558,8 @@ __device__ __forceinline__ void gemm16_block(const gemm_kargs &g, int pid, int n
                     for (int q = 0; q < 4; ++q) {
                         if (gcol + q >= N)
                             break;
-                        Cb[off + q] = o[q];
+                        if (!epi.skip_out)
+                            Cb[off + q] = o[q];
                         if (epi.z)
                             epi.z[off + q] = zv[q];
                         if (epi.c16)
@@ -618,7 +620,8 @@ __device__ __forceinline__ void epi_store(const pgk_epi &epi, float *c, size_t o
 {
     const float zv = v + (epi.bias ? epi.bias[col] : 0.0f);
     const float o = act_f(epi.act, zv);
-    c[off] = o;
+    if (!epi.skip_out)
+        c[off] = o;
     if (epi.z)
         epi.z[off] = zv;
     if (epi.c16)
@@ -734,7 +737,8 @@ __global__ void __launch_bounds__(256) k_splitk_sum(splitk_desc d0, splitk_desc 
 #pragma unroll
             for (int e = 0; e < 4; ++e)
                 o[e] = act_f(epi.act, zv[e]);
-            *q = o;
+            if (!epi.skip_out)
+                *q = o;
             if (epi.z)
                 *(f32x4 *)(epi.z + off) = zv;
             if (epi.c16)
@@ -1173,6 +1177,10 @@ extern "C" int pgk_gemm16_cu(int dtype, int ta, int tb, size_t m, size_t n, size
         return 0;
     const bool has_epi = epi && (epi->bias || epi->act != PGK_ACT_NONE || epi->z || epi->c16);
     if (has_epi && (beta || batch != 1 || (epi->c16 && epi->dtype16 != 1 && epi->dtype16 != 2)))
+        return (int)hipErrorInvalidValue;
+    // an unwritten C needs the epilogue on the GEMM or the split-K sum: the
+    // k-tail and empty-k paths apply it over C's accumulated values
+    if (has_epi && epi->skip_out && (!k || k_inkernel(ta, tb, k) != k))
         return (int)hipErrorInvalidValue;
     const int bad = check_gemm_args(ta, tb, m, n, k, a, lda, stride_a, a_extent, b, ldb, stride_b, b_extent, batch);
     if (bad)

@@ -148,6 +148,10 @@ typedef struct {
     float *z;
     uint16_t *c16;
     int dtype16; /* 1 = f16, 2 = bf16 */
+    /* C itself is not written (z and c16 are): the caller materialises
+     * act(z) when C is first read.  Only where the epilogue rides on the
+     * GEMM or the split-K sum (no k-tail, k > 0). */
+    int skip_out;
 } pgk_epi;
 int pgk_gemm16(int dtype, int ta, int tb, size_t m, size_t n, size_t k, const uint16_t *a, size_t lda,
                size_t stride_a, size_t a_extent, const uint16_t *b, size_t ldb, size_t stride_b, size_t b_extent,
