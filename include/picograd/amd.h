@@ -113,6 +113,18 @@ const pg_tensor *pg_amd_linear16_preact(const pg_node *n);
 void pg_amd_linear16_keep_dz(bool keep);
 const pg_tensor *pg_amd_linear16_dz(const pg_node *n);
 
+/* Narrow dgrads of linear16 layers (no counterpart in the reference).  The
+ * dgrad dx = q(dz).q(W)^T of a layer with at most 16 outputs, written into a
+ * grad with no earlier contribution, is formed by a pass that runs the
+ * GEMM's own MFMA sequence per 32 x 32 tile (so dx has the GEMM's bits)
+ * and writes dx once.  When x comes from another linear16 node, that
+ * node's backward forms it in its own activation pass (reading z and the
+ * narrow operands, writing dx and its dz) instead of reading back a
+ * written dx; any other reader of dx before then forms it first.
+ * pg_amd_linear16_narrow(false) turns both off (the GEMM launch, then
+ * the activation pass reading dx); on by default. */
+void pg_amd_linear16_narrow(bool on);
+
 /* JIT compile statistics: programs compiled by hiprtc, and cache lookups
  * that found a loaded kernel. */
 size_t pg_amd_jit_compiles(void);

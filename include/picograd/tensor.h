@@ -53,6 +53,9 @@ typedef struct pg_data_ref {
     int act_pending;
     const float *act_src;
     struct pg_data_ref *act_src_ref;
+    /* elements not yet written: the product of a narrow next layer's dz and
+     * weights (its dgrad), formed by the first reader; library-internal */
+    struct pg_narrow_pending *narrow;
 } pg_data_ref;
 
 typedef struct pg_tensor {

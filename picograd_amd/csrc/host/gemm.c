@@ -746,6 +746,9 @@ typedef struct {
 
 /* pg_amd_linear16_keep_dz: keep each backward's dz on its node (tests) */
 static bool g_keep_dz;
+/* pg_amd_linear16_narrow: narrow dgrads on the VALU, fused into the
+ * producing linear16 node's activation pass when they can be */
+static bool g_narrow = true;
 
 void pgm_linear16_free_ctx(void *ctx)
 {
@@ -758,6 +761,7 @@ void pgm_linear16_free_ctx(void *ctx)
 }
 
 void pg_amd_linear16_keep_dz(bool keep) { g_keep_dz = keep; }
+void pg_amd_linear16_narrow(bool on) { g_narrow = on; }
 
 static const lin16_ctx *lin16_of(const pg_node *n)
 {
@@ -774,6 +778,43 @@ const pg_tensor *pg_amd_linear16_dz(const pg_node *n)
 {
     const lin16_ctx *cx = lin16_of(n);
     return cx ? cx->dz : NULL;
+}
+
+/* The narrow dgrad of a layer with at most 16 outputs (dz16 [M, ld] and
+ * qw [K, ld], ld = 8 or 16), written into a grad taken fresh (beta 0): when
+ * x comes from a linear16 node and gx is the whole of its storage, left
+ * pending on gx (pgt_narrow_release / pgt_settle) for that node's backward,
+ * which forms it in its activation pass; otherwise formed now.  Either way
+ * with the GEMM's MFMA sequence (pgk_act_bwd16n), so the bits are the GEMM's.
+ * Takes *dz_owned / *w_owned (set to NULL) when it keeps them. */
+static void narrow_dgrad(pg_node *px, pg_tensor *gx, pg_tensor *w, const uint16_t *dz16, void **dz_owned,
+                         size_t dzb, pg_data_ref *dz_ref, const uint16_t *qw, uint16_t **w_owned, size_t wb,
+                         size_t M, size_t K, size_t N, size_t ld, int dt)
+{
+    pg_data_ref *r = gx->data_ref;
+    pg_narrow_pending *p = NULL;
+    if (lin16_of(px) && r && !r->narrow && !r->act_pending && !r->clip_pending && gx->dev == r->ptr &&
+        gx->numel * 4 == r->nbytes && pgt_is_contiguous(gx))
+        p = calloc(1, sizeof *p);
+    if (!p) {
+        pgd_check(pgk_act_bwd16n(0, dz16, qw, (int)ld, dt, NULL, gx->dev, NULL, M, K, NULL, up8(K), 0, NULL, 0, NULL,
+                                 pgd_stream()),
+                  "linear16 narrow dgrad");
+        return;
+    }
+    *p = (pg_narrow_pending){.dn = dz16, .wn = qw, .m = M, .n = K, .kw = (int)ld, .dtype = dt};
+    p->own[0] = *dz_owned;
+    p->own_bytes[0] = *dz_owned ? dzb : 0;
+    p->hold[0] = *dz_owned ? NULL : dz_ref;
+    p->own[1] = *w_owned;
+    p->own_bytes[1] = *w_owned ? wb : 0;
+    p->hold[1] = *w_owned ? NULL : w->data_ref;
+    for (int i = 0; i < 2; i++)
+        if (p->hold[i])
+            p->hold[i]->refs++;
+    *dz_owned = NULL;
+    *w_owned = NULL;
+    r->narrow = p;
 }
 
 void pgm_linear16_backward(pg_node *n)
@@ -806,10 +847,42 @@ void pgm_linear16_backward(pg_node *n)
     size_t wsz = db ? pgk_act_bwd16_workspace(M, N) : 0;
     void *ws = wsz ? pgd_scratch(3, wsz) : NULL;
     int tk = pgd_tbegin(PGD_T_STAGE);
-    bool ok = (!wsz || ws) &&
-              pgd_check(pgk_act_bwd16(cx->act, n->grad->dev, cx->z ? cx->z->dev : NULL, M, N, dz16, N8, dt, db,
-                                      dbeta, ws, pgd_stream()),
-                        "linear16 act backward");
+    /* the grad left pending as the next layer's narrow dgrad is formed in
+     * the activation pass, each element used for dz there; the grad itself
+     * stays pending (written by its first reader, dropped by the next write
+     * of the whole grad), its product now over a copy of the narrow weights
+     * the pass makes (an optimiser step may rewrite the layer's own) */
+    pg_data_ref *gr = n->grad->data_ref;
+    pg_narrow_pending *np = gr ? gr->narrow : NULL;
+    bool ok;
+    if (np && np->m == M && np->n == N && n->grad->dev == gr->ptr) {
+        const size_t wsb = N * (size_t)np->kw * 2;
+        uint16_t *wsnap = pgd_malloc(wsb);
+        ok = (!wsz || ws) &&
+             pgd_check(pgk_act_bwd16n(cx->act, np->dn, np->wn, np->kw, np->dtype, wsnap, wsnap ? NULL : n->grad->dev,
+                                      cx->z ? cx->z->dev : NULL, M, N, dz16, N8, dt, db, dbeta, ws, pgd_stream()),
+                       "linear16 act backward (narrow dgrad)");
+        if (ok && wsnap) {
+            if (np->own[1])
+                pgd_free(np->own[1], np->own_bytes[1]);
+            pgt_ref_release(np->hold[1]);
+            np->hold[1] = NULL;
+            np->own[1] = wsnap;
+            np->own_bytes[1] = wsb;
+            np->wn = wsnap;
+        } else {
+            if (wsnap)
+                pgd_free(wsnap, wsb);
+            if (ok) /* written in the pass */
+                pgt_narrow_release(gr);
+        }
+    } else {
+        pgt_settle(n->grad);
+        ok = (!wsz || ws) &&
+             pgd_check(pgk_act_bwd16(cx->act, n->grad->dev, cx->z ? cx->z->dev : NULL, M, N, dz16, N8, dt, db,
+                                     dbeta, ws, pgd_stream()),
+                       "linear16 act backward");
+    }
     pgd_tend(tk);
     /* each grad taken for writing once (that clears a pending zero and
      * fixes beta), then both GEMMs as one whole-chip launch when they pair,
@@ -830,6 +903,11 @@ void pgm_linear16_backward(pg_node *n)
     const uint16_t *qx = gw && !alias ? operand16(x, dt, M, K, M, K8, &ox, &obx) : NULL;
     const pgk_gemm_desc dd = {M, K, N8, dz16, N8, 0, M, qw, N8, 0, K, gx ? gx->dev : NULL, K, 0, 1, bx};
     const pgk_gemm_desc dw = {K, N, M, qx, K8, 0, K8, dz16, N8, 0, N8, gw ? gw->dev : NULL, N, 0, 1, bw};
+    void *dz_owned = keep ? NULL : dz16;
+    if (qw && g_narrow && N <= 16 && !bx && !alias) {
+        narrow_dgrad(px, gx, w, dz16, &dz_owned, dzb, keep ? keep->data_ref : NULL, qw, &ow, obw, M, K, N, N8, dt);
+        qw = NULL; /* formed, or pending on gx */
+    }
     if (!(qw && qx && pair_full(dt, &dd, &dw, "linear16 dgrad + wgrad"))) {
         if (qw)
             gemm16(dt, 0, 0, M, K, N8, dz16, N8, 0, M, qw, N8, 0, K, gx->dev, K, 0, 1, bx, "linear16 dgrad");
@@ -842,8 +920,8 @@ void pgm_linear16_backward(pg_node *n)
         pgd_free(ow, obw);
     if (ox)
         pgd_free(ox, obx);
-    if (!keep)
-        pgd_free(dz16, dzb);
+    if (dz_owned)
+        pgd_free(dz_owned, dzb);
 }
 
 pg_node *pg_amd_ag_linear16(pg_node *x, pg_node *w, pg_node *b, int act, pg_dtype dtype)

@@ -18,9 +18,11 @@
 
 /* pg_tensor.pg_flags */
 #define PG_TENSOR_ZERO_PENDING 1u /* logically zero; device bytes not written */
-/* Values pending on a storage: a clip-by-norm scale (pg_data_ref.clip_pending)
- * or elements not yet written as act(pre-activation) (act_pending, a
- * linear16 output).  pgt_settle writes them to the elements (before any
+/* Values pending on a storage: a clip-by-norm scale (pg_data_ref.clip_pending),
+ * elements not yet written as act(pre-activation) (act_pending, a
+ * linear16 output) or as a narrow product (narrow: a linear16 grad that is
+ * the dgrad of a next layer of at most 16 outputs, formed by this layer's
+ * backward in its activation pass).  pgt_settle writes them to the elements (before any
  * read of them other than by the optimiser kernels, which apply a pending
  * clip scale as they read), pgt_overwrite drops them when all of the
  * storage is about to be written (else settles), pgt_drop_clip drops them
@@ -28,6 +30,19 @@
 bool pgt_settle(const pg_tensor *t);
 void pgt_overwrite(const pg_tensor *t);
 void pgt_drop_clip(const pg_tensor *t);
+/* g = dn . wn^T over an [m, n] f32 storage, dn [m, kw] and wn [n, kw]
+ * 16-bit (pgk_act_bwd16n's operands); the pending state owns up to two
+ * device buffers (freed with pgd_free) and holds up to two storages */
+typedef struct pg_narrow_pending {
+    const uint16_t *dn, *wn;
+    size_t m, n;
+    int kw, dtype;
+    void *own[2];
+    size_t own_bytes[2];
+    pg_data_ref *hold[2];
+} pg_narrow_pending;
+/* releases r's pending narrow product without writing it */
+void pgt_narrow_release(pg_data_ref *r);
 
 /* ---- device layer (device.c) ---- */
 bool pgd_ok(void);                 /* init on first use; false if no device */

@@ -80,9 +80,24 @@ pg_tensor *pgt_alloc(pg_dtype dtype, size_t ndim, const size_t *shape)
     return t;
 }
 
+void pgt_narrow_release(pg_data_ref *r)
+{
+    pg_narrow_pending *p = r ? r->narrow : NULL;
+    if (!p)
+        return;
+    r->narrow = NULL;
+    for (int i = 0; i < 2; i++) {
+        if (p->own[i])
+            pgd_free(p->own[i], p->own_bytes[i]);
+        pgt_ref_release(p->hold[i]);
+    }
+    free(p);
+}
+
 void pgt_ref_release(pg_data_ref *r)
 {
     if (r && --r->refs == 0) {
+        pgt_narrow_release(r);
         pgd_free(r->ptr, r->nbytes);
         if (r->shadow)
             pgd_free(r->shadow, r->shadow_bytes);
@@ -132,6 +147,15 @@ bool pgt_settle(const pg_tensor *t)
     if (!r)
         return true;
     bool ok = true;
+    if (r->narrow) {
+        /* the narrow product with the arithmetic of the fused pass */
+        const pg_narrow_pending *p = r->narrow;
+        r->shadow_stale = true;
+        ok = pgd_check(pgk_act_bwd16n(0, p->dn, p->wn, p->kw, p->dtype, NULL, (float *)r->ptr, NULL, p->m, p->n,
+                                      NULL, (p->n + 7) & ~(size_t)7, 0, NULL, 0, NULL, pgd_stream()),
+                       "pending narrow product");
+        pgt_narrow_release(r);
+    }
     if (r->act_pending) {
         /* the elements act(src), with the GEMM epilogue's arithmetic (the
          * unary kernel's ReLU and GELU are the same expressions); the 16-bit
@@ -158,6 +182,7 @@ void pgt_drop_clip(const pg_tensor *t)
     if (!r)
         return;
     r->clip_pending = false;
+    pgt_narrow_release(r);
     if (r->act_pending) {
         r->act_pending = 0;
         pgt_ref_release(r->act_src_ref);
@@ -168,7 +193,7 @@ void pgt_drop_clip(const pg_tensor *t)
 
 void pgt_overwrite(const pg_tensor *t)
 {
-    if (!t || !t->data_ref || !(t->data_ref->clip_pending || t->data_ref->act_pending))
+    if (!t || !t->data_ref || !(t->data_ref->clip_pending || t->data_ref->act_pending || t->data_ref->narrow))
         return;
     /* every element of t is about to be written: a pending clip scale of
      * the whole storage is dropped, of a larger storage applied first */

@@ -590,8 +590,13 @@ static bool walk(pg_node *loss, const pg_tensor *seed, wmode mode)
             pg_tensor_free(loss->grad);
             loss->grad = NULL;
         }
-        for (size_t k = 0; k < N; k++)
-            pgt_materialize(order.v[k]->grad);
+        /* a grad pending as a narrow product stays so: its first reader
+         * writes it (a training step never reads it) */
+        for (size_t k = 0; k < N; k++) {
+            pg_tensor *g = order.v[k]->grad;
+            if (!(g && g->data_ref && g->data_ref->narrow))
+                pgt_materialize(g);
+        }
     }
 out:
     for (size_t k = 0; k < N; k++)

@@ -735,6 +735,182 @@ __global__ void __launch_bounds__(kBlock) k_act_bwd16(const float *__restrict__ 
     }
 }
 
+// The same pass when the grad g is itself the dgrad of a narrow next layer:
+// g = dn . wn^T with dn [m, kw] and wn [n, kw] 16-bit, kw = ldn = ldw = 8
+// or 16 (a layer of at most 16 outputs, its dz and its weights' copy with
+// zero columns past the real width).  g is formed here with the MFMA
+// sequence k_gemm16 runs for that dgrad -- one v_mfma_f32_32x32x16 on the
+// operands (the upper 8 k zero when kw = 8) from zero accumulators, then
+// three on zeros for the rest of its 64-deep k-tile -- so every g element has
+// the bits the GEMM writes; g is written out as the grad and used at once,
+// so the [m, n] grad is written once and never read back.  A block is four
+// waves over 128 columns, wave w taking columns 32 w .. 32 w + 31 of the
+// block's rows, 64 rows per step (two 32 x 32 products, every load of the
+// step issued first): the products go through a per-wave LDS tile to one
+// half row of 16 columns per lane (rows lane / 2 and lane / 2 + 32), where
+// z is read, g, dz and the column sums formed as in k_act_bwd16 (the lane's
+// rows in order, then the 32 row lanes in order).  Without d16 (and
+// part) the pass is the narrow dgrad alone.
+typedef __bf16 nbf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 nf16x8 __attribute__((ext_vector_type(8)));
+typedef float nf32x16 __attribute__((ext_vector_type(16)));
+
+template <bool F16>
+__device__ __forceinline__ nf32x16 narrow_mfma(const uint4 &a, const uint4 &b, const nf32x16 &c)
+{
+    if constexpr (F16)
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(nf16x8, a), __builtin_bit_cast(nf16x8, b), c,
+                                                      0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(nbf16x8, a),
+                                                       __builtin_bit_cast(nbf16x8, b), c, 0, 0, 0);
+}
+
+constexpr int kNarrowLd = 36; // LDS tile pitch (floats): 16-byte rows
+constexpr int kNarrowT = 2;   // 32-row MFMA tiles per step, every load of a step issued first
+
+template <int ACT, bool F16>
+__global__ void __launch_bounds__(kBlock, 4) k_act_bwd16n(const uint16_t *__restrict__ dn, const uint16_t *__restrict__ wn,
+                                                       int kw, uint16_t *__restrict__ wsnap, float *__restrict__ g,
+                                                       const float *__restrict__ z, size_t m, size_t n,
+                                                       uint16_t *__restrict__ d16, size_t ldd, int dtype,
+                                                       float *__restrict__ part, size_t rpb)
+{
+    constexpr int T = kNarrowT;
+    __shared__ __attribute__((aligned(16))) float tile[4][32 * T][kNarrowLd];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const size_t j0 = (size_t)blockIdx.x * 128 + (size_t)wave * 32;
+    const size_t rb = (size_t)blockIdx.y * rpb, re = rb + rpb < m ? rb + rpb : m;
+    const int h = lane >> 5;
+    const uint4 zero4 = make_uint4(0u, 0u, 0u, 0u);
+    // the weights' fragment: row j0 + lane % 32, k 8 h .. 8 h + 7
+    uint4 bfrag = zero4;
+    {
+        const size_t j = j0 + (lane & 31);
+        if (j < n && 8 * h < kw) {
+            bfrag = *reinterpret_cast<const uint4 *>(wn + j * (size_t)kw + 8 * h);
+            // the first row block copies the weights it read (the pending
+            // product of a grad not written here keeps this copy)
+            if (wsnap && blockIdx.y == 0)
+                *reinterpret_cast<uint4 *>(wsnap + j * (size_t)kw + 8 * h) = bfrag;
+        }
+    }
+    // after the transpose: rows r, r + 32, ... of the step, columns c .. c + 15
+    const int r = lane >> 1, c = 16 * (lane & 1);
+    const size_t jc = j0 + c;
+    const bool vec = jc + 16 <= n && (n & 3) == 0 && ((((uintptr_t)g) | ((uintptr_t)z)) & 15) == 0;
+    float cs[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q)
+        cs[q] = 0.0f;
+    for (size_t i0 = rb; i0 < re; i0 += 32 * T) {
+        // every load of the step first: the dz fragments (rows past re read
+        // row re - 1, zeroed below) and z of the lane's rows
+        uint4 araw[T];
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const size_t ia = i0 + 32 * t + (lane & 31);
+            araw[t] = *reinterpret_cast<const uint4 *>(dn + (ia < re ? ia : re - 1) * (size_t)kw +
+                                                       (8 * h < kw ? 8 * h : 0));
+        }
+        float zv[T][16];
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const size_t i = i0 + 32 * t + r < re ? i0 + 32 * t + r : re - 1;
+            if (ACT && vec) {
+#pragma unroll
+                for (int q = 0; q < 16; q += 4) {
+                    const float4 v = *reinterpret_cast<const float4 *>(z + i * n + jc + q);
+                    zv[t][q] = v.x, zv[t][q + 1] = v.y, zv[t][q + 2] = v.z, zv[t][q + 3] = v.w;
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < 16; ++q)
+                    zv[t][q] = (ACT && jc + q < n) ? z[i * n + jc + q] : 0.0f;
+            }
+        }
+        // the products: tile t is rows i0 + 32 t .. + 31; lane holds column
+        // lane % 32 of rows 8 (e / 4) + 4 h + e % 4
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const uint4 afrag = (i0 + 32 * t + (lane & 31) < re && 8 * h < kw) ? araw[t] : zero4;
+            nf32x16 acc;
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+                acc[e] = 0.0f;
+            acc = narrow_mfma<F16>(afrag, bfrag, acc);
+#pragma unroll
+            for (int s = 1; s < 4; ++s)
+                acc = narrow_mfma<F16>(zero4, zero4, acc);
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+                tile[wave][32 * t + 8 * (e >> 2) + 4 * h + (e & 3)][lane & 31] = acc[e];
+        }
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            float gv[16];
+#pragma unroll
+            for (int q = 0; q < 16; q += 4) {
+                const float4 v = *reinterpret_cast<const float4 *>(&tile[wave][32 * t + r][c + q]);
+                gv[q] = v.x, gv[q + 1] = v.y, gv[q + 2] = v.z, gv[q + 3] = v.w;
+            }
+            const size_t i = i0 + 32 * t + r;
+            const bool row = i < re && jc < n;
+            float d[16];
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const bool in = row && jc + q < n;
+                d[q] = in ? (ACT ? gv[q] * act_grad(ACT, zv[t][q]) : gv[q]) : 0.0f;
+                cs[q] += d[q];
+            }
+            if (!row)
+                continue;
+            if (g && vec) {
+#pragma unroll
+                for (int q = 0; q < 16; q += 4)
+                    *reinterpret_cast<float4 *>(g + i * n + jc + q) =
+                        make_float4(gv[q], gv[q + 1], gv[q + 2], gv[q + 3]);
+            } else if (g) {
+#pragma unroll
+                for (int q = 0; q < 16; ++q)
+                    if (jc + q < n)
+                        g[i * n + jc + q] = gv[q];
+            }
+            if (d16) {
+                // columns past n store zeros; ldd % 8 == 0, so the lane's 16
+                // columns are within ldd whole or by their first 8
+                uint32_t w[8];
+#pragma unroll
+                for (int q = 0; q < 8; ++q)
+                    w[q] = to16x2(dtype, d[2 * q], d[2 * q + 1]);
+                uint4 *dst = reinterpret_cast<uint4 *>(d16 + i * ldd + jc);
+                dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
+                if (jc + 16 <= ldd)
+                    dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+            }
+        }
+        __builtin_amdgcn_wave_barrier(); // every lane has read the tile before the next step writes it
+    }
+    if (part) {
+        // the 32 row lanes of each column half, in row order
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int q = 0; q < 16; q += 4)
+            *reinterpret_cast<float4 *>(&tile[wave][r][c + q]) = make_float4(cs[q], cs[q + 1], cs[q + 2], cs[q + 3]);
+        __builtin_amdgcn_wave_barrier();
+        if (lane < 32) {
+            float sum = 0.0f;
+#pragma unroll 8
+            for (int y = 0; y < 32; ++y)
+                sum += tile[wave][y][lane];
+            const size_t col = j0 + lane;
+            if (col < n)
+                part[(size_t)blockIdx.y * n + col] = sum;
+        }
+    }
+}
+
 __global__ void __launch_bounds__(64) k_colsum_fin(const float *__restrict__ part, size_t nblk, size_t n,
                                                    float *__restrict__ out, int beta)
 {
@@ -1143,6 +1319,46 @@ extern "C" int pgk_act_bwd16(int act, const float *g, const float *z, size_t m, 
         hipLaunchKernelGGL(k_act_bwd16<1>, grid, dim3(kBlock), 0, (hipStream_t)s, g, z, m, n, d16, ldd, dtype, part, rpb);
     else
         hipLaunchKernelGGL(k_act_bwd16<2>, grid, dim3(kBlock), 0, (hipStream_t)s, g, z, m, n, d16, ldd, dtype, part, rpb);
+    if (db)
+        hipLaunchKernelGGL(k_colsum_fin, dim3((unsigned)((n + 63) / 64)), dim3(64), 0, (hipStream_t)s, part, nrb, n,
+                           db, db_beta);
+    return status();
+}
+
+extern "C" int pgk_act_bwd16n(int act, const uint16_t *dn, const uint16_t *wn, int kw, int ndtype, uint16_t *wsnap,
+                              float *g, const float *z, size_t m, size_t n, uint16_t *d16, size_t ldd, int dtype,
+                              float *db, int db_beta, void *ws, pgk_stream s)
+{
+    if (!m || !n)
+        return 0;
+    if ((ldd & 7) || ldd < n || (((uintptr_t)d16) & 15) || (act && !z) || (db && !ws) || act < 0 || act > 2 ||
+        (kw != 8 && kw != 16) || !dn || !wn || (!g && !d16) ||
+        ((((uintptr_t)dn) | ((uintptr_t)wn) | ((uintptr_t)wsnap)) & 15) || (((uintptr_t)g) & 3) ||
+        (ndtype != 1 && ndtype != 2))
+        return (int)hipErrorInvalidValue;
+    const size_t rpb = act_bwd_rpb(m, ldd), nrb = (m + rpb - 1) / rpb;
+    if (nrb > 65535)
+        return (int)hipErrorInvalidValue;
+    const unsigned gx = (unsigned)((ldd + 127) / 128);
+    float *part = db ? (float *)ws : nullptr;
+    const dim3 grid(gx, (unsigned)nrb);
+#define PGK_NARROW(A, F)                                                                                               \
+    hipLaunchKernelGGL((k_act_bwd16n<A, F>), grid, dim3(kBlock), 0, (hipStream_t)s, dn, wn, kw, wsnap, g, z, m, n, d16, \
+                       ldd, dtype, part, rpb)
+    const bool f16 = ndtype == 1;
+    if (act == 0 && f16)
+        PGK_NARROW(0, true);
+    else if (act == 0)
+        PGK_NARROW(0, false);
+    else if (act == 1 && f16)
+        PGK_NARROW(1, true);
+    else if (act == 1)
+        PGK_NARROW(1, false);
+    else if (f16)
+        PGK_NARROW(2, true);
+    else
+        PGK_NARROW(2, false);
+#undef PGK_NARROW
     if (db)
         hipLaunchKernelGGL(k_colsum_fin, dim3((unsigned)((n + 63) / 64)), dim3(64), 0, (hipStream_t)s, part, nrb, n,
                            db, db_beta);

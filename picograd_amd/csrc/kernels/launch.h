@@ -213,6 +213,16 @@ int pgk_gemm_f32(int ta, int tb, size_t m, size_t n, size_t k, const float *a, s
 size_t pgk_act_bwd16_workspace(size_t m, size_t n);
 int pgk_act_bwd16(int act, const float *g, const float *z, size_t m, size_t n, uint16_t *d16, size_t ldd,
                   int dtype, float *db, int db_beta, void *ws, pgk_stream s);
+/* The same pass with g formed in it as the dgrad of a narrow next layer:
+ * g = dn . wn^T, dn [m, kw] and wn [n, kw] 16-bit of ndtype (kw 8 or 16,
+ * zero columns past the layer's width), with the MFMA sequence of
+ * pgk_gemm16's dgrad of those operands (the same bits), used for dz and,
+ * when g is given, written to g [m, n] (every element).  With wsnap, wn is
+ * copied there (n x kw).  ws as for pgk_act_bwd16.  With d16 and db NULL
+ * only g is written (the narrow dgrad itself); g and d16 are not both NULL. */
+int pgk_act_bwd16n(int act, const uint16_t *dn, const uint16_t *wn, int kw, int ndtype, uint16_t *wsnap, float *g,
+                   const float *z, size_t m, size_t n, uint16_t *d16, size_t ldd, int dtype, float *db, int db_beta,
+                   void *ws, pgk_stream s);
 
 /* multi-tensor SGD */
 typedef struct {
