@@ -242,3 +242,39 @@ def test_pending_grad_keeps_the_weights_it_was_formed_with(lib, oracle, keep_dz)
         lib.pg_tensor_free(seed)
         for n in (out, h, nx, n1w, n2w):
             lib.pg_node_free(n)
+
+
+@pytest.mark.parametrize("M,N,act", [(2730, 20, RELU), (4096, 16, NONE), (1, 3, RELU), (257, 1000, RELU),
+                                     (4096, 10, GELU)])
+def test_small_activation_pass(lib, oracle, keep_dz, M, N, act):
+    """The activation pass at narrow and ragged widths (ldd 8 to 1000, one
+    row up to 4096): dz bit for bit (ReLU, none), within one ulp (GELU), db
+    within the summation bound."""
+    print(f"small activation pass M={M} N={N} act={act}", flush=True)
+    rng = np.random.default_rng(M * 7 + N)
+    dt = BF16
+    K = 24
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w = (rng.standard_normal((K, N)) / np.sqrt(K)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(N)).astype(np.float32)
+    g = rng.standard_normal((M, N)).astype(np.float32)
+    nx, nw, nb = lib.var(x), lib.var(w), lib.var(b)
+    out = lib._check(lib.pg_amd_ag_linear16(nx, nw, nb, act, dt))
+    seed = lib.tensor(g)
+    lib.pg_amd_backward_from(out, seed)
+    dz = _kept_dz(lib, out, N)
+    if act == NONE:
+        d = g
+        assert np.array_equal(dz, oracle.cast16(dt, d))
+    else:
+        z = lib.read(lib.pg_amd_linear16_preact(out))
+        if act == RELU:
+            d = g * (z > 0).astype(np.float32)
+            assert np.array_equal(dz, oracle.cast16(dt, d))
+        else:
+            d = oracle.gelu_backward(z, g)
+            assert _dz_within_one_ulp(dz, oracle.cast16(BF16, d), z, g) <= 1e-3
+    assert np.all(np.abs(lib.grad(nb) - d.astype(np.float64).sum(axis=0)) <= dbias_bound(d, 128))
+    lib.pg_tensor_free(seed)
+    for n in (out, nx, nw, nb):
+        lib.pg_node_free(n)
