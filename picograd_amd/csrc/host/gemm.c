@@ -971,7 +971,7 @@ pg_node *pg_amd_ag_linear16(pg_node *x, pg_node *w, pg_node *b, int act, pg_dtyp
     bool ok = out && cx && (z || !grad || act == PGK_ACT_NONE);
     /* out's 16-bit copy, kept as its shadow (rows of N need N % 8 == 0 to be
      * a GEMM operand in place) */
-    if (ok && N % 8 == 0 && M * N) {
+    if (ok && N % 8 == 0 && M * N != 0) {
         pg_data_ref *r = out->data_ref;
         r->shadow = pgd_malloc(M * N * 2);
         r->shadow_bytes = M * N * 2;
