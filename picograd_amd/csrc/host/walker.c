@@ -590,11 +590,15 @@ static bool walk(pg_node *loss, const pg_tensor *seed, wmode mode)
             pg_tensor_free(loss->grad);
             loss->grad = NULL;
         }
-        /* a grad pending as a narrow product stays so: its first reader
-         * writes it (a training step never reads it) */
+        /* a grad pending as a narrow product over the copy of the weights
+         * its consumer's pass made stays so: its first reader writes it (a
+         * training step never reads it).  One still over the layer's own
+         * 16-bit weights (its consumer did not run) is written now: an
+         * optimiser step may rewrite those */
         for (size_t k = 0; k < N; k++) {
             pg_tensor *g = order.v[k]->grad;
-            if (!(g && g->data_ref && g->data_ref->narrow))
+            const pg_narrow_pending *np = g && g->data_ref ? g->data_ref->narrow : NULL;
+            if (!np || np->hold[1])
                 pgt_materialize(g);
         }
     }
