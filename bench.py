@@ -504,7 +504,9 @@ def c5_counts(dims=C5_DIMS, batch=C5_BATCH):
     """GEMM FLOP per step (forward, wgrad of every layer, dgrad of layers
     2..L) and SGD bytes (p, buf read + write, g read = 20 B per parameter,
     plus the 2 B bf16 weight copy written for each weight the GEMMs read
-    unpadded)."""
+    unpadded).  The last layer's dgrad (0.34 GFLOP of 894) is formed inside
+    the activation pass of the layer before it, so its time falls in
+    act_bwd_ms_per_step, not in gemm_ms_per_step."""
     kn = [dims[i] * dims[i + 1] for i in range(len(dims) - 1)]
     fwd = 2 * batch * sum(kn)
     bwd = 2 * batch * sum(kn) + 2 * batch * sum(kn[1:])
