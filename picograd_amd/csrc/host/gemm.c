@@ -635,28 +635,33 @@ static void mm16_backward(pg_node *n)
     uint16_t *g16 = stage16(dt, 0, g->dev, M, N, N, M, N8, 1, 0, &gbytes);
     if (!g16)
         return;
-    if (pa->requires_grad) {
-        int beta;
-        pg_tensor *ga = pga_grad_for_write(pa, &beta);
-        uint16_t *own;
-        size_t ob;
-        const uint16_t *qb = operand16(b, dt, K, N, K, N8, &own, &ob);
-        if (ga && qb)
-            gemm16(dt, 0, 0, M, K, N8, g16, N8, 0, M, qb, N8, 0, K, ga->dev, K, 0, 1, beta, "matmul16 dgrad");
-        if (own)
-            pgd_free(own, ob);
+    /* each grad taken for writing once, then both GEMMs as one whole-chip
+     * launch when they pair (as linear16's backward does), else one after
+     * the other; a and b in one storage (a.a) share one grad and one kept
+     * copy, so then each operand is taken right before its GEMM and dgrad
+     * runs first (it holds the grad's first beta) */
+    int ba = 0, bb = 0;
+    pg_tensor *ga = pa->requires_grad ? pga_grad_for_write(pa, &ba) : NULL;
+    pg_tensor *gb = pb->requires_grad ? pga_grad_for_write(pb, &bb) : NULL;
+    const bool alias = a->data_ref == b->data_ref || (ga && gb && (ga == gb || ga->data_ref == gb->data_ref));
+    uint16_t *ownb = NULL, *owna = NULL;
+    size_t obb = 0, oba = 0;
+    const uint16_t *qb = ga ? operand16(b, dt, K, N, K, N8, &ownb, &obb) : NULL;
+    const uint16_t *qa = gb && !alias ? operand16(a, dt, M, K, M, K8, &owna, &oba) : NULL;
+    const pgk_gemm_desc dd = {M, K, N8, g16, N8, 0, M, qb, N8, 0, K, ga ? ga->dev : NULL, K, 0, 1, ba};
+    const pgk_gemm_desc dw = {K, N, M, qa, K8, 0, K8, g16, N8, 0, N8, gb ? gb->dev : NULL, N, 0, 1, bb};
+    if (!(qb && qa && pair_full(dt, &dd, &dw, "matmul16 dgrad + wgrad"))) {
+        if (qb)
+            gemm16(dt, 0, 0, M, K, N8, g16, N8, 0, M, qb, N8, 0, K, ga->dev, K, 0, 1, ba, "matmul16 dgrad");
+        if (gb && alias)
+            qa = operand16(a, dt, M, K, M, K8, &owna, &oba);
+        if (qa)
+            gemm16(dt, 1, 1, K, N, M, qa, K8, 0, K8, g16, N8, 0, N8, gb->dev, N, 0, 1, bb, "matmul16 wgrad");
     }
-    if (pb->requires_grad) {
-        int beta;
-        pg_tensor *gb = pga_grad_for_write(pb, &beta);
-        uint16_t *own;
-        size_t ob;
-        const uint16_t *qa = operand16(a, dt, M, K, M, K8, &own, &ob);
-        if (gb && qa)
-            gemm16(dt, 1, 1, K, N, M, qa, K8, 0, K8, g16, N8, 0, N8, gb->dev, N, 0, 1, beta, "matmul16 wgrad");
-        if (own)
-            pgd_free(own, ob);
-    }
+    if (ownb)
+        pgd_free(ownb, obb);
+    if (owna)
+        pgd_free(owna, oba);
     pgd_free(g16, gbytes);
 }
 
