@@ -133,7 +133,9 @@ size_t pg_amd_jit_cache_hits(void);
 /* The launch plan of a 16-bit MFMA GEMM C[m, n] over a reduction of k
  * (batch entries of it), as the library's GEMM paths choose it (a
  * measurement and test aid): returns the tile (1: 128 x 128, four waves;
- * 2: 256 x 256, eight waves; 3: 128 x 256, eight waves), stores the
+ * 2: 256 x 256, eight waves; 3: 128 x 256, eight waves; 4: the skinny
+ * kernel for n <= 16 with B MN-contiguous and at least 1009 rows, 16 rows
+ * of C per block, one launch with no split), stores the
  * split-K factor (1 = none) in *splits and the planner's time estimate in
  * seconds in *seconds (either may be NULL).  cu_budget: the CUs the launch
  * may occupy when it shares the chip with another (a matmul's dgrad and

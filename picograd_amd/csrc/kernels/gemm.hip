@@ -628,6 +628,152 @@ __device__ __forceinline__ void epi_store(const pgk_epi &epi, float *c, size_t o
         epi.c16[off] = to16(epi.dtype16, o);
 }
 
+// Skinny product: C[m, n] (+)= A . B for n <= 16 with B MN-contiguous
+// (b[p * ldb + j]), A K-contiguous (TA false: the forward x . W of a narrow
+// layer) or MN-contiguous (TA true: a narrow layer's weight grad x^T . dz).
+// Such a product streams A once, so split-K's partials and summing launch
+// dominated it.  A block owns 16 rows of C (256 blocks for 4096 rows: every
+// CU streams) and its eight waves split the reduction into runs of 64-deep
+// chunks, each wave with a three-stage ring of its own in LDS (no block
+// barrier in the k-loop: a wave waits only on its own loads; two chunks
+// ahead measured faster than four).  The 32 x 32 x 16 MFMA holds the 16 rows and 16
+// columns in a quarter of its outputs: its other rows and columns read
+// duplicates or zeros and are never stored.  The waves' partial products
+// are added through LDS in wave order, then each element goes through the
+// plain store (beta) or the forward epilogue.
+constexpr int kSkWaves = 8, kSkStages = 3, kSkRows = 16;
+constexpr int kSkA = kSkRows * 64 / 8, kSkB = 64 * 16 / 8; // uint4 of one A and one B stage
+
+template <bool TA, bool F16>
+__global__ void __launch_bounds__(kSkWaves * 64, 1)
+    k_skinny(const uint16_t *__restrict__ A, size_t lda, int a_extent, const uint16_t *__restrict__ B, size_t ldb,
+             int b_extent, float *__restrict__ C, size_t ldc, int m, int n, int k, int beta, pgk_epi epi, int has_epi)
+{
+    __shared__ uint4 smem[kSkWaves * kSkStages * (kSkA + kSkB)];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    // consecutive row tiles on one XCD: with A MN-contiguous four tiles
+    // share each 128-byte line of a row
+    int pid = (int)blockIdx.x;
+    const int nb = (int)gridDim.x;
+    if ((nb & 7) == 0)
+        pid = (pid & 7) * (nb >> 3) + (pid >> 3);
+    const int r0 = pid * kSkRows;
+    LDS uint4 *const ring = (LDS uint4 *)smem + wave * kSkStages * (kSkA + kSkB);
+    // this wave's run of chunks; loads at k >= kend read the zero page
+    const int nct = (k + 63) / 64, cpw = (nct + kSkWaves - 1) / kSkWaves, c0 = wave * cpw;
+    const int nc = nct - c0 < cpw ? (nct - c0 > 0 ? nct - c0 : 0) : cpw;
+    const int kend = (c0 + nc) * 64 < k ? (c0 + nc) * 64 : k;
+    using TK = TileK<kSkRows, 64, 64>;
+    static_assert(TK::NQ == 2, "two loads of 8 rows x 128 bytes per A stage");
+    constexpr int LPT = 4; // loads per chunk: two of A, two of B
+    auto load = [&](int c, int st) {
+        LDS uint4 *sa = ring + st * (kSkA + kSkB), *sb = sa + kSkA;
+        const int k0 = (c0 + c) * 64;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            if constexpr (!TA) {
+                TK::load_q(q, A, lda, r0, a_extent, k0, kend, sa, lane);
+            } else {
+                // [64 p][16 i]: two 16-byte chunks per p-row
+                const int slot = q * 64 + lane, p = slot >> 1;
+                int i = r0 + (slot & 1) * 8;
+                i = i < a_extent ? i : a_extent - 8;
+                const void *src = k0 + p < kend ? (const void *)(A + (size_t)(k0 + p) * lda + i) : (const void *)&g_zero16;
+                dma16(src, sa + q * 64);
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            // [64 p][16 j]: two 16-byte chunks per p-row
+            const int slot = q * 64 + lane, p = slot >> 1, j = (slot & 1) * 8;
+            const void *src =
+                k0 + p < kend && j < b_extent ? (const void *)(B + (size_t)(k0 + p) * ldb + j) : (const void *)&g_zero16;
+            dma16(src, sb + q * 64);
+        }
+    };
+    // ds_read_b64_tr_b16 pair over a [64][16] tile (32-byte rows): in 16-lane
+    // group g, source lane q points at [k0 + q / 4][4 (q % 4)] and result lane
+    // i holds column i, k = k0 .. k0 + 7 (k0 = 16 s + 8 (g >> 1))
+    auto tr_frag = [&](const LDS uint4 *st, int s) {
+        const int g = (lane >> 4) & 3, q = lane & 15;
+        uint2 h2[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int p = 16 * s + 8 * (g >> 1) + 4 * h + (q >> 2);
+            h2[h] = __builtin_bit_cast(
+                uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((LDS v4s *)((const LDS char *)st + p * 32 + (q & 3) * 8)));
+        }
+        return make_uint4(h2[0].x, h2[0].y, h2[1].x, h2[1].y);
+    };
+    // lanes of B columns 0 .. 15 (the rest hold columns 16 .. 31: zero)
+    const bool bcol = ((lane >> 4) & 1) == 0;
+    f32x16 acc;
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+        acc[e] = 0.0f;
+    if (nc > 0) {
+#pragma unroll
+        for (int s = 0; s < kSkStages; ++s)
+            load(s, s);
+        for (int c = 0; c < nc; ++c) {
+            const int st = c % kSkStages;
+            const LDS uint4 *sa = ring + st * (kSkA + kSkB), *sb = sa + kSkA;
+            // chunk c landed (the newest kSkStages - 1 chunks may be in flight)
+            __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0_imm((kSkStages - 1) * LPT));
+            __asm__ volatile("" ::: "memory");
+            uint4 af[4], bf[4];
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                if constexpr (!TA) {
+                    // rows lane % 16 (lanes 16 .. 31 of each half repeat them)
+                    const int r = lane & 15;
+                    const u32x4 v = ((const LDS u32x4 *)sa)[r * TK::CH + TK::swz(2 * s + (lane >> 5), r)];
+                    af[s] = __builtin_bit_cast(uint4, v);
+                } else {
+                    af[s] = tr_frag(sa, s);
+                }
+                const uint4 b = tr_frag(sb, s);
+                bf[s] = bcol ? b : make_uint4(0u, 0u, 0u, 0u);
+            }
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+                acc = mfma32<F16>(af[s], bf[s], acc);
+            // the stage's reads are done before its refill
+            __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0_imm(63));
+            __asm__ volatile("" ::: "memory");
+            load(c + kSkStages, st);
+        }
+        __builtin_amdgcn_s_waitcnt(vmcnt_lgkm0_imm(0));
+    }
+    // the waves' partials through LDS (the rings are done), added in wave
+    // order; output rows 8 (e / 4) + 4 (lane / 32) + e % 4 < 16 are e < 8
+    __syncthreads();
+    constexpr int RP = 17;
+    LDS float *red = (LDS float *)smem;
+    static_assert(kSkWaves * kSkRows * RP * 4 <= (int)sizeof(smem), "partials fit the rings");
+    const int col = lane & 31, lk = lane >> 5;
+    if (col < 16) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            red[(wave * kSkRows + (e >> 2) * 8 + lk * 4 + (e & 3)) * RP + col] = acc[e];
+    }
+    __syncthreads();
+    static_assert(kSkWaves * 64 >= kSkRows * 16, "a thread per element of the block's rows");
+    const int t = (int)threadIdx.x, row = t >> 4, j = t & 15, gr = r0 + row;
+    if (row < kSkRows && gr < m && j < n) {
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kSkWaves; ++w)
+            v += red[(w * kSkRows + row) * RP + j];
+        const size_t off = (size_t)gr * ldc + j;
+        if (has_epi)
+            epi_store(epi, C, off, j, v);
+        else
+            C[off] = beta ? C[off] + v : v;
+    }
+}
+
 // the same epilogue as a pass over a finished C (k-tail runs)
 __global__ void __launch_bounds__(256) k_bias_act(float *__restrict__ c, size_t ldc, int m, int n, pgk_epi epi)
 {
@@ -1104,6 +1250,15 @@ static gemm_plan plan_gemm(size_t m, size_t n, size_t kin, size_t batch, int cu_
 // zero-padded slabs in one more launch
 static size_t k_inkernel(int ta, int tb, size_t k) { return (ta && tb) || k % 8 == 0 ? k : k - k % BK; }
 
+// k_skinny's products: at most 16 columns of C from an MN-contiguous B, one
+// problem, a reduction it covers whole (any k with both operands
+// MN-contiguous, k % 8 == 0 with A K-contiguous), and rows enough for 64 of
+// its 16-row blocks; the rest keep the tiled plans (split-K among them)
+static bool skinny_ok(int ta, int tb, size_t m, size_t n, size_t k, size_t batch)
+{
+    return tb && n <= 16 && batch == 1 && k && (ta || k % 8 == 0) && (m + 15) / 16 >= 64;
+}
+
 static size_t tail_ws(int ta, int tb, size_t m, size_t n, size_t k, size_t batch)
 {
     if (k_inkernel(ta, tb, k) == k)
@@ -1134,6 +1289,8 @@ int check_gemm_args(int ta, int tb, size_t m, size_t n, size_t k, const uint16_t
 
 extern "C" size_t pgk_gemm16_workspace_cu(int ta, int tb, size_t m, size_t n, size_t k, size_t batch, int cu_budget)
 {
+    if (skinny_ok(ta, tb, m, n, k, batch))
+        return 0;
     const gemm_plan pl = plan_gemm(m, n, k_inkernel(ta, tb, k), batch, cu_budget);
     const size_t part = pl.sp > 1 ? (((size_t)pl.sp * m * n * sizeof(float) + 255) & ~(size_t)255) : 0;
     return part + tail_ws(ta, tb, m, n, k, batch);
@@ -1146,6 +1303,11 @@ extern "C" size_t pgk_gemm16_workspace(int ta, int tb, size_t m, size_t n, size_
 
 extern "C" int pgk_gemm16_plan(int ta, int tb, size_t m, size_t n, size_t k, size_t batch, int cu_budget, int *splits)
 {
+    if (skinny_ok(ta, tb, m, n, k, batch)) {
+        if (splits)
+            *splits = 1;
+        return 4;
+    }
     const gemm_plan pl = plan_gemm(m, n, k_inkernel(ta, tb, k), batch, cu_budget);
     if (splits)
         *splits = pl.sp;
@@ -1154,6 +1316,8 @@ extern "C" int pgk_gemm16_plan(int ta, int tb, size_t m, size_t n, size_t k, siz
 
 extern "C" double pgk_gemm16_time(int ta, int tb, size_t m, size_t n, size_t k, size_t batch, int cu_budget)
 {
+    if (skinny_ok(ta, tb, m, n, k, batch)) // A streamed once at ~5 TB/s, one launch
+        return (double)(m * k * 2 + k * 32 + m * n * 4) / 5.0e12 + 5e-6;
     double t = 0.0;
     plan_gemm(m, n, k_inkernel(ta, tb, k), batch, cu_budget, &t);
     return t;
@@ -1196,6 +1360,27 @@ extern "C" int pgk_gemm16_cu(int dtype, int ta, int tb, size_t m, size_t n, size
                                (int)m, (int)n);
         if (has_epi)
             hipLaunchKernelGGL(k_bias_act, dim3(gmn), dim3(256), 0, st, c, ldc, (int)m, (int)n, *epi);
+        return (int)hipGetLastError();
+    }
+    if (skinny_ok(ta, tb, m, n, k, batch)) {
+        const dim3 grid((unsigned)((m + 15) / 16));
+        const pgk_epi e = has_epi ? *epi : pgk_epi{};
+        const int he = has_epi ? 1 : 0;
+        if (ta) {
+            if (f16)
+                hipLaunchKernelGGL((k_skinny<true, true>), grid, dim3(kSkWaves * 64), 0, st, a, lda, (int)a_extent, b, ldb,
+                                   (int)b_extent, c, ldc, (int)m, (int)n, (int)k, beta, e, he);
+            else
+                hipLaunchKernelGGL((k_skinny<true, false>), grid, dim3(kSkWaves * 64), 0, st, a, lda, (int)a_extent, b, ldb,
+                                   (int)b_extent, c, ldc, (int)m, (int)n, (int)k, beta, e, he);
+        } else {
+            if (f16)
+                hipLaunchKernelGGL((k_skinny<false, true>), grid, dim3(kSkWaves * 64), 0, st, a, lda, (int)a_extent, b, ldb,
+                                   (int)b_extent, c, ldc, (int)m, (int)n, (int)k, beta, e, he);
+            else
+                hipLaunchKernelGGL((k_skinny<false, false>), grid, dim3(kSkWaves * 64), 0, st, a, lda, (int)a_extent, b, ldb,
+                                   (int)b_extent, c, ldc, (int)m, (int)n, (int)k, beta, e, he);
+        }
         return (int)hipGetLastError();
     }
     const gemm_plan pl = plan_gemm(m, n, kmain, batch, cu_budget);
@@ -1288,8 +1473,10 @@ extern "C" int pgk_gemm16_pair_dw(int dtype, const pgk_gemm_desc *d, const pgk_g
                               w->stride_b, w->b_extent, w->batch);
     if (bad)
         return bad;
-    // one launch covers each problem: no k tail, one tile size for both
-    if (k_inkernel(0, 0, d->k) != d->k || k_inkernel(1, 1, w->k) != w->k)
+    // one launch covers each problem: no k tail, one tile size for both (a
+    // skinny wgrad runs alone)
+    if (k_inkernel(0, 0, d->k) != d->k || k_inkernel(1, 1, w->k) != w->k ||
+        skinny_ok(1, 1, w->m, w->n, w->k, w->batch))
         return PGK_GEMM_NOT_PAIRED;
     const gemm_plan pd = plan_gemm(d->m, d->n, d->k, d->batch, cu_d), pw = plan_gemm(w->m, w->n, w->k, w->batch,
                                                                                       kCUs - cu_d);

@@ -211,8 +211,8 @@ def test_gemm_launch_plans_of_the_configs():
     layers: their dgrad and wgrad then pair in one launch), the 128 x 256 tile for config 4's ragged grads on their shares
     of the chip (160 CUs for dgrad, 96 for wgrad: both then run without
     split-K, in one launch), 128 x 256 tiles split two ways for config 5's
-    first-layer wgrad and split-K over 128 x 128 tiles for its 10-wide
-    layer."""
+    first-layer wgrad and the skinny kernel (one launch, no split) for its
+    10-wide layer's forward and wgrad."""
     lib = picograd_amd.load()
     assert _plan(lib, 0, 0, 8192, 4096, 4096) == (2, 1)    # config 3 dgrad
     assert _plan(lib, 1, 1, 4096, 4096, 8192) == (2, 1)    # config 3 wgrad
@@ -222,7 +222,9 @@ def test_gemm_launch_plans_of_the_configs():
     assert _plan(lib, 0, 0, 4096, 4096, 4096) == (2, 1)
     assert _plan(lib, 1, 1, 4096, 4096, 4096) == (2, 1)
     assert _plan(lib, 1, 1, 1024, 4096, 4096) == (3, 2)    # config 5 first-layer wgrad
-    assert _plan(lib, 0, 1, 4096, 10, 4096) == (1, 8)      # config 5 10-wide forward
+    assert _plan(lib, 0, 1, 4096, 10, 4096) == (4, 1)      # config 5 10-wide forward: skinny kernel
+    assert _plan(lib, 1, 1, 4096, 10, 4096) == (4, 1)      # config 5 10-wide wgrad: skinny kernel
+    assert _plan(lib, 0, 1, 512, 10, 4096) == (1, 8)       # too few rows for it: split-K
     assert _plan(lib, 0, 0, 4097, 1000, 3000, cus=160) == (3, 1)  # config 4 dgrad
     assert _plan(lib, 1, 1, 1000, 3000, 4097, cus=96) == (3, 1)   # config 4 wgrad
     assert _plan(lib, 0, 0, 512, 128, 512, batch=32, cus=128) == (1, 1)  # config 4 bmm grads

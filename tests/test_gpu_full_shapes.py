@@ -300,9 +300,10 @@ def _round(oracle, dt, x):
 @pytest.mark.parametrize("N", [10, 33])
 def test_splitk_narrow_weight_grad_accumulates(lib, oracle, dt, N):
     """dW = q(X1)^T.q(G1) + q(X2)^T.q(G2) for one W [1024, N] used by two
-    matmul16 nodes over 4096-row batches: each wgrad (m = 1024, n = N,
-    k = 4096) runs split-K, and n % 4 != 0 sends the partial sums through
-    k_splitk_sum's one-element-per-thread path, the second with beta = 1."""
+    matmul16 nodes over 4096-row batches, the second wgrad with beta = 1.
+    Each wgrad (m = 1024, n = N, k = 4096) runs in the skinny kernel for
+    N = 10; for N = 33 it runs split-K, and n % 4 != 0 sends the partial sums
+    through k_splitk_sum's one-element-per-thread path."""
     B, K = 4096, 1024
     print(f"split-K narrow wgrad dt={dt} N={N}", flush=True)
     rng = np.random.default_rng(N)

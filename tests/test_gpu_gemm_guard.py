@@ -9,8 +9,10 @@ The whole buffer starts as a NaN sentinel; afterwards the guard rows and
 slack columns must hold the sentinel bit for bit, and every element of C
 must match the f64 product of the same operands within the f32 summation
 bound (gemm_check.check_product).  Shapes: the ragged M = 4097 with
-N = 10 and 33 (split-K outputs summed one element per thread) and
-N = 3000, every operand layout (forward, dgrad, wgrad), K % 64 != 0 and
+N = 10 and 33 (the skinny kernel for at most 16 columns, split-K outputs
+summed one element per thread past that) and N = 3000, the skinny kernel at
+widths 1 to 16 and reductions from 8 to 9000, every operand layout
+(forward, dgrad, wgrad), K % 64 != 0 and
 K % 8 != 0 (the zero-page tail and the padded k-slab launch), beta 0 and
 beta 1, the whole chip and a CU budget, and the paired dgrad + wgrad launch
 (split between CUs, and whole-chip).
@@ -159,6 +161,15 @@ CASES = [
     (F16, 0, 0, 4097, 3000, 1000, 0, 0),
     (F16, 1, 1, 1000, 3000, 4097, 1, 96),
     (BF16, 0, 1, 4097, 3000, 1004, 0, 160),
+    # the skinny kernel (n <= 16, B MN-contiguous, 64 or more 16-row
+    # blocks; the 1000-row cases above take split-K): widths 1, 8 and 16, a
+    # reduction shorter than one chunk, one ending mid-chunk, a long one,
+    # config 5's 10-wide weight grad, beta 1
+    (F16, 0, 1, 1040, 16, 136, 1, 0),
+    (BF16, 0, 1, 2048, 1, 8, 0, 0),
+    (BF16, 1, 1, 4096, 10, 4096, 0, 0),
+    (F16, 1, 1, 1032, 8, 77, 0, 0),
+    (BF16, 1, 1, 1024, 16, 9000, 1, 0),
 ]
 
 

@@ -1,12 +1,14 @@
-"""Forward products with a narrow output (n <= 16 columns, as config 5's
-10-wide layer), which the launch plan runs as split-K over 128 x 128 MFMA
-tiles with the epilogue applied by the summing launch.  Each output against
-the f32-accumulating product of the same 16-bit operands (identical
-operands, only the summation order differs: relative Frobenius <= 1e-5),
-through pg_amd_ag_linear16 (bias + GELU epilogue in the sum, the
-pre-activation kept for the backward, whose bias grad must match) and
-through matmul16 (no epilogue), at ragged row counts, k not a multiple of
-the k-tile, and widths 1, 10 and 16; a repeat reproduces every bit.
+"""Products with a narrow output (n <= 16 columns, as config 5's 10-wide
+layer): with rows enough for 32 blocks of 32 the skinny kernel (one launch,
+the epilogue applied per element after the waves' partial sums), else
+split-K over 128 x 128 MFMA tiles with the epilogue applied by the summing
+launch.  Each output against the f32-accumulating product of the same
+16-bit operands (identical operands, only the summation order differs:
+relative Frobenius <= 1e-5), through pg_amd_ag_linear16 (bias + GELU
+epilogue, the pre-activation kept for the backward, whose bias grad must
+match, and the weight grad over the dz the backward formed) and through
+matmul16 (no epilogue), at ragged row counts, k not a multiple of the
+k-tile, and widths 1, 10 and 16; a repeat reproduces every bit.
 """
 from math import erf
 
@@ -21,6 +23,10 @@ pytestmark = pytest.mark.gpu
 
 def _q(oracle, dt, x):
     h = oracle.cast16(dt, np.ascontiguousarray(x))
+    return f16_to_f32(h) if dt == F16 else bf16_to_f32(h)
+
+
+def _f32q(dt, h):
     return f16_to_f32(h) if dt == F16 else bf16_to_f32(h)
 
 
@@ -43,12 +49,20 @@ def test_narrow_linear16_forward_and_grads(lib, oracle, dt, M, K, N):
     qx, qw = _q(oracle, dt, x), _q(oracle, dt, w)
     z = oracle.gemm(F32, qx, qw, threads=16).astype(np.float64) + b
     assert rel_fro(got, _gelu(z)) <= 1e-5
-    # the backward reads the kept pre-activation: db = sum of dz over rows
+    # the backward reads the kept pre-activation: db = sum of dz over rows;
+    # dW = q(x)^T . dz over the 16-bit dz the backward formed (read back)
     seed = lib.tensor(g)
-    lib.pg_amd_backward_from(out, seed)
+    lib.pg_amd_linear16_keep_dz(True)
+    try:
+        lib.pg_amd_backward_from(out, seed)
+        dz = _f32q(dt, lib.read(lib.pg_amd_linear16_dz(out)))[:, :N]
+    finally:
+        lib.pg_amd_linear16_keep_dz(False)
     db = lib.grad(nb)
     dgelu = 0.5 * (1.0 + np.vectorize(erf)(z / np.sqrt(2.0))) + z * np.exp(-0.5 * z * z) / np.sqrt(2.0 * np.pi)
     assert rel_fro(db, (g * dgelu).sum(axis=0)) <= 1e-4
+    dw = lib.grad(nw)
+    assert rel_fro(dw, oracle.gemm(F32, np.ascontiguousarray(qx.T), np.ascontiguousarray(dz), threads=16)) <= 1e-5
     lib.pg_tensor_free(seed)
     for n in (out, nx, nw, nb):
         lib.pg_node_free(n)
