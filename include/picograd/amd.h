@@ -125,6 +125,16 @@ const pg_tensor *pg_amd_linear16_dz(const pg_node *n);
  * the activation pass reading dx); on by default. */
 void pg_amd_linear16_narrow(bool on);
 
+/* The 16-bit operand copies of matmul16 (pg_amd_ag_matmul16) written by the
+ * fused elementwise kernels beside their f32 outputs, in place of a cast
+ * pass over them: a deferred forward run whose output a matmul16 takes as
+ * its operand (b = gelu(x + bias); matmul16(b, W)), and a fused backward
+ * region that writes a matmul16 node's grad whole.  Each copy is rounded as
+ * the cast kernel rounds, so every result is the same bit for bit either
+ * way.  pg_amd_jit_copies16(false) turns both off (the cast pass runs);
+ * on by default. */
+void pg_amd_jit_copies16(bool on);
+
 /* JIT compile statistics: programs compiled by hiprtc, and cache lookups
  * that found a loaded kernel. */
 size_t pg_amd_jit_compiles(void);

@@ -181,6 +181,7 @@ _AMD_PROTOS = {
     "pg_amd_linear16_preact": (vp, [vp]),
     "pg_amd_linear16_keep_dz": (None, [bo]),
     "pg_amd_linear16_narrow": (None, [bo]),
+    "pg_amd_jit_copies16": (None, [bo]),
     "pg_amd_linear16_dz": (vp, [vp]),
     "pg_amd_tensor_modified": (None, [vp]),
     "pg_amd_tensor_refresh16": (bo, [vp]),

@@ -197,6 +197,10 @@ pg_tensor *pga_grad_for_write(pg_node *n, int *beta)
         *beta = 0;
         return n->grad;
     }
+    /* a 16-bit copy kept with the grad no longer matches it (a writer that
+     * also writes the copy marks it current after its launch) */
+    if (n->grad->data_ref)
+        n->grad->data_ref->shadow_stale = true;
     if (n->grad->pg_flags & PG_TENSOR_ZERO_PENDING) {
         n->grad->pg_flags &= ~PG_TENSOR_ZERO_PENDING;
         pgt_overwrite(n->grad);
@@ -297,6 +301,8 @@ typedef struct {
     int nin;
     int in[2]; /* >= 0: run input; < 0: -(k + 1) = output of op k */
     lz_tensor out;
+    uint16_t *out16; /* with dt16: the output's 16-bit copy is written here too */
+    int dt16;
 } lz_op;
 
 /* reduce_all over a run's output, recorded with the run when it is small
@@ -511,20 +517,55 @@ static void lz_finish(bool ran, bool red_done)
     }
     for (int j = 0; j < g_lz.nin; j++)
         pgt_ref_release(g_lz.in[j].ref);
-    for (int k = 0; k < g_lz.nops; k++)
+    for (int k = 0; k < g_lz.nops; k++) {
         pgt_ref_release(g_lz.op[k].out.ref);
+        g_lz.op[k].out16 = NULL;
+        g_lz.op[k].dt16 = 0;
+    }
     g_lz.nops = g_lz.nin = 0;
     g_lz.flushing = false;
 }
+
+/* set by pga_lazy_flush: the last run's fused kernel wrote the requested
+ * 16-bit copies */
+static bool g_lz_wrote16;
 
 void pga_lazy_flush(void)
 {
     if (!g_lz.nops || g_lz.flushing)
         return;
     g_lz.flushing = true;
+    g_lz_wrote16 = false;
     bool ok = false, red_done = false;
     int idi[LZ_MAX], ido[LZ_MAX];
     pg_jit_graph *g = lz_graph(idi, ido);
+    /* requested 16-bit copies: more outputs after the run's own */
+    void *x16[LZ_MAX];
+    size_t n16 = 0;
+    for (int k = 0; k < g_lz.nops && g; k++)
+        if (g_lz.op[k].out16) {
+            pgj_mark_output16(g, ido[k], g_lz.op[k].dt16);
+            x16[n16++] = g_lz.op[k].out16;
+        }
+    if (g && n16) {
+        if (lz_run_small(g, NULL, 0, x16, n16)) {
+            ok = red_done = true;
+        } else {
+            const void *ip[LZ_MAX];
+            void *op[2 * LZ_MAX];
+            size_t no = 0;
+            for (int j = 0; j < g_lz.nin; j++)
+                ip[j] = g_lz.in[j].dev;
+            for (int k = 0; k < g_lz.nops; k++)
+                op[no++] = g_lz.op[k].out.dev;
+            for (size_t k = 0; k < n16; k++)
+                op[no++] = x16[k];
+            ok = pgj_launch(g, g_lz.ndim, g_lz.shape, ip, (size_t)g_lz.nin, op, no);
+        }
+        g_lz_wrote16 = ok;
+        pg_jit_graph_free(g);
+        g = NULL;
+    }
     if (g) {
         if (lz_run_small(g, NULL, 0, NULL, 0))
             ok = red_done = true;
@@ -551,6 +592,24 @@ void pga_lazy_flush(void)
         if (!(eager_ok = lz_run_eager(k))) /* the device error is recorded; the rest are not run */
             break;
     lz_finish(eager_ok, red_done);
+}
+
+static bool g_copies16 = true;
+void pg_amd_jit_copies16(bool on) { g_copies16 = on; }
+bool pga_copies16(void) { return g_copies16; }
+
+bool pga_lazy_shadow16(const pg_tensor *t, int dt, uint16_t *dst)
+{
+    if (!g_copies16 || !g_lz.nops || g_lz.flushing || !t || !dst)
+        return false;
+    int k = lz_find(t);
+    if (k >= 0 || k == -LZ_MAX - 1)
+        return false; /* not an op's output */
+    k = -k - 1;
+    g_lz.op[k].out16 = dst;
+    g_lz.op[k].dt16 = dt;
+    pga_lazy_flush();
+    return g_lz_wrote16;
 }
 
 static bool lz_overlaps_ptr(const lz_tensor *x, const void *p, size_t nbytes)

@@ -631,8 +631,11 @@ static void mm16_backward(pg_node *n)
     if ((!pa->requires_grad && !pb->requires_grad) || !mm16_dims(a, b, &M, &K, &N) || !M || !N || !K)
         return;
     size_t K8 = up8(K), N8 = up8(N);
-    size_t gbytes;
-    uint16_t *g16 = stage16(dt, 0, g->dev, M, N, N, M, N8, 1, 0, &gbytes);
+    size_t gbytes = 0;
+    /* the grad's 16-bit copy when the fused backward region wrote it beside
+     * the grad (kept with the grad's storage), else a staged copy */
+    const uint16_t *gk = N == N8 ? pgt_shadow16_fresh(g, (pg_dtype)dt) : NULL;
+    uint16_t *g16 = gk ? (uint16_t *)gk : stage16(dt, 0, g->dev, M, N, N, M, N8, 1, 0, &gbytes);
     if (!g16)
         return;
     /* each grad taken for writing once, then both GEMMs as one whole-chip
@@ -662,7 +665,15 @@ static void mm16_backward(pg_node *n)
         pgd_free(ownb, obb);
     if (owna)
         pgd_free(owna, oba);
-    pgd_free(g16, gbytes);
+    if (!gk)
+        pgd_free(g16, gbytes);
+}
+
+int pgm_mm16_grad16(const pg_node *n)
+{
+    if (!n || n->backward != mm16_backward || !n->ctx || !n->value || n->value->ndim != 2 || n->value->shape[1] % 8)
+        return 0;
+    return ((const mm16_ctx *)n->ctx)->dt;
 }
 
 pg_node *pg_amd_ag_matmul16(pg_node *a, pg_node *b, pg_dtype dtype)

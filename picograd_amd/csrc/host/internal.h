@@ -100,6 +100,14 @@ void pgt_materialize(pg_tensor *t);
  * (pgt_touch), rewritten by pg_sgd_step in the pass that updates the
  * elements.  NULL (device error set) on failure. */
 const uint16_t *pgt_shadow16(pg_tensor *t, pg_dtype dt);
+/* t's 16-bit copy when it is current (t the whole of its storage, nothing
+ * pending on it), else NULL; never launches anything */
+const uint16_t *pgt_shadow16_fresh(const pg_tensor *t, pg_dtype dt);
+/* the buffer of t's 16-bit copy (allocated if missing, marked stale) for a
+ * kernel that writes the copy beside t's elements; the writer marks it
+ * current (shadow_stale = false) once its launch is queued.  NULL when t is
+ * not the whole of its storage or the allocation fails */
+uint16_t *pgt_shadow16_target(pg_tensor *t, pg_dtype dt);
 /* the same copy held as rows of `cols` elements at a pitch of `ld`
  * (ld % 8 == 0: rows of whole 16-byte pieces) with zeros between, for a
  * GEMM operand whose rows are not; the storage is whole rows of cols */
@@ -133,6 +141,12 @@ void pga_lazy_flush(void);
  * (true), or nothing launched (false) */
 bool pga_lazy_flush_with_backward(const pg_jit_graph *bwd, size_t lnd, const size_t *ls, const void *const *bin,
                                   size_t bnin, void *const *bout, size_t bnout);
+/* t is the output of a pending op: the run is flushed with t's 16-bit copy
+ * (dt) also written into dst by its fused kernel.  True when that kernel
+ * wrote it; false (the run flushed or left pending, dst not written) else */
+bool pga_lazy_shadow16(const pg_tensor *t, int dt, uint16_t *dst);
+/* the fused kernels write 16-bit operand copies (pg_amd_jit_copies16) */
+bool pga_copies16(void);
 
 /* ---- JIT internals (jit.c) ---- */
 /* the graph's kernel is compiled without contracting a product and a sum
@@ -167,6 +181,10 @@ typedef struct { float p0, p1; } pga_param_ctx;
 
 /* ---- matmul helpers (gemm.c) ---- */
 pg_tensor *pgm_matmul_forward(const pg_tensor *a, const pg_tensor *b);
+/* the 16-bit dtype in which a matmul16 node's backward reads its grad whole
+ * (its grad [M, N] with N % 8 == 0: a current copy kept with the grad's
+ * storage replaces its staging pass), else 0 */
+int pgm_mm16_grad16(const pg_node *n);
 void pgm_matmul_backward(pg_node *n);
 /* pg_amd_ag_linear16's backward and the destructor of its node context
  * (the kept pre-activation), called by pg_node_free */
@@ -181,6 +199,11 @@ int pgj_add_input_ex(pg_jit_graph *g, size_t ndim, const size_t *shape);
 /* marks node `id` as an output reduced (summed) onto `ndim/shape`, a shape
  * broadcast-compatible with the loop shape, combining with beta */
 void pgj_mark_output_ex(pg_jit_graph *g, int id, size_t ndim, const size_t *shape, int beta);
+/* one more output: node id's values rounded to 16 bits (dt16 PG_DTYPE_F16 or
+ * PG_DTYPE_BF16, as k_cast_to16 rounds) into a uint16_t buffer of the node's
+ * shape, which the launch takes among the outputs; the node must have the
+ * loop's full shape */
+void pgj_mark_output16(pg_jit_graph *g, int id, int dt16);
 int pgj_op_internal(pg_jit_graph *g, int op, int a, int b);
 /* dst gains src's nodes (src input i -> dst node in_map[i]) and, after its
  * own, src's outputs, each of which must have the loop shape (lnd, ls) */

@@ -56,6 +56,7 @@ typedef struct {
     size_t ndim;            /* target shape: equals the node's for a plain output */
     size_t shape[PG_MAX_NDIM];
     int beta;
+    int dt16; /* 0: f32; PG_DTYPE_F16 / PG_DTYPE_BF16: the node's 16-bit copy (pgj_mark_output16) */
 } jout;
 
 struct pg_jit_graph {
@@ -344,6 +345,18 @@ void pgj_mark_output_ex(pg_jit_graph *g, int id, size_t ndim, const size_t *shap
     o->ndim = ndim;
     memcpy(o->shape, shape, ndim * sizeof(size_t));
     o->beta = beta;
+    o->dt16 = 0;
+}
+
+void pgj_mark_output16(pg_jit_graph *g, int id, int dt16)
+{
+    if (!g || id < 0 || (size_t)id >= g->nn || (dt16 != PG_DTYPE_F16 && dt16 != PG_DTYPE_BF16)) {
+        jset_err("invalid 16-bit output");
+        return;
+    }
+    pgj_mark_output_ex(g, id, g->nodes[id].ndim, g->nodes[id].shape, 0);
+    if (g->nout && g->outs[g->nout - 1].node == id)
+        g->outs[g->nout - 1].dt16 = dt16;
 }
 
 /* Appends src's nodes to dst: src's input i becomes dst's node in_map[i],
@@ -378,8 +391,11 @@ bool pgj_graph_append(pg_jit_graph *dst, const pg_jit_graph *src, const int *in_
             ok = (map[id] = pgj_op_internal(dst, n->op, map[n->in[0]], n->nin == 2 ? map[n->in[1]] : -1)) >= 0;
         }
     }
-    for (size_t o = 0; o < src->nout && ok; o++)
+    for (size_t o = 0; o < src->nout && ok; o++) {
         pgj_mark_output_ex(dst, map[src->outs[o].node], src->outs[o].ndim, src->outs[o].shape, src->outs[o].beta);
+        if (dst->nout)
+            dst->outs[dst->nout - 1].dt16 = src->outs[o].dt16;
+    }
     free(map);
     return ok;
 }
@@ -432,6 +448,11 @@ uint64_t pg_jit_graph_hash(const pg_jit_graph *g)
     h = fnv(&g->nout, sizeof g->nout, h);
     if (g->exact)
         h = fnv("exact", 5, h);
+    for (size_t i = 0; i < g->nout; i++)
+        if (g->outs[i].dt16) {
+            h = fnv(&i, sizeof i, h);
+            h = fnv(&g->outs[i].dt16, sizeof g->outs[i].dt16, h);
+        }
     for (size_t i = 0; i < g->nn; i++) {
         const jnode *n = &g->nodes[i];
         h = fnv(&n->kind, sizeof n->kind, h);
@@ -472,7 +493,7 @@ static bool graph_equal(const pg_jit_graph *a, const pg_jit_graph *b)
         return false;
     for (size_t i = 0; i < a->nout; i++) {
         const jout *x = &a->outs[i], *y = &b->outs[i];
-        if (x->node != y->node || x->ndim != y->ndim || x->beta != y->beta ||
+        if (x->node != y->node || x->ndim != y->ndim || x->beta != y->beta || x->dt16 != y->dt16 ||
             memcmp(x->shape, y->shape, x->ndim * sizeof(size_t)))
             return false;
     }
@@ -510,6 +531,7 @@ typedef struct {
     int out_node[MAXIO * 2];
     int out_red[MAXIO * 2]; /* 1: reduced over dims < ksplit */
     int out_beta[MAXIO * 2];
+    int out_dt16[MAXIO * 2]; /* a 16-bit copy of the node (full loop shape, beta 0) */
     int ksplit;
     int64_t R, C;
     int vec;
@@ -589,6 +611,7 @@ static bool make_plan(const pg_jit_graph *g, size_t lnd, const size_t *ls, plan_
         const jout *o = &g->outs[i];
         P->out_node[i] = o->node;
         P->out_beta[i] = o->beta;
+        P->out_dt16[i] = o->dt16;
         if (!bstrides(o->ndim, o->shape, lnd, ls, lstr[nrow])) {
             jset_err("output %zu shape not broadcast-compatible with the loop shape", i);
             return false;
@@ -596,6 +619,10 @@ static bool make_plan(const pg_jit_graph *g, size_t lnd, const size_t *ls, plan_
         size_t on = pg_shape_numel(o->ndim, o->shape);
         size_t ln = pg_shape_numel(lnd, ls);
         P->out_red[i] = on != ln;
+        if (o->dt16 && (P->out_red[i] || o->beta)) {
+            jset_err("16-bit output %zu must be a full-shape write", i);
+            return false;
+        }
         if (P->out_red[i]) {
             /* must be a trailing-dims pattern: broadcast (zero stride) over
              * every non-1 dim before the first kept dim, kept after it */
@@ -834,30 +861,77 @@ static void emit_compute(sbuf *b, const pg_jit_graph *g, const bool *reach, int 
     }
 }
 
-/* stores of the full-shape (not reduced) outputs of one copy */
+/* node nid has a full-shape (stored) output */
+static bool stored_node(const plan_t *P, int nid)
+{
+    for (int o = 0; o < P->nout; o++)
+        if (!(P->R > 0 && P->out_red[o]) && P->out_node[o] == nid)
+            return true;
+    return false;
+}
+
+/* Each stored node's value of one copy goes through an empty asm (w<node>
+ * names it), and its stores and column sums read that copy: whatever the
+ * compiler would make of the product behind it (contracted into a column
+ * sum's add, or not, a choice that shifts with the number of stores), every
+ * consumer reads the one rounded value, so a node's f32 results are the
+ * same bits whether or not its 16-bit copy is also stored. */
+static void emit_launder(sbuf *b, const plan_t *P, int vec, int u)
+{
+    for (int o = 0; o < P->nout; o++) {
+        if (P->R > 0 && P->out_red[o])
+            continue;
+        int nid = P->out_node[o], seen = 0;
+        for (int q = 0; q < o; q++)
+            seen |= !(P->R > 0 && P->out_red[q]) && P->out_node[q] == nid;
+        if (seen)
+            continue;
+        for (int e = 0; e < vec; e++)
+            sb_add(b, "    float w%d_%d_%d = v%d_%d_%d; __asm__(\"\" : \"+v\"(w%d_%d_%d));\n", nid, u, e, nid, u, e, nid,
+                   u, e);
+    }
+}
+
+/* stores of the full-shape (not reduced) outputs of one copy (after
+ * emit_launder of that copy) */
 static void emit_stores(sbuf *b, const plan_t *P, int vec, const char *idx, int u)
 {
     for (int o = 0; o < P->nout; o++) {
         if (P->R > 0 && P->out_red[o])
             continue;
         int nid = P->out_node[o];
+        if (P->out_dt16[o]) {
+            /* the node's 16-bit copy, rounded as k_cast_to16 rounds */
+            const int dt = P->out_dt16[o];
+            if (vec == 4 && dt == PG_DTYPE_BF16)
+                sb_add(b, "    __builtin_nontemporal_store((pgu2){f32x2_to_bf16x2(w%d_%d_0, w%d_%d_1), "
+                          "f32x2_to_bf16x2(w%d_%d_2, w%d_%d_3)}, (pgu2 *)(out%d + %s));\n",
+                       nid, u, nid, u, nid, u, nid, u, o, idx);
+            else if (vec == 4)
+                sb_add(b, "    __builtin_nontemporal_store((pgu2){(unsigned)f32_to_f16(w%d_%d_0) | ((unsigned)f32_to_f16(w%d_%d_1) << 16), "
+                          "(unsigned)f32_to_f16(w%d_%d_2) | ((unsigned)f32_to_f16(w%d_%d_3) << 16)}, (pgu2 *)(out%d + %s));\n",
+                       nid, u, nid, u, nid, u, nid, u, o, idx);
+            else
+                sb_add(b, "    out%d[%s] = to16(%d, w%d_%d_0);\n", o, idx, dt, nid, u);
+            continue;
+        }
         /* each output element is written once per launch: stream the stores
          * (and the read of an accumulating output) past the caches */
         if (vec == 4) {
             if (P->out_beta[o])
                 sb_add(b, "    { pgf4 *p = (pgf4 *)(out%d + %s); pgf4 t = __builtin_nontemporal_load(p);"
-                          " t.x += v%d_%d_0; t.y += v%d_%d_1; t.z += v%d_%d_2; t.w += v%d_%d_3;"
+                          " t.x += w%d_%d_0; t.y += w%d_%d_1; t.z += w%d_%d_2; t.w += w%d_%d_3;"
                           " __builtin_nontemporal_store(t, p); }\n",
                        o, idx, nid, u, nid, u, nid, u, nid, u);
             else
-                sb_add(b, "    __builtin_nontemporal_store((pgf4){v%d_%d_0, v%d_%d_1, v%d_%d_2, v%d_%d_3}, (pgf4 *)(out%d + %s));\n",
+                sb_add(b, "    __builtin_nontemporal_store((pgf4){w%d_%d_0, w%d_%d_1, w%d_%d_2, w%d_%d_3}, (pgf4 *)(out%d + %s));\n",
                        nid, u, nid, u, nid, u, nid, u, o, idx);
         } else {
             if (P->out_beta[o])
-                sb_add(b, "    __builtin_nontemporal_store(__builtin_nontemporal_load(out%d + %s) + v%d_%d_0, out%d + %s);\n",
+                sb_add(b, "    __builtin_nontemporal_store(__builtin_nontemporal_load(out%d + %s) + w%d_%d_0, out%d + %s);\n",
                        o, idx, nid, u, o, idx);
             else
-                sb_add(b, "    __builtin_nontemporal_store(v%d_%d_0, out%d + %s);\n", nid, u, o, idx);
+                sb_add(b, "    __builtin_nontemporal_store(w%d_%d_0, out%d + %s);\n", nid, u, o, idx);
         }
     }
 }
@@ -871,8 +945,24 @@ static void emit_prologue(sbuf *b, const plan_t *P)
         if (P->in_used[i])
             sb_add(b, "  const float *__restrict__ in%d = a.in[%d];\n", i, i);
     for (int o = 0; o < P->nout; o++)
-        if (!(P->R > 0 && P->out_red[o]))
+        if (P->out_dt16[o])
+            sb_add(b, "  unsigned short *__restrict__ out%d = (unsigned short *)a.out[%d];\n", o, o);
+        else if (!(P->R > 0 && P->out_red[o]))
             sb_add(b, "  float *__restrict__ out%d = a.out[%d];\n", o, o);
+}
+
+/* kernels/convert16.h, embedded by the build: the f32 -> 16-bit rounding of
+ * the hand-written kernels, for programs that store 16-bit copies */
+extern const char pgk_convert_source[];
+
+static void emit_headers(sbuf *b, const plan_t *P)
+{
+    sb_add(b, "%s\n", pgk_math_source);
+    bool any16 = false;
+    for (int o = 0; o < P->nout; o++)
+        any16 = any16 || P->out_dt16[o];
+    if (any16)
+        sb_add(b, "%s\ntypedef unsigned int pgu2 __attribute__((ext_vector_type(2)));\n", pgk_convert_source);
 }
 
 static char *gen_source(const pg_jit_graph *g, const plan_t *P, const bool *reach)
@@ -881,7 +971,7 @@ static char *gen_source(const pg_jit_graph *g, const plan_t *P, const bool *reac
     bool red = P->R > 0;
     bool wide = P->numel >= ((int64_t)1 << 31);
     sb_add(&b, "// picograd-amd fused elementwise kernel (generated)\n");
-    sb_add(&b, "%s\n", pgk_math_source);
+    emit_headers(&b, P);
     sb_add(&b, "typedef %s IDX;\n", wide ? "unsigned long long" : "unsigned int");
     sb_add(&b, "typedef float pgf4 __attribute__((ext_vector_type(4)));\n");
     /* exactly the pointers this kernel takes (the host packs the same) */
@@ -907,11 +997,14 @@ static char *gen_source(const pg_jit_graph *g, const plan_t *P, const bool *reac
         emit_loads(&b, P, vec, "i1", 1);
         emit_compute(&b, g, reach, vec, 0);
         emit_compute(&b, g, reach, vec, 1);
+        emit_launder(&b, P, vec, 0);
+        emit_launder(&b, P, vec, 1);
         emit_stores(&b, P, vec, "i0", 0);
         emit_stores(&b, P, vec, "i1", 1);
         sb_add(&b, "  }\n  if (i < N) {\n    const IDX i0 = i;\n");
         emit_loads(&b, P, vec, "i0", 0);
         emit_compute(&b, g, reach, vec, 0);
+        emit_launder(&b, P, vec, 0);
         emit_stores(&b, P, vec, "i0", 0);
         sb_add(&b, "  }\n}\n");
         return b.s;
@@ -949,19 +1042,24 @@ static char *gen_source(const pg_jit_graph *g, const plan_t *P, const bool *reac
     for (int u = 0; u < RU; u++)
         emit_compute(&b, g, reach, vec, u);
     for (int u = 0; u < RU; u++)
+        emit_launder(&b, P, vec, u);
+    for (int u = 0; u < RU; u++)
         for (int o = 0; o < P->nout; o++)
             if (P->out_red[o])
                 for (int e = 0; e < vec; e++)
-                    sb_add(&b, "    acc%d_%d += v%d_%d_%d;\n", o, e, P->out_node[o], u, e);
+                    sb_add(&b, "    acc%d_%d += %c%d_%d_%d;\n", o, e, stored_node(P, P->out_node[o]) ? 'w' : 'v',
+                           P->out_node[o], u, e);
     for (int u = 0; u < RU; u++)
         emit_stores(&b, P, vec, iname[u], u);
     sb_add(&b, "  }\n  for (; r < r1; r += 4u) {\n    const IDX i0 = r * C + c;\n");
     emit_loads(&b, P, vec, "i0", 0);
     emit_compute(&b, g, reach, vec, 0);
+    emit_launder(&b, P, vec, 0);
     for (int o = 0; o < P->nout; o++)
         if (P->out_red[o])
             for (int e = 0; e < vec; e++)
-                sb_add(&b, "    acc%d_%d += v%d_0_%d;\n", o, e, P->out_node[o], e);
+                sb_add(&b, "    acc%d_%d += %c%d_0_%d;\n", o, e, stored_node(P, P->out_node[o]) ? 'w' : 'v',
+                       P->out_node[o], e);
     emit_stores(&b, P, vec, "i0", 0);
     sb_add(&b, "  }\n  }\n");
     /* combine the 4 row lanes in LDS, fixed order, one partial row per block */
@@ -1039,7 +1137,7 @@ static char *gen_source_small(const pg_jit_graph *g, const plan_t *P, const bool
     const int ni = P->nin ? P->nin : 1, no = P->nout ? P->nout : 1;
     const int vec = P->vec, T = PGJ_SMALL_THREADS;
     sb_add(&b, "// picograd-amd fused elementwise kernel, one-block run (generated)\n");
-    sb_add(&b, "%s\n", pgk_math_source);
+    emit_headers(&b, P);
     sb_add(&b, "typedef unsigned int IDX;\n");
     sb_add(&b, "typedef float pgf4 __attribute__((ext_vector_type(4)));\n");
     sb_add(&b, "typedef unsigned int pgu4 __attribute__((ext_vector_type(4)));\n");
@@ -1078,11 +1176,14 @@ static char *gen_source_small(const pg_jit_graph *g, const plan_t *P, const bool
     emit_loads(&b, P, vec, "i1", 1);
     emit_compute(&b, g, reach, vec, 0);
     emit_compute(&b, g, reach, vec, 1);
+    emit_launder(&b, P, vec, 0);
+    emit_launder(&b, P, vec, 1);
     emit_stores(&b, P, vec, "i0", 0);
     emit_stores(&b, P, vec, "i1", 1);
     sb_add(&b, "  }\n  if (i < N) {\n    const IDX i0 = i;\n");
     emit_loads(&b, P, vec, "i0", 0);
     emit_compute(&b, g, reach, vec, 0);
+    emit_launder(&b, P, vec, 0);
     emit_stores(&b, P, vec, "i0", 0);
     sb_add(&b, "  }\n  }\n");
     /* 3. the reduction */

@@ -422,10 +422,46 @@ const uint16_t *pgt_shadow16(pg_tensor *t, pg_dtype dt)
         r->shadow_bytes = bytes;
     }
     r->shadow_dtype = (int)dt;
+    /* elements still pending in a deferred forward run: its fused kernel
+     * writes the copy beside them, in place of a pass over them */
+    if (t->dev == r->ptr && t->numel == n && pga_lazy_shadow16(t, (int)dt, r->shadow)) {
+        r->shadow_stale = false;
+        return r->shadow;
+    }
     pgt_materialize(t);
     if (!pgd_check(pgk_cast_to16((int)dt, r->ptr, r->shadow, n, pgd_stream()), "shadow16"))
         return NULL;
     r->shadow_stale = false;
+    return r->shadow;
+}
+
+const uint16_t *pgt_shadow16_fresh(const pg_tensor *t, pg_dtype dt)
+{
+    const pg_data_ref *r = t ? t->data_ref : NULL;
+    if (!r || !r->shadow || r->shadow_stale || r->shadow_dtype != (int)dt || r->shadow_cols || t->dev != r->ptr ||
+        t->numel * 4 != r->nbytes || (t->pg_flags & PG_TENSOR_ZERO_PENDING) || r->narrow || r->act_pending ||
+        r->clip_pending)
+        return NULL;
+    return r->shadow;
+}
+
+uint16_t *pgt_shadow16_target(pg_tensor *t, pg_dtype dt)
+{
+    if (!t || !t->data_ref || t->dtype != PG_DTYPE_F32 || (dt != PG_DTYPE_F16 && dt != PG_DTYPE_BF16) ||
+        t->dev != t->data_ref->ptr || t->numel * 4 != t->data_ref->nbytes)
+        return NULL;
+    pg_data_ref *r = t->data_ref;
+    if (r->shadow && r->shadow_cols)
+        shadow_drop(r);
+    if (!r->shadow) {
+        const size_t bytes = t->numel ? t->numel * 2 : 1;
+        r->shadow = pgd_malloc(bytes);
+        if (!r->shadow)
+            return NULL;
+        r->shadow_bytes = bytes;
+    }
+    r->shadow_dtype = (int)dt;
+    r->shadow_stale = true; /* until the writer's launch is queued */
     return r->shadow;
 }
 

@@ -438,8 +438,14 @@ static bool run_region(wctx *w, int r, const pg_tensor *root_grad, float scale, 
         outn[nout++] = p;
     }
     bool ok = !b.fail && nout > 0;
-    void *optr[32];
+    void *optr[64];
     int betas[32];
+    /* a grad written whole (beta 0, the loop's shape) that a matmul16 node's
+     * backward reads as 16 bits gets its copy from the region too, beside
+     * the f32 elements (kept with the grad's storage, current from here
+     * until the grad is next written) */
+    pg_data_ref *ref16[32];
+    size_t n16 = 0;
     if (ok) {
         for (size_t i = 0; i < nout; i++) {
             pg_node *p = outn[i];
@@ -453,12 +459,26 @@ static bool run_region(wctx *w, int r, const pg_tensor *root_grad, float scale, 
             optr[i] = dg->dev;
             pgj_mark_output_ex(b.g, b.grad[nm_get(w->idx, p)], p->value->ndim, p->value->shape, betas[i]);
         }
+        for (size_t i = 0; ok && i < nout; i++) {
+            pg_node *p = outn[i];
+            const int dt16 = pga_copies16() ? pgm_mm16_grad16(p) : 0;
+            if (!dt16 || betas[i] || !pg_shape_equal(p->value->ndim, p->value->shape, L->ndim, L->shape))
+                continue;
+            uint16_t *sh = pgt_shadow16_target(p->grad, (pg_dtype)dt16);
+            if (!sh)
+                continue;
+            pgj_mark_output16(b.g, b.grad[nm_get(w->idx, p)], dt16);
+            optr[nout + n16] = sh;
+            ref16[n16++] = p->grad->data_ref;
+        }
     }
     if (ok) {
         /* a small forward run still pending (config 1: leaves, forward and
          * sum in one block) takes the region into its own launch */
-        ok = pga_lazy_flush_with_backward(b.g, L->ndim, L->shape, b.in_ptr, b.nin, optr, nout) ||
-             pgj_launch(b.g, L->ndim, L->shape, b.in_ptr, b.nin, optr, nout);
+        ok = pga_lazy_flush_with_backward(b.g, L->ndim, L->shape, b.in_ptr, b.nin, optr, nout + n16) ||
+             pgj_launch(b.g, L->ndim, L->shape, b.in_ptr, b.nin, optr, nout + n16);
+        for (size_t i = 0; ok && i < n16; i++)
+            ref16[i]->shadow_stale = false;
         if (!ok) {
             pga_set_err("fused backward failed: %s", pg_jit_last_error());
             /* restore the zero flag of grads the kernel did not write */

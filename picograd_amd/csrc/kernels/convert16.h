@@ -8,8 +8,15 @@
 #ifndef PGK_CONVERT16_H
 #define PGK_CONVERT16_H
 
+#ifdef __HIPCC_RTC__
+// the JIT compiles this file's text with hiprtc, whose fixed-width types
+// live in a namespace of its own
+using __hip_internal::uint16_t;
+using __hip_internal::uint32_t;
+#else
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#endif
 
 // f32 -> bf16 by the hardware convert (v_cvt_pk_bf16_f32): round to nearest
 // even, f32 subnormals kept (the kernels run in the default FP mode, which
