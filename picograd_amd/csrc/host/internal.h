@@ -204,6 +204,11 @@ void pgj_mark_output_ex(pg_jit_graph *g, int id, size_t ndim, const size_t *shap
  * shape, which the launch takes among the outputs; the node must have the
  * loop's full shape */
 void pgj_mark_output16(pg_jit_graph *g, int id, int dt16);
+/* the graph's stored values pass one asm copy each, read by their stores and
+ * column sums (implied by a 16-bit output): set on a graph that stores a
+ * 16-bit copy in one mode of its caller and not in another, so both modes
+ * compute the same bits */
+void pgj_graph_set_launder(pg_jit_graph *g);
 int pgj_op_internal(pg_jit_graph *g, int op, int a, int b);
 /* dst gains src's nodes (src input i -> dst node in_map[i]) and, after its
  * own, src's outputs, each of which must have the loop shape (lnd, ls) */

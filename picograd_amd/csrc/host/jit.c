@@ -67,6 +67,7 @@ struct pg_jit_graph {
     jout outs[MAXIO * 2];
     size_t nout;
     bool exact; /* no FMA contraction between the graph's ops (pgj_graph_set_exact) */
+    bool launder; /* stored values through one asm copy (pgj_graph_set_launder) */
 };
 
 /* one compiled kernel for one (graph, loop shape) */
@@ -137,6 +138,12 @@ size_t pg_amd_jit_cache_hits(void) { return pgj_stat_hits; }
 /* ---------------------------------------------------------------- graph */
 
 pg_jit_graph *pg_jit_graph_new(void) { return calloc(1, sizeof(pg_jit_graph)); }
+
+void pgj_graph_set_launder(pg_jit_graph *g)
+{
+    if (g)
+        g->launder = true;
+}
 
 void pgj_graph_set_exact(pg_jit_graph *g)
 {
@@ -391,6 +398,7 @@ bool pgj_graph_append(pg_jit_graph *dst, const pg_jit_graph *src, const int *in_
             ok = (map[id] = pgj_op_internal(dst, n->op, map[n->in[0]], n->nin == 2 ? map[n->in[1]] : -1)) >= 0;
         }
     }
+    dst->launder = dst->launder || src->launder;
     for (size_t o = 0; o < src->nout && ok; o++) {
         pgj_mark_output_ex(dst, map[src->outs[o].node], src->outs[o].ndim, src->outs[o].shape, src->outs[o].beta);
         if (dst->nout)
@@ -448,6 +456,8 @@ uint64_t pg_jit_graph_hash(const pg_jit_graph *g)
     h = fnv(&g->nout, sizeof g->nout, h);
     if (g->exact)
         h = fnv("exact", 5, h);
+    if (g->launder)
+        h = fnv("launder", 7, h);
     for (size_t i = 0; i < g->nout; i++)
         if (g->outs[i].dt16) {
             h = fnv(&i, sizeof i, h);
@@ -477,7 +487,7 @@ uint64_t pg_jit_graph_hash(const pg_jit_graph *g)
 
 static bool graph_equal(const pg_jit_graph *a, const pg_jit_graph *b)
 {
-    if (a->nn != b->nn || a->nin != b->nin || a->nout != b->nout || a->exact != b->exact)
+    if (a->nn != b->nn || a->nin != b->nin || a->nout != b->nout || a->exact != b->exact || a->launder != b->launder)
         return false;
     for (size_t i = 0; i < a->nn; i++) {
         const jnode *x = &a->nodes[i], *y = &b->nodes[i];
@@ -532,6 +542,7 @@ typedef struct {
     int out_red[MAXIO * 2]; /* 1: reduced over dims < ksplit */
     int out_beta[MAXIO * 2];
     int out_dt16[MAXIO * 2]; /* a 16-bit copy of the node (full loop shape, beta 0) */
+    bool launder;            /* stored values through one asm copy (emit_launder) */
     int ksplit;
     int64_t R, C;
     int vec;
@@ -592,6 +603,7 @@ static void mark_reach(const pg_jit_graph *g, bool *reach)
 static bool make_plan(const pg_jit_graph *g, size_t lnd, const size_t *ls, plan_t *P, const bool *reach)
 {
     memset(P, 0, sizeof *P);
+    P->launder = g->launder;
     int64_t lstr[MAXIO * 4][PG_MAX_NDIM]; /* inputs then outputs */
     int nrow = 0;
     P->nin = (int)g->nin;
@@ -612,6 +624,7 @@ static bool make_plan(const pg_jit_graph *g, size_t lnd, const size_t *ls, plan_
         P->out_node[i] = o->node;
         P->out_beta[i] = o->beta;
         P->out_dt16[i] = o->dt16;
+        P->launder = P->launder || o->dt16;
         if (!bstrides(o->ndim, o->shape, lnd, ls, lstr[nrow])) {
             jset_err("output %zu shape not broadcast-compatible with the loop shape", i);
             return false;
@@ -870,12 +883,14 @@ static bool stored_node(const plan_t *P, int nid)
     return false;
 }
 
-/* Each stored node's value of one copy goes through an empty asm (w<node>
- * names it), and its stores and column sums read that copy: whatever the
- * compiler would make of the product behind it (contracted into a column
- * sum's add, or not, a choice that shifts with the number of stores), every
- * consumer reads the one rounded value, so a node's f32 results are the
- * same bits whether or not its 16-bit copy is also stored. */
+/* In a laundering graph (one that stores, or in another mode of the same
+ * caller would store, a node's 16-bit copy) each stored node's value of one
+ * copy goes through an empty asm (w<node> names it), and its stores and
+ * column sums read that copy: whatever the compiler would make of the
+ * product behind it (contracted into a column sum's add, or not, a choice
+ * that shifts with the number of stores), every consumer reads the one
+ * rounded value, so a node's f32 results are the same bits whether or not
+ * its 16-bit copy is also stored.  Elsewhere w<node> is a plain alias. */
 static void emit_launder(sbuf *b, const plan_t *P, int vec, int u)
 {
     for (int o = 0; o < P->nout; o++) {
@@ -886,9 +901,13 @@ static void emit_launder(sbuf *b, const plan_t *P, int vec, int u)
             seen |= !(P->R > 0 && P->out_red[q]) && P->out_node[q] == nid;
         if (seen)
             continue;
-        for (int e = 0; e < vec; e++)
-            sb_add(b, "    float w%d_%d_%d = v%d_%d_%d; __asm__(\"\" : \"+v\"(w%d_%d_%d));\n", nid, u, e, nid, u, e, nid,
-                   u, e);
+        for (int e = 0; e < vec; e++) {
+            if (P->launder)
+                sb_add(b, "    float w%d_%d_%d = v%d_%d_%d; __asm__(\"\" : \"+v\"(w%d_%d_%d));\n", nid, u, e, nid, u, e,
+                       nid, u, e);
+            else
+                sb_add(b, "    const float w%d_%d_%d = v%d_%d_%d;\n", nid, u, e, nid, u, e);
+        }
     }
 }
 

@@ -461,8 +461,12 @@ static bool run_region(wctx *w, int r, const pg_tensor *root_grad, float scale, 
         }
         for (size_t i = 0; ok && i < nout; i++) {
             pg_node *p = outn[i];
-            const int dt16 = pga_copies16() ? pgm_mm16_grad16(p) : 0;
+            const int dt16 = pgm_mm16_grad16(p);
             if (!dt16 || betas[i] || !pg_shape_equal(p->value->ndim, p->value->shape, L->ndim, L->shape))
+                continue;
+            /* the same arithmetic with the copies on or off */
+            pgj_graph_set_launder(b.g);
+            if (!pga_copies16())
                 continue;
             uint16_t *sh = pgt_shadow16_target(p->grad, (pg_dtype)dt16);
             if (!sh)
