@@ -623,13 +623,16 @@ __global__ void __launch_bounds__(kBlock) k_sgd(sgd_table tab, float lr, float m
 
 // ---------------------------------------------------------------- linear backward
 // dz = g * act'(z) (act 0: dz = g) for a [m, n] f32 grad, written as RNE
-// 16-bit rows of ldd (ldd % 8 == 0) with zeros in columns [n, ldd).  A
-// block is 16 x 16 lanes over 128 columns: lane (cx, ry) takes columns
-// 8 cx .. 8 cx + 7 of rows ry, ry + 16, ... of the block's `rpb` rows, so a
-// wave reads 4 rows of 512 contiguous bytes per load.  With part given,
-// the block's column sums (the 16 row lanes added in ry order) go to
-// part[row block][n]; k_colsum_fin adds the row blocks in order
-// (deterministic).
+// 16-bit rows of ldd (ldd % 8 == 0) with zeros in columns [n, ldd); DT 1
+// stores f16, 2 bf16.  A block is 16 x 16 lanes over 128 columns: lane
+// (cx, ry) takes columns 4 cx .. 4 cx + 3 and 64 + 4 cx .. 64 + 4 cx + 3 of
+// rows ry, ry + 16, ... of the block's `rpb` rows, so each load of a wave
+// reads 4 rows of two whole 128-byte lines and each 16-bit store writes 4
+// rows of one.  The lane's rows go in pairs (r, r + 16), the next pair's
+// loads issued before the current pair's products.  With part given, the
+// block's column sums (each lane's rows in order, then the 16 row lanes in
+// ry order) go to part[row block][n]; k_colsum_fin adds the row blocks in
+// order (deterministic).
 __device__ __forceinline__ float act_grad(int act, float z)
 {
     if (act == 1)
@@ -639,92 +642,132 @@ __device__ __forceinline__ float act_grad(int act, float z)
     return 1.0f;
 }
 
-// one row of lane (cx, ry)'s eight columns: the products, their 16-bit
-// store and the column sums (in row order)
-template <int ACT>
+// one row of the lane's eight columns (c0 .. c0 + 3 in gv[0..3], c0 + 64 ..
+// in gv[4..7]): the products, their 16-bit stores (each 4-column group
+// whose first column is below ldd: ldd % 8 == 0, so a group is inside or
+// outside whole) and the column sums (in row order)
+template <int ACT, int DT>
 __device__ __forceinline__ void act_bwd_row(const float (&gv)[8], const float (&zv)[8], float (&acc)[8],
-                                            uint16_t *__restrict__ dst, int dtype)
+                                            uint16_t *__restrict__ dst, bool lo, bool hi)
 {
     uint32_t w[4];
 #pragma unroll
     for (int q = 0; q < 8; q += 2) {
+        // the sums add the rounded f32 products, as a sum over the dz tensor
+        // would (no product contracted into the add)
+#pragma clang fp contract(off)
         const float d0 = ACT ? gv[q] * act_grad(ACT, zv[q]) : gv[q];
         const float d1 = ACT ? gv[q + 1] * act_grad(ACT, zv[q + 1]) : gv[q + 1];
         acc[q] += d0;
         acc[q + 1] += d1;
-        w[q / 2] = to16x2(dtype, d0, d1);
+        w[q / 2] = to16x2(DT, d0, d1);
     }
     // columns past n hold g = 0, so they store zeros
-    *reinterpret_cast<uint4 *>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+    if (lo)
+        *reinterpret_cast<uint2 *>(dst) = make_uint2(w[0], w[1]);
+    if (hi)
+        *reinterpret_cast<uint2 *>(dst + 64) = make_uint2(w[2], w[3]);
 }
 
+// the loads of rows r and r + 16 (off = r * n + c0)
 template <int ACT>
+__device__ __forceinline__ void act_bwd_load2(const float *__restrict__ g, const float *__restrict__ z, size_t off,
+                                              size_t n, float4 (&gq)[2][2], float4 (&zq)[2][2])
+{
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const size_t o = off + 16 * u * n;
+        gq[u][0] = *reinterpret_cast<const float4 *>(g + o);
+        gq[u][1] = *reinterpret_cast<const float4 *>(g + o + 64);
+        if (ACT) {
+            zq[u][0] = *reinterpret_cast<const float4 *>(z + o);
+            zq[u][1] = *reinterpret_cast<const float4 *>(z + o + 64);
+        }
+    }
+}
+
+template <int ACT, int DT>
+__device__ __forceinline__ void act_bwd_pair(const float4 (&gq)[2][2], const float4 (&zq)[2][2], float (&acc)[8],
+                                             uint16_t *__restrict__ dst, size_t ldd)
+{
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const float gv[8] = {gq[u][0].x, gq[u][0].y, gq[u][0].z, gq[u][0].w,
+                             gq[u][1].x, gq[u][1].y, gq[u][1].z, gq[u][1].w};
+        float zv[8] = {};
+        if (ACT) {
+            const float zt[8] = {zq[u][0].x, zq[u][0].y, zq[u][0].z, zq[u][0].w,
+                                 zq[u][1].x, zq[u][1].y, zq[u][1].z, zq[u][1].w};
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+                zv[q] = zt[q];
+        }
+        act_bwd_row<ACT, DT>(gv, zv, acc, dst + 16 * u * ldd, true, true);
+    }
+}
+
+template <int ACT, int DT>
 __global__ void __launch_bounds__(kBlock) k_act_bwd16(const float *__restrict__ g, const float *__restrict__ z,
                                                       size_t m, size_t n, uint16_t *__restrict__ d16, size_t ldd,
-                                                      int dtype, float *__restrict__ part, size_t rpb)
+                                                      float *__restrict__ part, size_t rpb)
 {
     __shared__ float red[16][129];
     const int cx = threadIdx.x & 15, ry = threadIdx.x >> 4;
-    const size_t c0 = (size_t)blockIdx.x * 128 + (size_t)cx * 8;
+    const size_t cb = (size_t)blockIdx.x * 128, c0 = cb + (size_t)cx * 4;
     const size_t rb = (size_t)blockIdx.y * rpb, re = rb + rpb < m ? rb + rpb : m;
-    const bool vec = c0 + 8 <= n && (n & 3) == 0 && ((((uintptr_t)g) | ((uintptr_t)z)) & 15) == 0;
+    const bool lo = c0 < ldd, hi = c0 + 64 < ldd;
+    // every column of the block inside n: the 16-byte path for every lane
+    const bool vec = cb + 128 <= n && (n & 3) == 0 && ((((uintptr_t)g) | ((uintptr_t)z)) & 15) == 0;
     float acc[8];
 #pragma unroll
     for (int q = 0; q < 8; ++q)
         acc[q] = 0.0f;
-    if (c0 < ldd) {
-        size_t r = rb + ry;
-        if (vec) {
-            // four of the lane's rows per pass, every load of the pass
-            // issued before the first product
-            constexpr int R = 4;
-            for (; r + 16 * (R - 1) < re; r += 16 * R) {
-                float4 gq[R][2], zq[R][2];
-#pragma unroll
-                for (int u = 0; u < R; ++u) {
-                    const size_t off = (r + 16 * u) * n + c0;
-                    gq[u][0] = *reinterpret_cast<const float4 *>(g + off);
-                    gq[u][1] = *reinterpret_cast<const float4 *>(g + off + 4);
-                    if (ACT) {
-                        zq[u][0] = *reinterpret_cast<const float4 *>(z + off);
-                        zq[u][1] = *reinterpret_cast<const float4 *>(z + off + 4);
-                    }
-                }
-#pragma unroll
-                for (int u = 0; u < R; ++u) {
-                    const float gv[8] = {gq[u][0].x, gq[u][0].y, gq[u][0].z, gq[u][0].w,
-                                         gq[u][1].x, gq[u][1].y, gq[u][1].z, gq[u][1].w};
-                    float zv[8] = {};
-                    if (ACT) {
-                        const float zt[8] = {zq[u][0].x, zq[u][0].y, zq[u][0].z, zq[u][0].w,
-                                             zq[u][1].x, zq[u][1].y, zq[u][1].z, zq[u][1].w};
-#pragma unroll
-                        for (int q = 0; q < 8; ++q)
-                            zv[q] = zt[q];
-                    }
-                    act_bwd_row<ACT>(gv, zv, acc, d16 + (r + 16 * u) * ldd + c0, dtype);
-                }
-            }
+    size_t r = rb + ry;
+    // pairs of rows every row lane of the block has (rows up to re)
+    const size_t np = vec ? (re - rb) / 32 : 0;
+    if (np) {
+        float4 ga[2][2], za[2][2], gb[2][2], zb[2][2];
+        act_bwd_load2<ACT>(g, z, r * n + c0, n, ga, za);
+        size_t p = 0;
+        for (; p + 2 < np; p += 2, r += 64) {
+            act_bwd_load2<ACT>(g, z, (r + 32) * n + c0, n, gb, zb);
+            act_bwd_pair<ACT, DT>(ga, za, acc, d16 + r * ldd + c0, ldd);
+            act_bwd_load2<ACT>(g, z, (r + 64) * n + c0, n, ga, za);
+            act_bwd_pair<ACT, DT>(gb, zb, acc, d16 + (r + 32) * ldd + c0, ldd);
         }
+        if (p + 1 < np) {
+            act_bwd_load2<ACT>(g, z, (r + 32) * n + c0, n, gb, zb);
+            act_bwd_pair<ACT, DT>(ga, za, acc, d16 + r * ldd + c0, ldd);
+            act_bwd_pair<ACT, DT>(gb, zb, acc, d16 + (r + 32) * ldd + c0, ldd);
+            r += 64;
+        } else {
+            act_bwd_pair<ACT, DT>(ga, za, acc, d16 + r * ldd + c0, ldd);
+            r += 32;
+        }
+    }
+    if (lo) {
         for (; r < re; r += 16) {
             float gv[8], zv[8];
             const size_t off = r * n + c0;
 #pragma unroll
             for (int q = 0; q < 8; ++q) {
-                const bool in = c0 + q < n;
-                gv[q] = in ? g[off + q] : 0.0f;
-                zv[q] = (in && ACT) ? z[off + q] : 0.0f;
+                const size_t o = q < 4 ? q : 60 + q; // columns c0 + q, then c0 + 64 + q - 4
+                const bool in = c0 + o < n;
+                gv[q] = in ? g[off + o] : 0.0f;
+                zv[q] = (in && ACT) ? z[off + o] : 0.0f;
             }
-            act_bwd_row<ACT>(gv, zv, acc, d16 + r * ldd + c0, dtype);
+            act_bwd_row<ACT, DT>(gv, zv, acc, d16 + r * ldd + c0, lo, hi);
         }
     }
     if (part) {
 #pragma unroll
-        for (int q = 0; q < 8; ++q)
-            red[ry][cx * 8 + q] = acc[q];
+        for (int q = 0; q < 4; ++q) {
+            red[ry][cx * 4 + q] = acc[q];
+            red[ry][64 + cx * 4 + q] = acc[4 + q];
+        }
         __syncthreads();
         if (threadIdx.x < 128) {
-            const size_t col = (size_t)blockIdx.x * 128 + threadIdx.x;
+            const size_t col = cb + threadIdx.x;
             float sum = 0.0f;
 #pragma unroll
             for (int y = 0; y < 16; ++y)
@@ -745,12 +788,13 @@ __global__ void __launch_bounds__(kBlock) k_act_bwd16(const float *__restrict__ 
 // the bits the GEMM writes; g is written out as the grad and used at once,
 // so the [m, n] grad is written once and never read back.  A block is four
 // waves over 128 columns, wave w taking columns 32 w .. 32 w + 31 of the
-// block's rows, 64 rows per step (two 32 x 32 products, every load of the
-// step issued first): the products go through a per-wave LDS tile to one
-// half row of 16 columns per lane (rows lane / 2 and lane / 2 + 32), where
-// z is read, g, dz and the column sums formed as in k_act_bwd16 (the lane's
-// rows in order, then the 32 row lanes in order).  Without d16 (and
-// part) the pass is the narrow dgrad alone.
+// block's rows, 32 rows per step (one 32 x 32 product; the next step's loads
+// issued before the current step's product): the product goes through a
+// per-wave LDS tile to four columns of four rows per lane (columns
+// 4 (lane % 8) .. + 3 of rows lane / 8 + 8 i, so each z load of a wave reads
+// 8 whole 128-byte row segments), where z is read, g, dz and the column sums
+// formed as in k_act_bwd16 (the lane's rows in order, then the 8 row lanes
+// in order).  Without d16 (and part) the pass is the narrow dgrad alone.
 typedef __bf16 nbf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 nf16x8 __attribute__((ext_vector_type(8)));
 typedef float nf32x16 __attribute__((ext_vector_type(16)));
@@ -767,24 +811,162 @@ __device__ __forceinline__ nf32x16 narrow_mfma(const uint4 &a, const uint4 &b, c
 }
 
 constexpr int kNarrowLd = 36; // LDS tile pitch (floats): 16-byte rows
-constexpr int kNarrowT = 2;   // 32-row MFMA tiles per step, every load of a step issued first
 
-template <int ACT, bool F16>
+// what one lane of a narrow pass works with: the fixed arguments and the
+// lane's offsets from a step's first row (row lane / 8 of the step in z, g
+// and dz; its fragment row lane % 32 in dn)
+struct narrow_lane {
+    const uint16_t *dn;
+    const float *z;
+    float *g;
+    uint16_t *d16;
+    size_t re, n, ldd, jc;
+    size_t zo, dzo, ao;
+    int kw, lane;
+};
+
+// the loads of the 32-row step at i0: the dz fragment and z of the lane's
+// four rows.  In a step with rows past re (the last), those rows read row
+// re - 1 instead (zeroed at the product, not used).
+template <int ACT, bool VEC>
+__device__ __forceinline__ void narrow_load(const narrow_lane &L, size_t i0, uint4 &a, float (&zv)[4][4])
+{
+    const int h = L.lane >> 5, rl = L.lane >> 3;
+    if (i0 + 32 <= L.re) {
+        a = *reinterpret_cast<const uint4 *>(L.dn + i0 * (size_t)L.kw + L.ao);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float *zr = L.z + (i0 + 8 * i) * L.n + L.zo;
+            if (ACT && VEC) {
+                const float4 v = *reinterpret_cast<const float4 *>(zr);
+                zv[i][0] = v.x, zv[i][1] = v.y, zv[i][2] = v.z, zv[i][3] = v.w;
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    zv[i][q] = (ACT && L.jc + q < L.n) ? zr[q] : 0.0f;
+            }
+        }
+        return;
+    }
+    const size_t ia = i0 + (L.lane & 31);
+    a = *reinterpret_cast<const uint4 *>(L.dn + (ia < L.re ? ia : L.re - 1) * (size_t)L.kw +
+                                         (8 * h < L.kw ? 8 * h : 0));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const size_t r = i0 + rl + 8 * i, rr = r < L.re ? r : L.re - 1;
+        if (ACT && VEC) {
+            const float4 v = *reinterpret_cast<const float4 *>(L.z + rr * L.n + L.jc);
+            zv[i][0] = v.x, zv[i][1] = v.y, zv[i][2] = v.z, zv[i][3] = v.w;
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                zv[i][q] = (ACT && L.jc + q < L.n) ? L.z[rr * L.n + L.jc + q] : 0.0f;
+        }
+    }
+}
+
+// the step at i0: the product through the wave's tile, then g, dz and the
+// column sums of the lane's four rows
+template <int ACT, bool F16, int DT, bool VEC>
+__device__ __forceinline__ void narrow_step(const narrow_lane &L, float (*tile)[kNarrowLd], const uint4 &araw,
+                                            const uint4 &bfrag, const float (&zv)[4][4], size_t i0, float (&cs)[4])
+{
+    const int h = L.lane >> 5, rl = L.lane >> 3;
+    const uint4 zero4 = make_uint4(0u, 0u, 0u, 0u);
+    const uint4 afrag = (i0 + (L.lane & 31) < L.re && 8 * h < L.kw) ? araw : zero4;
+    nf32x16 acc;
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+        acc[e] = 0.0f;
+    acc = narrow_mfma<F16>(afrag, bfrag, acc);
+#pragma unroll
+    for (int s = 1; s < 4; ++s)
+        acc = narrow_mfma<F16>(zero4, zero4, acc);
+    // lane holds column lane % 32 of rows 8 (e / 4) + 4 h + e % 4
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+        tile[8 * (e >> 2) + 4 * h + (e & 3)][L.lane & 31] = acc[e];
+    __builtin_amdgcn_wave_barrier();
+    float gv[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float4 v = *reinterpret_cast<const float4 *>(&tile[rl + 8 * i][4 * (L.lane & 7)]);
+        gv[i][0] = v.x, gv[i][1] = v.y, gv[i][2] = v.z, gv[i][3] = v.w;
+    }
+    __builtin_amdgcn_wave_barrier(); // every lane has read the tile before the next step writes it
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const bool rin = i0 + rl + 8 * i < L.re, row = rin && L.jc < L.n;
+        float d[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+#pragma clang fp contract(off)
+            const bool in = row && L.jc + q < L.n;
+            d[q] = in ? (ACT ? gv[i][q] * act_grad(ACT, zv[i][q]) : gv[i][q]) : 0.0f;
+            cs[q] += d[q];
+        }
+        if (!rin)
+            continue;
+        if (L.g && row) {
+            float *gr = L.g + (i0 + 8 * i) * L.n + L.zo;
+            if (VEC) {
+                *reinterpret_cast<float4 *>(gr) = make_float4(gv[i][0], gv[i][1], gv[i][2], gv[i][3]);
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    if (L.jc + q < L.n)
+                        gr[q] = gv[i][q];
+            }
+        }
+        // columns past n store zeros; ldd % 8 == 0 and jc % 4 == 0, so the
+        // lane's 4 columns are inside ldd whole or not at all
+        if (L.d16 && L.jc < L.ldd)
+            *reinterpret_cast<uint2 *>(L.d16 + (i0 + 8 * i) * L.ldd + L.dzo) =
+                make_uint2(to16x2(DT, d[0], d[1]), to16x2(DT, d[2], d[3]));
+    }
+}
+
+// the steps of rows [rb, re), each step's loads issued before the
+// previous step's product
+template <int ACT, bool F16, int DT, bool VEC>
+__device__ __forceinline__ void narrow_rows(const narrow_lane &L, float (*tile)[kNarrowLd], const uint4 &bfrag,
+                                            size_t rb, float (&cs)[4])
+{
+    if (rb >= L.re)
+        return;
+    uint4 aa, ab;
+    float za[4][4], zb[4][4];
+    narrow_load<ACT, VEC>(L, rb, aa, za);
+    for (size_t i0 = rb;; i0 += 64) {
+        if (i0 + 32 >= L.re) {
+            narrow_step<ACT, F16, DT, VEC>(L, tile, aa, bfrag, za, i0, cs);
+            break;
+        }
+        narrow_load<ACT, VEC>(L, i0 + 32, ab, zb);
+        narrow_step<ACT, F16, DT, VEC>(L, tile, aa, bfrag, za, i0, cs);
+        if (i0 + 64 >= L.re) {
+            narrow_step<ACT, F16, DT, VEC>(L, tile, ab, bfrag, zb, i0 + 32, cs);
+            break;
+        }
+        narrow_load<ACT, VEC>(L, i0 + 64, aa, za);
+        narrow_step<ACT, F16, DT, VEC>(L, tile, ab, bfrag, zb, i0 + 32, cs);
+    }
+}
+
+template <int ACT, bool F16, int DT>
 __global__ void __launch_bounds__(kBlock, 4) k_act_bwd16n(const uint16_t *__restrict__ dn, const uint16_t *__restrict__ wn,
                                                        int kw, uint16_t *__restrict__ wsnap, float *__restrict__ g,
                                                        const float *__restrict__ z, size_t m, size_t n,
-                                                       uint16_t *__restrict__ d16, size_t ldd, int dtype,
+                                                       uint16_t *__restrict__ d16, size_t ldd,
                                                        float *__restrict__ part, size_t rpb)
 {
-    constexpr int T = kNarrowT;
-    __shared__ __attribute__((aligned(16))) float tile[4][32 * T][kNarrowLd];
+    __shared__ __attribute__((aligned(16))) float tile[4][32][kNarrowLd];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const size_t j0 = (size_t)blockIdx.x * 128 + (size_t)wave * 32;
     const size_t rb = (size_t)blockIdx.y * rpb, re = rb + rpb < m ? rb + rpb : m;
     const int h = lane >> 5;
-    const uint4 zero4 = make_uint4(0u, 0u, 0u, 0u);
     // the weights' fragment: row j0 + lane % 32, k 8 h .. 8 h + 7
-    uint4 bfrag = zero4;
+    uint4 bfrag = make_uint4(0u, 0u, 0u, 0u);
     {
         const size_t j = j0 + (lane & 31);
         if (j < n && 8 * h < kw) {
@@ -795,114 +977,28 @@ __global__ void __launch_bounds__(kBlock, 4) k_act_bwd16n(const uint16_t *__rest
                 *reinterpret_cast<uint4 *>(wsnap + j * (size_t)kw + 8 * h) = bfrag;
         }
     }
-    // after the transpose: rows r, r + 32, ... of the step, columns c .. c + 15
-    const int r = lane >> 1, c = 16 * (lane & 1);
-    const size_t jc = j0 + c;
-    const bool vec = jc + 16 <= n && (n & 3) == 0 && ((((uintptr_t)g) | ((uintptr_t)z)) & 15) == 0;
-    float cs[16];
-#pragma unroll
-    for (int q = 0; q < 16; ++q)
-        cs[q] = 0.0f;
-    for (size_t i0 = rb; i0 < re; i0 += 32 * T) {
-        // every load of the step first: the dz fragments (rows past re read
-        // row re - 1, zeroed below) and z of the lane's rows
-        uint4 araw[T];
-#pragma unroll
-        for (int t = 0; t < T; ++t) {
-            const size_t ia = i0 + 32 * t + (lane & 31);
-            araw[t] = *reinterpret_cast<const uint4 *>(dn + (ia < re ? ia : re - 1) * (size_t)kw +
-                                                       (8 * h < kw ? 8 * h : 0));
-        }
-        float zv[T][16];
-#pragma unroll
-        for (int t = 0; t < T; ++t) {
-            const size_t i = i0 + 32 * t + r < re ? i0 + 32 * t + r : re - 1;
-            if (ACT && vec) {
-#pragma unroll
-                for (int q = 0; q < 16; q += 4) {
-                    const float4 v = *reinterpret_cast<const float4 *>(z + i * n + jc + q);
-                    zv[t][q] = v.x, zv[t][q + 1] = v.y, zv[t][q + 2] = v.z, zv[t][q + 3] = v.w;
-                }
-            } else {
-#pragma unroll
-                for (int q = 0; q < 16; ++q)
-                    zv[t][q] = (ACT && jc + q < n) ? z[i * n + jc + q] : 0.0f;
-            }
-        }
-        // the products: tile t is rows i0 + 32 t .. + 31; lane holds column
-        // lane % 32 of rows 8 (e / 4) + 4 h + e % 4
-#pragma unroll
-        for (int t = 0; t < T; ++t) {
-            const uint4 afrag = (i0 + 32 * t + (lane & 31) < re && 8 * h < kw) ? araw[t] : zero4;
-            nf32x16 acc;
-#pragma unroll
-            for (int e = 0; e < 16; ++e)
-                acc[e] = 0.0f;
-            acc = narrow_mfma<F16>(afrag, bfrag, acc);
-#pragma unroll
-            for (int s = 1; s < 4; ++s)
-                acc = narrow_mfma<F16>(zero4, zero4, acc);
-#pragma unroll
-            for (int e = 0; e < 16; ++e)
-                tile[wave][32 * t + 8 * (e >> 2) + 4 * h + (e & 3)][lane & 31] = acc[e];
-        }
-        __builtin_amdgcn_wave_barrier();
-#pragma unroll
-        for (int t = 0; t < T; ++t) {
-            float gv[16];
-#pragma unroll
-            for (int q = 0; q < 16; q += 4) {
-                const float4 v = *reinterpret_cast<const float4 *>(&tile[wave][32 * t + r][c + q]);
-                gv[q] = v.x, gv[q + 1] = v.y, gv[q + 2] = v.z, gv[q + 3] = v.w;
-            }
-            const size_t i = i0 + 32 * t + r;
-            const bool row = i < re && jc < n;
-            float d[16];
-#pragma unroll
-            for (int q = 0; q < 16; ++q) {
-                const bool in = row && jc + q < n;
-                d[q] = in ? (ACT ? gv[q] * act_grad(ACT, zv[t][q]) : gv[q]) : 0.0f;
-                cs[q] += d[q];
-            }
-            if (!row)
-                continue;
-            if (g && vec) {
-#pragma unroll
-                for (int q = 0; q < 16; q += 4)
-                    *reinterpret_cast<float4 *>(g + i * n + jc + q) =
-                        make_float4(gv[q], gv[q + 1], gv[q + 2], gv[q + 3]);
-            } else if (g) {
-#pragma unroll
-                for (int q = 0; q < 16; ++q)
-                    if (jc + q < n)
-                        g[i * n + jc + q] = gv[q];
-            }
-            if (d16) {
-                // columns past n store zeros; ldd % 8 == 0, so the lane's 16
-                // columns are within ldd whole or by their first 8
-                uint32_t w[8];
-#pragma unroll
-                for (int q = 0; q < 8; ++q)
-                    w[q] = to16x2(dtype, d[2 * q], d[2 * q + 1]);
-                uint4 *dst = reinterpret_cast<uint4 *>(d16 + i * ldd + jc);
-                dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
-                if (jc + 16 <= ldd)
-                    dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
-            }
-        }
-        __builtin_amdgcn_wave_barrier(); // every lane has read the tile before the next step writes it
-    }
+    const size_t jc = j0 + 4 * (size_t)(lane & 7), rl = (size_t)(lane >> 3);
+    const narrow_lane L = {dn,          z,           g,
+                           d16,         re,          n,
+                           ldd,         jc,          rl * n + jc,
+                           rl * ldd + jc, (size_t)(lane & 31) * kw + (8 * h < kw ? 8 * h : 0), kw,
+                           lane};
+    // the wave's 32 columns inside n: 16-byte accesses for every lane
+    const bool vec = j0 + 32 <= n && (n & 3) == 0 && ((((uintptr_t)g) | ((uintptr_t)z)) & 15) == 0;
+    float cs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (vec)
+        narrow_rows<ACT, F16, DT, true>(L, tile[wave], bfrag, rb, cs);
+    else
+        narrow_rows<ACT, F16, DT, false>(L, tile[wave], bfrag, rb, cs);
     if (part) {
-        // the 32 row lanes of each column half, in row order
+        // the 8 row lanes of each column, in row order
         __builtin_amdgcn_wave_barrier();
-#pragma unroll
-        for (int q = 0; q < 16; q += 4)
-            *reinterpret_cast<float4 *>(&tile[wave][r][c + q]) = make_float4(cs[q], cs[q + 1], cs[q + 2], cs[q + 3]);
+        *reinterpret_cast<float4 *>(&tile[wave][lane >> 3][4 * (lane & 7)]) = make_float4(cs[0], cs[1], cs[2], cs[3]);
         __builtin_amdgcn_wave_barrier();
         if (lane < 32) {
             float sum = 0.0f;
-#pragma unroll 8
-            for (int y = 0; y < 32; ++y)
+#pragma unroll
+            for (int y = 0; y < 8; ++y)
                 sum += tile[wave][y][lane];
             const size_t col = j0 + lane;
             if (col < n)
@@ -1313,12 +1409,22 @@ extern "C" int pgk_act_bwd16(int act, const float *g, const float *z, size_t m, 
     const unsigned gx = (unsigned)((ldd + 127) / 128);
     float *part = db ? (float *)ws : nullptr;
     const dim3 grid(gx, (unsigned)nrb);
-    if (act == 0)
-        hipLaunchKernelGGL(k_act_bwd16<0>, grid, dim3(kBlock), 0, (hipStream_t)s, g, z, m, n, d16, ldd, dtype, part, rpb);
+#define PGK_ACT_BWD(A, D)                                                                                              \
+    hipLaunchKernelGGL((k_act_bwd16<A, D>), grid, dim3(kBlock), 0, (hipStream_t)s, g, z, m, n, d16, ldd, part, rpb)
+    const bool f16 = dtype == 1;
+    if (act == 0 && f16)
+        PGK_ACT_BWD(0, 1);
+    else if (act == 0)
+        PGK_ACT_BWD(0, 2);
+    else if (act == 1 && f16)
+        PGK_ACT_BWD(1, 1);
     else if (act == 1)
-        hipLaunchKernelGGL(k_act_bwd16<1>, grid, dim3(kBlock), 0, (hipStream_t)s, g, z, m, n, d16, ldd, dtype, part, rpb);
+        PGK_ACT_BWD(1, 2);
+    else if (f16)
+        PGK_ACT_BWD(2, 1);
     else
-        hipLaunchKernelGGL(k_act_bwd16<2>, grid, dim3(kBlock), 0, (hipStream_t)s, g, z, m, n, d16, ldd, dtype, part, rpb);
+        PGK_ACT_BWD(2, 2);
+#undef PGK_ACT_BWD
     if (db)
         hipLaunchKernelGGL(k_colsum_fin, dim3((unsigned)((n + 63) / 64)), dim3(64), 0, (hipStream_t)s, part, nrb, n,
                            db, db_beta);
@@ -1342,22 +1448,30 @@ extern "C" int pgk_act_bwd16n(int act, const uint16_t *dn, const uint16_t *wn, i
     const unsigned gx = (unsigned)((ldd + 127) / 128);
     float *part = db ? (float *)ws : nullptr;
     const dim3 grid(gx, (unsigned)nrb);
-#define PGK_NARROW(A, F)                                                                                               \
-    hipLaunchKernelGGL((k_act_bwd16n<A, F>), grid, dim3(kBlock), 0, (hipStream_t)s, dn, wn, kw, wsnap, g, z, m, n, d16, \
-                       ldd, dtype, part, rpb)
+#define PGK_NARROW(A, F, D)                                                                                            \
+    hipLaunchKernelGGL((k_act_bwd16n<A, F, D>), grid, dim3(kBlock), 0, (hipStream_t)s, dn, wn, kw, wsnap, g, z, m, n,  \
+                       d16, ldd, part, rpb)
+#define PGK_NARROW_DT(A, F)                                                                                            \
+    do {                                                                                                               \
+        if (dtype == 1)                                                                                                \
+            PGK_NARROW(A, F, 1);                                                                                       \
+        else                                                                                                           \
+            PGK_NARROW(A, F, 2);                                                                                       \
+    } while (0)
     const bool f16 = ndtype == 1;
     if (act == 0 && f16)
-        PGK_NARROW(0, true);
+        PGK_NARROW_DT(0, true);
     else if (act == 0)
-        PGK_NARROW(0, false);
+        PGK_NARROW_DT(0, false);
     else if (act == 1 && f16)
-        PGK_NARROW(1, true);
+        PGK_NARROW_DT(1, true);
     else if (act == 1)
-        PGK_NARROW(1, false);
+        PGK_NARROW_DT(1, false);
     else if (f16)
-        PGK_NARROW(2, true);
+        PGK_NARROW_DT(2, true);
     else
-        PGK_NARROW(2, false);
+        PGK_NARROW_DT(2, false);
+#undef PGK_NARROW_DT
 #undef PGK_NARROW
     if (db)
         hipLaunchKernelGGL(k_colsum_fin, dim3((unsigned)((n + 63) / 64)), dim3(64), 0, (hipStream_t)s, part, nrb, n,
