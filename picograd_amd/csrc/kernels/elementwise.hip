@@ -1012,8 +1012,20 @@ __global__ void __launch_bounds__(64) k_colsum_fin(const float *__restrict__ par
 {
     for (size_t c = (size_t)blockIdx.x * blockDim.x + threadIdx.x; c < n; c += (size_t)gridDim.x * blockDim.x) {
         float acc = 0.0f;
+        size_t b = 0;
+        // 32 loads in flight before their (ordered) adds: a launch of a few
+        // waves, paced by memory latency
+        for (; b + 32 <= nblk; b += 32) {
+            float v[32];
+#pragma unroll
+            for (int q = 0; q < 32; ++q)
+                v[q] = part[(b + q) * n + c];
+#pragma unroll
+            for (int q = 0; q < 32; ++q)
+                acc += v[q];
+        }
 #pragma unroll 8
-        for (size_t b = 0; b < nblk; ++b)
+        for (; b < nblk; ++b)
             acc += part[b * n + c];
         out[c] = beta ? out[c] + acc : acc;
     }
