@@ -245,11 +245,14 @@ def test_pending_grad_keeps_the_weights_it_was_formed_with(lib, oracle, keep_dz)
 
 
 @pytest.mark.parametrize("M,N,act", [(2730, 20, RELU), (4096, 16, NONE), (1, 3, RELU), (257, 1000, RELU),
-                                     (4096, 10, GELU)])
+                                     (4096, 10, GELU), (3000, 4096, GELU), (1100, 640, RELU), (2050, 200, GELU)])
 def test_small_activation_pass(lib, oracle, keep_dz, M, N, act):
     """The activation pass at narrow and ragged widths (ldd 8 to 1000, one
-    row up to 4096): dz bit for bit (ReLU, none), within one ulp (GELU), db
-    within the summation bound."""
+    row up to 4096) and at wide ones whose row blocks take an odd number of
+    row pairs (3000 x 4096: 96 rows per block), one pair (1100 x 640), or
+    pairs and then single rows beside a partial column block (2050 x 200):
+    dz bit for bit (ReLU, none), within one ulp (GELU), db within the
+    summation bound."""
     print(f"small activation pass M={M} N={N} act={act}", flush=True)
     rng = np.random.default_rng(M * 7 + N)
     dt = BF16
