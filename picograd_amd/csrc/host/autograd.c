@@ -201,6 +201,7 @@ pg_tensor *pga_grad_for_write(pg_node *n, int *beta)
      * also writes the copy marks it current after its launch) */
     if (n->grad->data_ref)
         n->grad->data_ref->shadow_stale = true;
+    pgm_colsum_flush_for(n->grad); /* its deferred sums land first */
     if (n->grad->pg_flags & PG_TENSOR_ZERO_PENDING) {
         n->grad->pg_flags &= ~PG_TENSOR_ZERO_PENDING;
         pgt_overwrite(n->grad);

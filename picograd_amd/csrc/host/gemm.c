@@ -766,6 +766,37 @@ static bool g_keep_dz;
  * producing linear16 node's activation pass when they can be */
 static bool g_narrow = true;
 
+/* The bias grad of the last activation pass whose row-block partials are
+ * not yet added: the next activation pass adds them in a row of extra
+ * blocks of its own launch (one launch less per layer), or
+ * pgm_colsum_flush does, at the end of the backward walk and before that
+ * grad is taken for writing again.  The partials sit in scratch slot
+ * g_fin_slot; the next pass writes its own into the other slot.  The
+ * additions are k_colsum_fin's either way (the same bits). */
+#define PGM_FIN_SLOT_A 3
+#define PGM_FIN_SLOT_B 6
+static pgk_colsum_job g_fin;
+static int g_fin_slot = PGM_FIN_SLOT_A;
+
+void pgm_colsum_flush(void)
+{
+    if (!g_fin.part)
+        return;
+    const pgk_colsum_job j = g_fin;
+    g_fin = (pgk_colsum_job){0};
+    pgd_check(pgk_colsum_run(&j, pgd_stream()), "linear16 bias grad sums");
+}
+
+void pgm_colsum_flush_for(const pg_tensor *t)
+{
+    const pg_data_ref *r = t ? t->data_ref : NULL;
+    if (!g_fin.part || !r || !r->ptr)
+        return;
+    const char *lo = r->ptr, *p = (const char *)g_fin.out;
+    if (p + g_fin.n * sizeof(float) > lo && p < lo + r->nbytes)
+        pgm_colsum_flush();
+}
+
 void pgm_linear16_free_ctx(void *ctx)
 {
     lin16_ctx *cx = ctx;
@@ -814,7 +845,7 @@ static void narrow_dgrad(pg_node *px, pg_tensor *gx, pg_tensor *w, const uint16_
         p = calloc(1, sizeof *p);
     if (!p) {
         pgd_check(pgk_act_bwd16n(0, dz16, qw, (int)ld, dt, NULL, gx->dev, NULL, M, K, NULL, up8(K), 0, NULL, 0, NULL,
-                                 pgd_stream()),
+                                 NULL, NULL, pgd_stream()),
                   "linear16 narrow dgrad");
         return;
     }
@@ -860,8 +891,13 @@ void pgm_linear16_backward(pg_node *n)
         pg_tensor *gb = pga_grad_for_write(pb, &dbeta);
         db = gb ? gb->dev : NULL;
     }
+    /* the pass adds the previous pass's deferred bias-grad sums in its own
+     * launch and defers its own, their partials in the other scratch slot */
+    const pgk_colsum_job fold = g_fin;
+    const int slot = fold.part && g_fin_slot == PGM_FIN_SLOT_A ? PGM_FIN_SLOT_B : PGM_FIN_SLOT_A;
+    pgk_colsum_job next = {0};
     size_t wsz = db ? pgk_act_bwd16_workspace(M, N) : 0;
-    void *ws = wsz ? pgd_scratch(3, wsz) : NULL;
+    void *ws = wsz ? pgd_scratch(slot, wsz) : NULL;
     int tk = pgd_tbegin(PGD_T_STAGE);
     /* the grad left pending as the next layer's narrow dgrad is formed in
      * the activation pass, each element used for dz there; the grad itself
@@ -876,7 +912,8 @@ void pgm_linear16_backward(pg_node *n)
         uint16_t *wsnap = pgd_malloc(wsb);
         ok = (!wsz || ws) &&
              pgd_check(pgk_act_bwd16n(cx->act, np->dn, np->wn, np->kw, np->dtype, wsnap, wsnap ? NULL : n->grad->dev,
-                                      cx->z ? cx->z->dev : NULL, M, N, dz16, N8, dt, db, dbeta, ws, pgd_stream()),
+                                      cx->z ? cx->z->dev : NULL, M, N, dz16, N8, dt, db, dbeta, ws,
+                                      fold.part ? &fold : NULL, &next, pgd_stream()),
                        "linear16 act backward (narrow dgrad)");
         if (ok && wsnap) {
             if (np->own[1])
@@ -896,8 +933,12 @@ void pgm_linear16_backward(pg_node *n)
         pgt_settle(n->grad);
         ok = (!wsz || ws) &&
              pgd_check(pgk_act_bwd16(cx->act, n->grad->dev, cx->z ? cx->z->dev : NULL, M, N, dz16, N8, dt, db,
-                                     dbeta, ws, pgd_stream()),
+                                     dbeta, ws, fold.part ? &fold : NULL, &next, pgd_stream()),
                        "linear16 act backward");
+    }
+    if (ok) { /* the folded job ran in the pass */
+        g_fin = next;
+        g_fin_slot = slot;
     }
     pgd_tend(tk);
     /* each grad taken for writing once (that clears a pending zero and

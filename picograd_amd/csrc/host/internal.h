@@ -77,7 +77,7 @@ bool pgd_check(int status, const char *what);
 /* a scratch device buffer of at least nbytes, reused across calls on the
  * stream (grows, never shrinks) */
 void *pgd_scratch(int slot, size_t nbytes);
-#define PGD_SCRATCH_SLOTS 6 /* slot 5: a GEMM on the side stream */
+#define PGD_SCRATCH_SLOTS 7 /* slot 5: a GEMM on the side stream; 3 and 6: linear16 bias-grad partials */
 /* kernel timer (pg_amd_timer_*): kinds and bracket calls */
 enum {
     PGD_T_JIT_MAIN = 0, PGD_T_JIT_FIN = 1, PGD_T_GEMM16 = 2, PGD_T_SGD = 3, PGD_T_STAGE = 4,
@@ -186,6 +186,11 @@ pg_tensor *pgm_matmul_forward(const pg_tensor *a, const pg_tensor *b);
  * storage replaces its staging pass), else 0 */
 int pgm_mm16_grad16(const pg_node *n);
 void pgm_matmul_backward(pg_node *n);
+/* a linear16 bias grad whose last step (the sum of its row-block partials)
+ * the next activation pass was to run: run it now (the walk's end), or now
+ * if it writes into t's storage (t is about to be written) */
+void pgm_colsum_flush(void);
+void pgm_colsum_flush_for(const pg_tensor *t);
 /* pg_amd_ag_linear16's backward and the destructor of its node context
  * (the kept pre-activation), called by pg_node_free */
 void pgm_linear16_backward(pg_node *n);

@@ -152,7 +152,7 @@ bool pgt_settle(const pg_tensor *t)
         const pg_narrow_pending *p = r->narrow;
         r->shadow_stale = true;
         ok = pgd_check(pgk_act_bwd16n(0, p->dn, p->wn, p->kw, p->dtype, NULL, (float *)r->ptr, NULL, p->m, p->n,
-                                      NULL, (p->n + 7) & ~(size_t)7, 0, NULL, 0, NULL, pgd_stream()),
+                                      NULL, (p->n + 7) & ~(size_t)7, 0, NULL, 0, NULL, NULL, NULL, pgd_stream()),
                        "pending narrow product");
         pgt_narrow_release(r);
     }

@@ -627,6 +627,7 @@ static bool walk(pg_node *loss, const pg_tensor *seed, wmode mode)
         }
     }
 out:
+    pgm_colsum_flush(); /* a bias grad's sums still deferred to a next pass */
     for (size_t k = 0; k < N; k++)
         order.v[k]->mark = 0;
     free(order.v);

@@ -621,6 +621,32 @@ __global__ void __launch_bounds__(kBlock) k_sgd(sgd_table tab, float lr, float m
     }
 }
 
+// ---------------------------------------------------------------- bias-grad sums
+// job.out[c] (beta ? += : =) sum_b job.part[b n + c], b in order, for
+// columns c0, c0 + step, ...: 32 loads in flight before their ordered adds
+// (a launch of few waves, paced by memory latency)
+__device__ __forceinline__ void colsum_cols(const pgk_colsum_job &job, size_t c0, size_t step)
+{
+    const size_t n = job.n, nblk = job.nblk;
+    for (size_t c = c0; c < n; c += step) {
+        float acc = 0.0f;
+        size_t b = 0;
+        for (; b + 32 <= nblk; b += 32) {
+            float v[32];
+#pragma unroll
+            for (int q = 0; q < 32; ++q)
+                v[q] = job.part[(b + q) * n + c];
+#pragma unroll
+            for (int q = 0; q < 32; ++q)
+                acc += v[q];
+        }
+#pragma unroll 8
+        for (; b < nblk; ++b)
+            acc += job.part[b * n + c];
+        job.out[c] = job.beta ? job.out[c] + acc : acc;
+    }
+}
+
 // ---------------------------------------------------------------- linear backward
 // dz = g * act'(z) (act 0: dz = g) for a [m, n] f32 grad, written as RNE
 // 16-bit rows of ldd (ldd % 8 == 0) with zeros in columns [n, ldd); DT 1
@@ -709,12 +735,22 @@ __device__ __forceinline__ void act_bwd_pair(const float4 (&gq)[2][2], const flo
 template <int ACT, int DT>
 __global__ void __launch_bounds__(kBlock) k_act_bwd16(const float *__restrict__ g, const float *__restrict__ z,
                                                       size_t m, size_t n, uint16_t *__restrict__ d16, size_t ldd,
-                                                      float *__restrict__ part, size_t rpb)
+                                                      float *__restrict__ part, size_t rpb, pgk_colsum_job fin)
 {
     __shared__ float red[16][129];
+    // with an earlier pass's bias-grad sums to finish, the first row of
+    // blocks adds them and the pass's row blocks follow
+    size_t by = blockIdx.y;
+    if (fin.part) {
+        if (by == 0) {
+            colsum_cols(fin, (size_t)blockIdx.x * kBlock + threadIdx.x, (size_t)gridDim.x * kBlock);
+            return;
+        }
+        --by;
+    }
     const int cx = threadIdx.x & 15, ry = threadIdx.x >> 4;
     const size_t cb = (size_t)blockIdx.x * 128, c0 = cb + (size_t)cx * 4;
-    const size_t rb = (size_t)blockIdx.y * rpb, re = rb + rpb < m ? rb + rpb : m;
+    const size_t rb = by * rpb, re = rb + rpb < m ? rb + rpb : m;
     const bool lo = c0 < ldd, hi = c0 + 64 < ldd;
     // every column of the block inside n: the 16-byte path for every lane
     const bool vec = cb + 128 <= n && (n & 3) == 0 && ((((uintptr_t)g) | ((uintptr_t)z)) & 15) == 0;
@@ -773,7 +809,7 @@ __global__ void __launch_bounds__(kBlock) k_act_bwd16(const float *__restrict__ 
             for (int y = 0; y < 16; ++y)
                 sum += red[y][threadIdx.x];
             if (col < n)
-                part[(size_t)blockIdx.y * n + col] = sum;
+                part[by * n + col] = sum;
         }
     }
 }
@@ -958,12 +994,22 @@ __global__ void __launch_bounds__(kBlock, 4) k_act_bwd16n(const uint16_t *__rest
                                                        int kw, uint16_t *__restrict__ wsnap, float *__restrict__ g,
                                                        const float *__restrict__ z, size_t m, size_t n,
                                                        uint16_t *__restrict__ d16, size_t ldd,
-                                                       float *__restrict__ part, size_t rpb)
+                                                       float *__restrict__ part, size_t rpb, pgk_colsum_job fin)
 {
     __shared__ __attribute__((aligned(16))) float tile[4][32][kNarrowLd];
+    // an earlier pass's bias-grad sums: the first row of blocks, as in
+    // k_act_bwd16
+    size_t by = blockIdx.y;
+    if (fin.part) {
+        if (by == 0) {
+            colsum_cols(fin, (size_t)blockIdx.x * kBlock + threadIdx.x, (size_t)gridDim.x * kBlock);
+            return;
+        }
+        --by;
+    }
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const size_t j0 = (size_t)blockIdx.x * 128 + (size_t)wave * 32;
-    const size_t rb = (size_t)blockIdx.y * rpb, re = rb + rpb < m ? rb + rpb : m;
+    const size_t rb = by * rpb, re = rb + rpb < m ? rb + rpb : m;
     const int h = lane >> 5;
     // the weights' fragment: row j0 + lane % 32, k 8 h .. 8 h + 7
     uint4 bfrag = make_uint4(0u, 0u, 0u, 0u);
@@ -973,7 +1019,7 @@ __global__ void __launch_bounds__(kBlock, 4) k_act_bwd16n(const uint16_t *__rest
             bfrag = *reinterpret_cast<const uint4 *>(wn + j * (size_t)kw + 8 * h);
             // the first row block copies the weights it read (the pending
             // product of a grad not written here keeps this copy)
-            if (wsnap && blockIdx.y == 0)
+            if (wsnap && by == 0)
                 *reinterpret_cast<uint4 *>(wsnap + j * (size_t)kw + 8 * h) = bfrag;
         }
     }
@@ -1002,33 +1048,14 @@ __global__ void __launch_bounds__(kBlock, 4) k_act_bwd16n(const uint16_t *__rest
                 sum += tile[wave][y][lane];
             const size_t col = j0 + lane;
             if (col < n)
-                part[(size_t)blockIdx.y * n + col] = sum;
+                part[by * n + col] = sum;
         }
     }
 }
 
-__global__ void __launch_bounds__(64) k_colsum_fin(const float *__restrict__ part, size_t nblk, size_t n,
-                                                   float *__restrict__ out, int beta)
+__global__ void __launch_bounds__(64) k_colsum_fin(pgk_colsum_job job)
 {
-    for (size_t c = (size_t)blockIdx.x * blockDim.x + threadIdx.x; c < n; c += (size_t)gridDim.x * blockDim.x) {
-        float acc = 0.0f;
-        size_t b = 0;
-        // 32 loads in flight before their (ordered) adds: a launch of a few
-        // waves, paced by memory latency
-        for (; b + 32 <= nblk; b += 32) {
-            float v[32];
-#pragma unroll
-            for (int q = 0; q < 32; ++q)
-                v[q] = part[(b + q) * n + c];
-#pragma unroll
-            for (int q = 0; q < 32; ++q)
-                acc += v[q];
-        }
-#pragma unroll 8
-        for (; b < nblk; ++b)
-            acc += part[b * n + c];
-        out[c] = beta ? out[c] + acc : acc;
-    }
+    colsum_cols(job, (size_t)blockIdx.x * blockDim.x + threadIdx.x, (size_t)gridDim.x * blockDim.x);
 }
 
 // ---------------------------------------------------------------- uploads
@@ -1408,21 +1435,65 @@ extern "C" size_t pgk_act_bwd16_workspace(size_t m, size_t n)
     return ((m + rpb - 1) / rpb) * n * sizeof(float);
 }
 
-extern "C" int pgk_act_bwd16(int act, const float *g, const float *z, size_t m, size_t n, uint16_t *d16, size_t ldd,
-                             int dtype, float *db, int db_beta, void *ws, pgk_stream s)
+extern "C" int pgk_colsum_run(const pgk_colsum_job *job, pgk_stream s)
 {
-    if (!m || !n)
+    if (!job || !job->n || !job->nblk)
         return 0;
+    if (!job->part || !job->out)
+        return (int)hipErrorInvalidValue;
+    const size_t blocks = (job->n + 63) / 64;
+    hipLaunchKernelGGL(k_colsum_fin, dim3((unsigned)(blocks < 65535 ? blocks : 65535)), dim3(64), 0, (hipStream_t)s,
+                       *job);
+    return status();
+}
+
+// the job an activation pass finishes in its first row of blocks (none: a
+// zero job, and no extra row)
+static int fold_job(const pgk_colsum_job *fold, pgk_colsum_job *j)
+{
+    *j = pgk_colsum_job{};
+    if (!fold || !fold->n || !fold->nblk)
+        return 0;
+    if (!fold->part || !fold->out)
+        return -1;
+    *j = *fold;
+    return 1;
+}
+
+// the last step of a pass's bias grad: handed to the caller, or launched
+static int finish_db(float *part, size_t nrb, size_t n, float *db, int beta, pgk_colsum_job *defer, pgk_stream s)
+{
+    const pgk_colsum_job j = {part, nrb, n, db, beta};
+    if (defer) {
+        *defer = j;
+        return 0;
+    }
+    return pgk_colsum_run(&j, s);
+}
+
+extern "C" int pgk_act_bwd16(int act, const float *g, const float *z, size_t m, size_t n, uint16_t *d16, size_t ldd,
+                             int dtype, float *db, int db_beta, void *ws, const pgk_colsum_job *fold,
+                             pgk_colsum_job *defer, pgk_stream s)
+{
+    if (defer)
+        *defer = pgk_colsum_job{};
+    pgk_colsum_job fin;
+    const int nf = fold_job(fold, &fin);
+    if (nf < 0)
+        return (int)hipErrorInvalidValue;
+    if (!m || !n)
+        return nf ? pgk_colsum_run(&fin, s) : 0;
     if ((ldd & 7) || ldd < n || (((uintptr_t)d16) & 15) || (act && !z) || (db && !ws) || act < 0 || act > 2)
         return (int)hipErrorInvalidValue;
     const size_t rpb = act_bwd_rpb(m, ldd), nrb = (m + rpb - 1) / rpb;
-    if (nrb > 65535)
+    if (nrb + nf > 65535)
         return (int)hipErrorInvalidValue;
     const unsigned gx = (unsigned)((ldd + 127) / 128);
     float *part = db ? (float *)ws : nullptr;
-    const dim3 grid(gx, (unsigned)nrb);
+    const dim3 grid(gx, (unsigned)(nrb + nf));
 #define PGK_ACT_BWD(A, D)                                                                                              \
-    hipLaunchKernelGGL((k_act_bwd16<A, D>), grid, dim3(kBlock), 0, (hipStream_t)s, g, z, m, n, d16, ldd, part, rpb)
+    hipLaunchKernelGGL((k_act_bwd16<A, D>), grid, dim3(kBlock), 0, (hipStream_t)s, g, z, m, n, d16, ldd, part, rpb,   \
+                       fin)
     const bool f16 = dtype == 1;
     if (act == 0 && f16)
         PGK_ACT_BWD(0, 1);
@@ -1437,32 +1508,39 @@ extern "C" int pgk_act_bwd16(int act, const float *g, const float *z, size_t m, 
     else
         PGK_ACT_BWD(2, 2);
 #undef PGK_ACT_BWD
-    if (db)
-        hipLaunchKernelGGL(k_colsum_fin, dim3((unsigned)((n + 63) / 64)), dim3(64), 0, (hipStream_t)s, part, nrb, n,
-                           db, db_beta);
-    return status();
+    const int st = status();
+    if (st || !db)
+        return st;
+    return finish_db(part, nrb, n, db, db_beta, defer, s);
 }
 
 extern "C" int pgk_act_bwd16n(int act, const uint16_t *dn, const uint16_t *wn, int kw, int ndtype, uint16_t *wsnap,
                               float *g, const float *z, size_t m, size_t n, uint16_t *d16, size_t ldd, int dtype,
-                              float *db, int db_beta, void *ws, pgk_stream s)
+                              float *db, int db_beta, void *ws, const pgk_colsum_job *fold, pgk_colsum_job *defer,
+                              pgk_stream s)
 {
+    if (defer)
+        *defer = pgk_colsum_job{};
+    pgk_colsum_job fin;
+    const int nf = fold_job(fold, &fin);
+    if (nf < 0)
+        return (int)hipErrorInvalidValue;
     if (!m || !n)
-        return 0;
+        return nf ? pgk_colsum_run(&fin, s) : 0;
     if ((ldd & 7) || ldd < n || (((uintptr_t)d16) & 15) || (act && !z) || (db && !ws) || act < 0 || act > 2 ||
         (kw != 8 && kw != 16) || !dn || !wn || (!g && !d16) ||
         ((((uintptr_t)dn) | ((uintptr_t)wn) | ((uintptr_t)wsnap)) & 15) || (((uintptr_t)g) & 3) ||
         (ndtype != 1 && ndtype != 2))
         return (int)hipErrorInvalidValue;
     const size_t rpb = act_bwd_rpb(m, ldd), nrb = (m + rpb - 1) / rpb;
-    if (nrb > 65535)
+    if (nrb + nf > 65535)
         return (int)hipErrorInvalidValue;
     const unsigned gx = (unsigned)((ldd + 127) / 128);
     float *part = db ? (float *)ws : nullptr;
-    const dim3 grid(gx, (unsigned)nrb);
+    const dim3 grid(gx, (unsigned)(nrb + nf));
 #define PGK_NARROW(A, F, D)                                                                                            \
     hipLaunchKernelGGL((k_act_bwd16n<A, F, D>), grid, dim3(kBlock), 0, (hipStream_t)s, dn, wn, kw, wsnap, g, z, m, n,  \
-                       d16, ldd, part, rpb)
+                       d16, ldd, part, rpb, fin)
 #define PGK_NARROW_DT(A, F)                                                                                            \
     do {                                                                                                               \
         if (dtype == 1)                                                                                                \
@@ -1485,8 +1563,8 @@ extern "C" int pgk_act_bwd16n(int act, const uint16_t *dn, const uint16_t *wn, i
         PGK_NARROW_DT(2, false);
 #undef PGK_NARROW_DT
 #undef PGK_NARROW
-    if (db)
-        hipLaunchKernelGGL(k_colsum_fin, dim3((unsigned)((n + 63) / 64)), dim3(64), 0, (hipStream_t)s, part, nrb, n,
-                           db, db_beta);
-    return status();
+    const int st = status();
+    if (st || !db)
+        return st;
+    return finish_db(part, nrb, n, db, db_beta, defer, s);
 }

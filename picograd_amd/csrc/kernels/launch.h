@@ -205,24 +205,41 @@ int pgk_gemm_f32(int ta, int tb, size_t m, size_t n, size_t k, const float *a, s
                  size_t stride_a, const float *b, size_t ldb, size_t stride_b, float *c,
                  size_t ldc, size_t stride_c, size_t batch, int beta, pgk_stream s);
 
+/* The last step of a bias grad: out[c] (beta ? += : =) the sum over the
+ * nblk row-block partials part[b * n + c], b in order. */
+typedef struct {
+    const float *part;
+    size_t nblk, n;
+    float *out;
+    int beta;
+} pgk_colsum_job;
+int pgk_colsum_run(const pgk_colsum_job *job, pgk_stream s);
+
 /* Backward of an activation feeding a 16-bit GEMM: dz = g * act'(z) over
  * a [m, n] f32 grad (act PGK_ACT_*; z the pre-activation, unused for
  * PGK_ACT_NONE), written RNE to d16 rows of ldd (ldd % 8 == 0, zero columns
  * past n); when db is given, db[j] (beta ? += : =) sum_i dz[i, j] in a
- * fixed order (ws holds pgk_act_bwd16_workspace bytes). */
+ * fixed order (ws holds pgk_act_bwd16_workspace bytes): the pass writes the
+ * row-block partials to ws and a second launch adds them, unless defer is
+ * given, which then receives that last step as a job (ws must stay as it is
+ * until the job runs).  A job given as fold (an earlier pass's deferred
+ * one, its partials not in ws) runs in this pass's launch, in a row of extra
+ * blocks. */
 size_t pgk_act_bwd16_workspace(size_t m, size_t n);
 int pgk_act_bwd16(int act, const float *g, const float *z, size_t m, size_t n, uint16_t *d16, size_t ldd,
-                  int dtype, float *db, int db_beta, void *ws, pgk_stream s);
+                  int dtype, float *db, int db_beta, void *ws, const pgk_colsum_job *fold, pgk_colsum_job *defer,
+                  pgk_stream s);
 /* The same pass with g formed in it as the dgrad of a narrow next layer:
  * g = dn . wn^T, dn [m, kw] and wn [n, kw] 16-bit of ndtype (kw 8 or 16,
  * zero columns past the layer's width), with the MFMA sequence of
  * pgk_gemm16's dgrad of those operands (the same bits), used for dz and,
  * when g is given, written to g [m, n] (every element).  With wsnap, wn is
- * copied there (n x kw).  ws as for pgk_act_bwd16.  With d16 and db NULL
- * only g is written (the narrow dgrad itself); g and d16 are not both NULL. */
+ * copied there (n x kw).  ws, fold and defer as for pgk_act_bwd16.  With
+ * d16 and db NULL only g is written (the narrow dgrad itself); g and d16
+ * are not both NULL. */
 int pgk_act_bwd16n(int act, const uint16_t *dn, const uint16_t *wn, int kw, int ndtype, uint16_t *wsnap, float *g,
                    const float *z, size_t m, size_t n, uint16_t *d16, size_t ldd, int dtype, float *db, int db_beta,
-                   void *ws, pgk_stream s);
+                   void *ws, const pgk_colsum_job *fold, pgk_colsum_job *defer, pgk_stream s);
 
 /* multi-tensor SGD */
 typedef struct {
