@@ -29,6 +29,20 @@ inline int grid_for(size_t work_items, int per_thread = 1)
 
 inline int status() { return (int)hipGetLastError(); }
 
+// 16-byte streaming (non-temporal) accesses, for data a kernel reads or
+// writes once
+__device__ __forceinline__ float4 ntl4(const float *q)
+{
+    const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(q));
+    return make_float4(v[0], v[1], v[2], v[3]);
+}
+
+__device__ __forceinline__ void nts4(const float4 &v, float *q)
+{
+    const f32x4 w = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(w, reinterpret_cast<f32x4 *>(q));
+}
+
 // ---------------------------------------------------------------- math
 
 __device__ __forceinline__ float unary_f(int op, float x, float p0, float p1)
@@ -550,11 +564,11 @@ __device__ __forceinline__ void sgd_vec(const pgk_sgd_seg &sg, size_t base, size
     for (int k = 0; k < kSgdVec; ++k) {
         e[k] = base + 4 * ((size_t)threadIdx.x + (size_t)k * kBlock);
         if (FULL || e[k] + 4 <= n) {
-            p[k] = reinterpret_cast<const float4 *>(sg.p + e[k])[0];
-            g[k] = reinterpret_cast<const float4 *>(sg.g + e[k])[0];
+            p[k] = ntl4(sg.p + e[k]);
+            g[k] = ntl4(sg.g + e[k]);
             g[k] = make_float4(sgd_clipped(sg, g[k].x), sgd_clipped(sg, g[k].y), sgd_clipped(sg, g[k].z),
                                sgd_clipped(sg, g[k].w));
-            b[k] = HAS_BUF ? reinterpret_cast<const float4 *>(sg.buf + e[k])[0] : make_float4(0, 0, 0, 0);
+            b[k] = HAS_BUF ? ntl4(sg.buf + e[k]) : make_float4(0, 0, 0, 0);
         }
     }
 #pragma unroll
@@ -564,9 +578,9 @@ __device__ __forceinline__ void sgd_vec(const pgk_sgd_seg &sg, size_t base, size
             sgd_elem(p[k].y, g[k].y, b[k].y, HAS_BUF, lr, mu, damp, wd, nesterov);
             sgd_elem(p[k].z, g[k].z, b[k].z, HAS_BUF, lr, mu, damp, wd, nesterov);
             sgd_elem(p[k].w, g[k].w, b[k].w, HAS_BUF, lr, mu, damp, wd, nesterov);
-            reinterpret_cast<float4 *>(sg.p + e[k])[0] = p[k];
+            nts4(p[k], sg.p + e[k]);
             if (HAS_BUF)
-                reinterpret_cast<float4 *>(sg.buf + e[k])[0] = b[k];
+                nts4(b[k], sg.buf + e[k]);
             if (sg.shadow) {
                 reinterpret_cast<uint2 *>(sg.shadow + e[k])[0] =
                     make_uint2(to16x2(sg.shadow_dtype, p[k].x, p[k].y), to16x2(sg.shadow_dtype, p[k].z, p[k].w));

@@ -19,6 +19,20 @@ constexpr int kBlock = 256;
 
 inline int status() { return (int)hipGetLastError(); }
 
+// 16-byte streaming (non-temporal) accesses: every optimiser array is read
+// and written once per step
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 ntl4(const float *q)
+{
+    const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(q));
+    return make_float4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ void nts4(const float4 &v, float *q)
+{
+    const f32x4 w = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(w, reinterpret_cast<f32x4 *>(q));
+}
+
 // ---------------------------------------------------------------- Adam
 // adam.c:157-177 per element, in the order the reference's -O3 -ffast-math
 // build evaluates it: decay (AdamW shrink or L2 grad term), moments
@@ -99,11 +113,11 @@ __global__ void __launch_bounds__(kBlock) k_adam(adam_table tab, pgk_adam_hyper 
         for (int k = 0; k < kAdamVec; ++k) {
             e[k] = base + 4 * ((size_t)threadIdx.x + (size_t)k * kBlock);
             if (e[k] + 4 <= n) {
-                p[k] = *reinterpret_cast<const float4 *>(P + e[k]);
-                g[k] = clipped4(sg, *reinterpret_cast<const float4 *>(G + e[k]));
-                m[k] = *reinterpret_cast<const float4 *>(M + e[k]);
-                v[k] = *reinterpret_cast<const float4 *>(V + e[k]);
-                vm[k] = ams ? *reinterpret_cast<const float4 *>(VM + e[k]) : make_float4(0, 0, 0, 0);
+                p[k] = ntl4(P + e[k]);
+                g[k] = clipped4(sg, ntl4(G + e[k]));
+                m[k] = ntl4(M + e[k]);
+                v[k] = ntl4(V + e[k]);
+                vm[k] = ams ? ntl4(VM + e[k]) : make_float4(0, 0, 0, 0);
             }
         }
 #pragma unroll
@@ -113,11 +127,11 @@ __global__ void __launch_bounds__(kBlock) k_adam(adam_table tab, pgk_adam_hyper 
                 adam_elem(p[k].y, g[k].y, m[k].y, v[k].y, vm[k].y, ams, h, sg.lr, sg.wd);
                 adam_elem(p[k].z, g[k].z, m[k].z, v[k].z, vm[k].z, ams, h, sg.lr, sg.wd);
                 adam_elem(p[k].w, g[k].w, m[k].w, v[k].w, vm[k].w, ams, h, sg.lr, sg.wd);
-                *reinterpret_cast<float4 *>(P + e[k]) = p[k];
-                *reinterpret_cast<float4 *>(M + e[k]) = m[k];
-                *reinterpret_cast<float4 *>(V + e[k]) = v[k];
+                nts4(p[k], P + e[k]);
+                nts4(m[k], M + e[k]);
+                nts4(v[k], V + e[k]);
                 if (ams)
-                    *reinterpret_cast<float4 *>(VM + e[k]) = vm[k];
+                    nts4(vm[k], VM + e[k]);
                 if (sg.shadow) {
                     *reinterpret_cast<uint2 *>(sg.shadow + e[k]) =
                         make_uint2(to16x2(sg.shadow_dtype, p[k].x, p[k].y), to16x2(sg.shadow_dtype, p[k].z, p[k].w));
