@@ -709,7 +709,8 @@ __device__ __forceinline__ void act_bwd_row(const float (&gv)[8], const float (&
         *reinterpret_cast<uint2 *>(dst + 64) = make_uint2(w[2], w[3]);
 }
 
-// the loads of rows r and r + 16 (off = r * n + c0)
+// the loads of rows r and r + 16 (off = r * n + c0), non-temporal: the
+// grad and the pre-activation are read once
 template <int ACT>
 __device__ __forceinline__ void act_bwd_load2(const float *__restrict__ g, const float *__restrict__ z, size_t off,
                                               size_t n, float4 (&gq)[2][2], float4 (&zq)[2][2])
@@ -717,11 +718,11 @@ __device__ __forceinline__ void act_bwd_load2(const float *__restrict__ g, const
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
         const size_t o = off + 16 * u * n;
-        gq[u][0] = *reinterpret_cast<const float4 *>(g + o);
-        gq[u][1] = *reinterpret_cast<const float4 *>(g + o + 64);
+        gq[u][0] = ntl4(g + o);
+        gq[u][1] = ntl4(g + o + 64);
         if (ACT) {
-            zq[u][0] = *reinterpret_cast<const float4 *>(z + o);
-            zq[u][1] = *reinterpret_cast<const float4 *>(z + o + 64);
+            zq[u][0] = ntl4(z + o);
+            zq[u][1] = ntl4(z + o + 64);
         }
     }
 }
@@ -888,7 +889,7 @@ __device__ __forceinline__ void narrow_load(const narrow_lane &L, size_t i0, uin
         for (int i = 0; i < 4; ++i) {
             const float *zr = L.z + (i0 + 8 * i) * L.n + L.zo;
             if (ACT && VEC) {
-                const float4 v = *reinterpret_cast<const float4 *>(zr);
+                const float4 v = ntl4(zr);
                 zv[i][0] = v.x, zv[i][1] = v.y, zv[i][2] = v.z, zv[i][3] = v.w;
             } else {
 #pragma unroll

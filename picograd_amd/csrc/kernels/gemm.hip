@@ -868,7 +868,7 @@ __global__ void __launch_bounds__(256) k_splitk_sum(splitk_desc d0, splitk_desc 
             const float *p = part + (size_t)r * n + 4 * j;
             f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
             for (int z = 0; z < splits; ++z)
-                acc += *(const f32x4 *)(p + (size_t)z * mn);
+                acc += __builtin_nontemporal_load((const f32x4 *)(p + (size_t)z * mn)); // read once
             f32x4 *q = (f32x4 *)(c + (size_t)r * ldc + 4 * j);
             const f32x4 v = beta ? *q + acc : acc;
             if (!d.has_epi) {
