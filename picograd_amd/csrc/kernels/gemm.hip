@@ -548,8 +548,10 @@ __device__ __forceinline__ void gemm16_block(const gemm_kargs &g, int pid, int n
                 if (v4) {
                     if (!epi.skip_out)
                         *reinterpret_cast<float4 *>(Cb + off) = make_float4(o[0], o[1], o[2], o[3]);
-                    if (epi.z)
-                        *reinterpret_cast<float4 *>(epi.z + off) = make_float4(zv[0], zv[1], zv[2], zv[3]);
+                    if (epi.z) { // read again only by the backward, much later
+                        const f32x4 zz = {zv[0], zv[1], zv[2], zv[3]};
+                        __builtin_nontemporal_store(zz, reinterpret_cast<f32x4 *>(epi.z + off));
+                    }
                     if (epi.c16)
                         *reinterpret_cast<uint2 *>(epi.c16 + off) =
                             make_uint2(to16x2(epi.dtype16, o[0], o[1]), to16x2(epi.dtype16, o[2], o[3]));
@@ -569,6 +571,9 @@ __device__ __forceinline__ void gemm16_block(const gemm_kargs &g, int pid, int n
             }
         }
     } else {
+        // non-temporal stores: the write burst passes the caches by (config
+        // 3's GEMM pair 213 -> 210 us and the cast pass after it faster,
+        // config 5 +1.6 %)
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
 #pragma unroll
@@ -581,8 +586,7 @@ __device__ __forceinline__ void gemm16_block(const gemm_kargs &g, int pid, int n
                     const int row = m0 + wm * WM + i * 32 + (e >> 2) * 8 + lk * 4 + (e & 3);
                     if (row < M) {
                         float *p = Cb + (size_t)row * ldc + col;
-                        const float v = acc[i][j][e];
-                        *p = beta ? *p + v : v;
+                        __builtin_nontemporal_store(beta ? *p + acc[i][j][e] : acc[i][j][e], p);
                     }
                 }
             }
