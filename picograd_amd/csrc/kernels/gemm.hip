@@ -571,9 +571,11 @@ __device__ __forceinline__ void gemm16_block(const gemm_kargs &g, int pid, int n
             }
         }
     } else {
-        // non-temporal stores: the write burst passes the caches by (config
-        // 3's GEMM pair 213 -> 210 us and the cast pass after it faster,
-        // config 5 +1.6 %)
+        // dgrad and wgrad outputs take non-temporal stores: the write burst
+        // passes the caches by (config 3's GEMM pair 213 -> 210 us and the
+        // cast pass after it faster, config 5 +1.6 %); a forward product
+        // (A K-contiguous, B MN-contiguous) keeps ordinary stores, as the
+        // next kernel reads it (config 5's unfused graph +1.3 %)
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
 #pragma unroll
@@ -586,7 +588,10 @@ __device__ __forceinline__ void gemm16_block(const gemm_kargs &g, int pid, int n
                     const int row = m0 + wm * WM + i * 32 + (e >> 2) * 8 + lk * 4 + (e & 3);
                     if (row < M) {
                         float *p = Cb + (size_t)row * ldc + col;
-                        __builtin_nontemporal_store(beta ? *p + acc[i][j][e] : acc[i][j][e], p);
+                        if constexpr (!TA && TB)
+                            *p = beta ? *p + acc[i][j][e] : acc[i][j][e];
+                        else
+                            __builtin_nontemporal_store(beta ? *p + acc[i][j][e] : acc[i][j][e], p);
                     }
                 }
             }
